@@ -1,0 +1,402 @@
+#!/usr/bin/env python3
+"""Paged-KV decode benchmark on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (the configuration the north-star HBM target is
+quoted on): 64 sequences with contexts U[512, 8192] (seed 2), 12 heads x 64,
+block size 16, bf16 K/V, each block table a random shuffle over a shared
+40000-block pool.  One step is one decode step of the paged path for one
+layer over the whole batch: the batched HIP append of each sequence's new
+token (into its last slot) followed by the batched direct paged decode
+attention over the full contexts.  Inputs are resident in HBM before timing.
+
+Printed: ONE JSON line.  `value` is algorithmic bytes (attention + append) per
+step over the measured step time, in GB/s.  `roofline` is the attention alone:
+its algorithmic bytes over its average duration from HIP events recorded on
+the launch stream around every attention call of the timed region.
+`cpu_baseline` times the oracle's gather + scaled_dot_product_attention path
+(the reference's CPU path) on a bounded sample of the same workload.
+`secondary` carries the per-token end-to-end decode latency (config 1) and the
+single-layer, append/gather and long-context figures (configs 2, 3, 5).
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
+
+METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
+PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--partition-tokens", type=int, default=0, help="0 = the library's automatic choice")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
+    return p.parse_args()
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+# ---- the measured step -----------------------------------------------------------
+
+
+def config4_setup(torch, partition_tokens):
+    from moe_engine import workloads
+
+    lens = workloads.cfg4_lens()
+    w = workloads.make_workload(lens, block_size=16, num_blocks=40000, dtype=torch.bfloat16, seed=2)
+    batch, heads, dim = len(lens), 12, 64
+    gen = torch.Generator(device="cuda").manual_seed(22)
+    k_new = torch.randn(batch, heads, 1, dim, generator=gen, device="cuda").to(torch.bfloat16)
+    v_new = torch.randn(batch, heads, 1, dim, generator=gen, device="cuda").to(torch.bfloat16)
+    positions = (w.context_lens - 1).contiguous()
+    out = torch.empty(batch, heads, dim, dtype=torch.bfloat16, device="cuda")
+    return w, k_new, v_new, positions, out
+
+
+def run_config4(torch, args):
+    from moe_engine import _native, kv_ops, paged_attention, workloads
+
+    w, k_new, v_new, positions, out = config4_setup(torch, args.partition_tokens)
+    heads, dim = 12, 64
+    attn_bytes = workloads.attention_bytes(w.lens, heads, dim, 16, 2)
+    app_bytes = workloads.append_bytes(len(w.lens), heads, dim, 2)
+    part, ws_bytes = _native.decode_plan(len(w.lens), heads, dim, w.max_len, torch.bfloat16, args.partition_tokens)
+
+    def append():
+        kv_ops.append(w.k_pool, w.v_pool, 0, k_new, v_new, w.block_tables, positions=positions)
+
+    def attend():
+        paged_attention.decode_batched(
+            w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
+            out=out, partition_tokens=args.partition_tokens,
+        )
+
+    for _ in range(args.warmup):
+        append()
+        attend()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        append()
+        starts[i].record()
+        attend()
+        ends[i].record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    attn_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    attn_avg_s = sum(attn_ms) / len(attn_ms) / 1e3
+    achieved = attn_bytes / attn_avg_s / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    return {
+        "workload": w,
+        "value": (attn_bytes + app_bytes) * args.steps / elapsed / 1e9,
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "attn_bytes": attn_bytes,
+        "append_bytes": app_bytes,
+        "partition_tokens": part,
+        "workspace_bytes": ws_bytes,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "mie_paged_decode (paged_decode_kernel + paged_decode_reduce_kernel)",
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": attn_bytes,
+            "avg_duration_us": round(attn_avg_s * 1e6, 2),
+            "median_duration_us": round(statistics.median(attn_ms) * 1e3, 2),
+        },
+    }
+
+
+# ---- CPU baseline (the oracle's gather + SDPA path, on the host cores) -------------
+
+
+def cpu_baseline(torch, w, budget_s):
+    from oracle import paged_ref as ref
+    from moe_engine import workloads
+
+    threads = torch.get_num_threads()
+    k_pool, v_pool = w.k_pool[w.layer : w.layer + 1].cpu(), w.v_pool[w.layer : w.layer + 1].cpu()
+    q = w.q.cpu()
+    sample = list(range(0, len(w.lens), 8))  # every 8th sequence: 8 of 64
+    lens = [w.lens[b] for b in sample]
+    tables = [w.tables[b] for b in sample]
+    sample_bytes = workloads.attention_bytes(lens, q.shape[1], q.shape[2], w.block_size, 2)
+    ref.batched_gather_sdpa(q[sample], k_pool, v_pool, 0, tables, lens)  # warm-up
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        ref.batched_gather_sdpa(q[sample], k_pool, v_pool, 0, tables, lens)
+        passes += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed >= budget_s or passes >= 1000:
+            break
+    return {
+        "value": round(sample_bytes * passes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"sequences {sample} of config 4 ({sum(lens)} tokens, bf16), {passes} passes of "
+            f"per-sequence gather + torch scaled_dot_product_attention in {elapsed:.1f} s; "
+            f"host {os.cpu_count()} logical CPUs, torch threads {threads}"
+        ),
+        "ms_per_pass": round(elapsed / passes * 1e3, 2),
+    }
+
+
+# ---- secondary figures -------------------------------------------------------------
+
+
+def timed_us(torch, fn, iters=50, warmup=5):
+    for _ in range(warmup):
+        fn()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(iters):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters * 1e3
+
+
+def secondary_config2(torch):
+    """Single layer, batch 1, context 2048, bf16: warm (same blocks every call)
+    and cold (64 disjoint sequences rotated, 403 MB > the 256 MB MALL)."""
+    from moe_engine import paged_attention, workloads
+
+    w = workloads.make_workload([2048] * 64, block_size=16, num_blocks=64 * 128, dtype=torch.bfloat16, seed=1)
+    nbytes = workloads.attention_bytes([2048], 12, 64, 16, 2)
+    k0, v0 = w.k_pool[0], w.v_pool[0]
+    tables = [w.block_tables[b].contiguous() for b in range(64)]
+    qs = [w.q[b : b + 1] for b in range(64)]
+    warm = timed_us(torch, lambda: paged_attention.decode_layer(qs[0], k0, v0, tables[0], context_len=2048))
+    it = [0]
+
+    def cold():
+        b = it[0] % 64
+        it[0] += 1
+        paged_attention.decode_layer(qs[b], k0, v0, tables[b], context_len=2048)
+
+    cold_us = timed_us(torch, cold, iters=128)
+    return {
+        "warm_us": round(warm, 2),
+        "warm_gbs": round(nbytes / warm / 1e3, 1),
+        "cold_us": round(cold_us, 2),
+        "cold_gbs": round(nbytes / cold_us / 1e3, 1),
+        "bytes": nbytes,
+    }
+
+
+def secondary_config3(torch):
+    """12 layers, bf16, context 8192 over a 65536-block pool: per-layer append
+    (one token) and per-layer gather of the full context."""
+    from moe_engine import kv_ops, workloads
+
+    L, NB, H, BS, D, C = 12, 65536, 12, 16, 64, 8192
+    k_pool = torch.zeros(L, NB, H, BS, D, dtype=torch.bfloat16, device="cuda")
+    v_pool = torch.zeros_like(k_pool)
+    table = torch.zeros(NB, dtype=torch.int32, device="cuda")
+    nblk = -(-C // BS)
+    table[:nblk] = torch.randperm(NB, generator=torch.Generator().manual_seed(3))[:nblk].to(torch.int32).cuda()
+    new = torch.randn(1, H, 1, D, device="cuda").to(torch.bfloat16)
+    outk = torch.empty(1, H, C, D, dtype=torch.bfloat16, device="cuda")
+    outv = torch.empty_like(outk)
+    append_us = timed_us(torch, lambda: [kv_ops.append(k_pool, v_pool, l, new, new, table, position=C - 1) for l in range(L)]) / L
+    gather_us = timed_us(torch, lambda: [kv_ops.gather(k_pool, v_pool, l, table, C, outk, outv) for l in range(L)], iters=20) / L
+    gb = workloads.gather_bytes(C, H, D, 2)
+    del k_pool, v_pool
+    torch.cuda.empty_cache()
+    return {
+        "append_us_per_layer": round(append_us, 2),
+        "gather_us_per_layer": round(gather_us, 2),
+        "gather_gbs": round(gb / gather_us / 1e3, 1),
+        "gather_bytes_per_layer": gb,
+        "context": C,
+    }
+
+
+def secondary_config5(torch):
+    """Long-context split decode, bf16, block 32: batch 1 and 8 at 131072."""
+    from moe_engine import paged_attention, workloads
+
+    res = {}
+    for batch in (1, 8):
+        w = workloads.make_workload([131072] * batch, block_size=32, dtype=torch.bfloat16, seed=5, heavy_fraction=0.01)
+        nbytes = workloads.attention_bytes(w.lens, 12, 64, 32, 2)
+        us = timed_us(
+            torch,
+            lambda: paged_attention.decode_batched(w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len),
+            iters=20,
+        )
+        res[f"b{batch}_c131072_us"] = round(us, 2)
+        res[f"b{batch}_c131072_gbs"] = round(nbytes / us / 1e3, 1)
+        del w
+        torch.cuda.empty_cache()
+    return res
+
+
+def secondary_e2e(torch, rounds=3, new_tokens=64):
+    """BASELINE config 1 on the GPU: per-token greedy decode latency of the
+    contiguous, paged-gather and paged-direct systems in interleaved rounds
+    (reference benchmarks/ab_compare.py:49-144), prompt excluded."""
+    from moe_engine.model import Model, ModelConfig
+
+    torch.manual_seed(0)
+    cfg = ModelConfig(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
+                      num_experts=8, top_k=2, ffn_dim=2048)
+    model = Model(cfg).to("cuda").eval()
+    prompt = torch.randint(0, cfg.vocab_size, (1, 32), generator=torch.Generator().manual_seed(0)).cuda()
+    systems = ["contiguous", "paged-gather", "paged-direct"]
+
+    def run(system):
+        cache = model.new_cache() if system == "contiguous" else model.new_block_allocator(
+            num_blocks=64, block_size=16, attention_mode=system[6:]).new_cache()
+        steps, tokens = [], []
+        with torch.no_grad():
+            logits = model(prompt, cache)
+            nxt = logits[:, -1].argmax(-1, keepdim=True)
+            for _ in range(new_tokens):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                logits = model(nxt, cache)
+                nxt = logits[:, -1].argmax(-1, keepdim=True)
+                torch.cuda.synchronize()
+                steps.append(time.perf_counter() - t0)
+                tokens.append(int(nxt))
+        if system != "contiguous":
+            cache.free()
+        return steps, tokens
+
+    for s in systems:
+        run(s)  # warm-up
+    per = {s: [] for s in systems}
+    toks = {}
+    for r in range(rounds):
+        order = systems[r % 3 :] + systems[: r % 3]
+        for s in order:
+            steps, tokens = run(s)
+            per[s].append(steps)
+            toks[s] = tokens
+    out = {}
+    for s in systems:
+        pooled = sorted(t for steps in per[s] for t in steps)
+        out[s] = {"median_ms": round(pooled[len(pooled) // 2] * 1e3, 3),
+                  "mean_ms": round(sum(pooled) / len(pooled) * 1e3, 3)}
+    deltas = [
+        (sum(d) / len(d) - sum(c) / len(c)) * 1e3 for d, c in zip(per["paged-direct"], per["contiguous"])
+    ]
+    out["direct_minus_contiguous_mean_ms"] = round(sum(deltas) / len(deltas), 3)
+    out["tokens_identical"] = toks["paged-direct"] == toks["contiguous"] == toks["paged-gather"]
+    out["rounds"] = rounds
+    out["new_tokens"] = new_tokens
+    return out
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(
+            f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}): "
+            "the paged decode path shards by sequence, head or layer with no exchange, "
+            "so multi-GPU figures are not produced by this build",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    from moe_engine import _native
+
+    _native.lib()  # fail loudly when the HIP library is missing
+    if not torch.cuda.is_available():
+        sys.exit("bench.py needs a ROCm GPU")
+    torch.cuda.set_device(0)
+    log("config 4: building workload")
+    main_res = run_config4(torch, args)
+    log(f"config 4: {main_res['value']:.1f} GB/s, attention {main_res['roofline']['achieved']} GB/s")
+    w = main_res.pop("workload")
+    total_tokens = sum(w.lens)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        cpu = cpu_baseline(torch, w, args.cpu_seconds)
+    del w
+    torch.cuda.empty_cache()
+
+    secondary = {}
+    if not args.no_secondary:
+        for name, fn in (
+            ("config2_single_layer", secondary_config2),
+            ("config3_append_gather", secondary_config3),
+            ("config5_long_context", secondary_config5),
+            ("config1_e2e_decode", secondary_e2e),
+        ):
+            log(f"secondary {name}")
+            try:
+                secondary[name] = fn(torch)
+            except Exception as exc:  # a secondary figure never hides the main line
+                secondary[name] = {"error": f"{type(exc).__name__}: {exc}"}
+            torch.cuda.empty_cache()
+
+    line = {
+        "metric": METRIC,
+        "value": round(main_res["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(main_res["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "batched paged decode step, BASELINE config 4: batched KV append + direct paged decode attention, one layer",
+            "batch": 64,
+            "context_lens": "U[512, 8192], seed 2",
+            "total_tokens": total_tokens,
+            "num_heads": 12,
+            "head_dim": 64,
+            "block_size": 16,
+            "pool_blocks": 40000,
+            "partition_tokens": main_res["partition_tokens"],
+            "attention_bytes_per_step": main_res["attn_bytes"],
+            "append_bytes_per_step": main_res["append_bytes"],
+            "parallelism": "single GPU",
+        },
+        "roofline": main_res["roofline"],
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,168 @@
+/*
+ * mie_paged_kv.h - C ABI of the MI355X (gfx950) paged-KV decode path.
+ *
+ * One shared library, libmie_paged.so, exports these entry points.  They
+ * replace the tensor work under the reference engine's paged KV cache
+ * (maokner/moe-inference-engine):
+ *
+ *   mie_kv_append     <- PagedKVCache.write     src/moe_engine/model.py:167-184
+ *   mie_kv_gather     <- PagedKVCache.read      src/moe_engine/model.py:186-201
+ *   mie_paged_decode  <- paged_attention.decode src/moe_engine/paged_attention.py:113-154
+ *                        and _paged_decode_kernel src/moe_engine/paged_attention.py:46-110
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers unless stated otherwise.  The library
+ *     allocates nothing and never synchronises the device: every launch is
+ *     queued on `stream` (a hipStream_t; NULL is the legacy default stream).
+ *   - Strides are in ELEMENTS, 64-bit.  The innermost (head_dim) axis of every
+ *     tensor must be contiguous.
+ *   - A KV pool for ONE layer is [num_blocks, num_heads, block_size, head_dim]
+ *     with the (block_size, head_dim) tile of each (block, head) contiguous:
+ *     the element (blk, h, slot, d) lives at
+ *         blk * pool_stride_block + h * pool_stride_head + slot * head_dim + d.
+ *     Callers pass the base pointer of the layer they address
+ *     (k_pool + layer * layer_stride), as the reference does with k_pool[layer]
+ *     (paged_attention.py:121-122).
+ *   - Logical token t of a sequence lives in physical block
+ *     block_table[t / block_size] at slot t % block_size
+ *     (paged_attention.py:86-88, model.py:145-147).
+ *   - A block-table row holds block_table_stride entries (num_blocks entries
+ *     when the stride is 0, as for the per-sequence mirror); logical blocks
+ *     past the row are never read.
+ *   - Block ids outside [0, num_blocks) are never dereferenced: append skips
+ *     the row, gather leaves the output row unwritten, decode writes NaN for
+ *     the affected (sequence, head).
+ *   - Every function returns MIE_OK (0) or a non-zero MIE_ERR_* code, with a
+ *     message available from mie_last_error() on the calling thread.
+ */
+#ifndef MIE_PAGED_KV_H
+#define MIE_PAGED_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types of pools, new K/V rows, queries and outputs. */
+enum mie_dtype {
+  MIE_DTYPE_F32 = 0,
+  MIE_DTYPE_BF16 = 1,
+  MIE_DTYPE_F16 = 2, /* append / gather only */
+  MIE_DTYPE_F64 = 3  /* append / gather only */
+};
+
+enum mie_status {
+  MIE_OK = 0,
+  MIE_ERR_INVALID = 1,     /* bad argument: shape, stride, pointer, size */
+  MIE_ERR_UNSUPPORTED = 2, /* valid but not built: dtype / head_dim combination */
+  MIE_ERR_WORKSPACE = 3,   /* split-context workspace missing or too small */
+  MIE_ERR_LAUNCH = 4       /* the HIP runtime rejected a launch */
+};
+
+/* Library ABI version (MIE_ABI_VERSION below). */
+int32_t mie_abi_version(void);
+#define MIE_ABI_VERSION 1
+
+/* Message for the last non-zero status returned on this thread ("" if none). */
+const char* mie_last_error(void);
+
+/*
+ * KV append: scatter new K/V rows into the pool through block tables.
+ * Replaces PagedKVCache.write (model.py:167-184): the decode store
+ * pool[l, bt[p // BS], :, p % BS] = k[0, :, 0] (model.py:173-178) for seq_len
+ * 1 and the prefill scatter pool[l, blocks, :, slots] = k[0].transpose(0, 1)
+ * (model.py:179-184) for seq_len > 1, for `batch` sequences in one launch:
+ *
+ *   for b < batch, s < seq_len, h < num_heads, d < head_dim, p = pos(b) + s:
+ *     pool[bt_b[p / block_size], h, p % block_size, d] = new[b, h, s, d]
+ *
+ * where pos(b) = positions[b] if `positions` is non-NULL (device int32[batch])
+ * else `position`, and bt_b = block_tables + b * block_table_stride.  The K and
+ * V sources share strides new_stride_{b,h,s}.  K and V are written by the same
+ * launch; the copy is bit-exact for every dtype.  Blocks must already be
+ * reserved in the tables (the host allocator does that, model.py:125-143).
+ */
+int32_t mie_kv_append(void* k_pool, void* v_pool, int64_t pool_stride_block,
+                      int64_t pool_stride_head, int32_t num_blocks,
+                      const void* k_new, const void* v_new, int64_t new_stride_b,
+                      int64_t new_stride_h, int64_t new_stride_s,
+                      const int32_t* block_tables, int64_t block_table_stride,
+                      const int32_t* positions, int32_t position, int32_t batch,
+                      int32_t seq_len, int32_t num_heads, int32_t head_dim,
+                      int32_t block_size, int32_t dtype, void* stream);
+
+/*
+ * KV gather: copy one sequence's first `length` tokens of K and V out of the
+ * pool into contiguous-by-token outputs.  Replaces PagedKVCache.read
+ * (model.py:186-201), which returns pool[l, bt[:nb]].transpose(0, 1)
+ * .reshape(H, -1, D)[:, :length]:
+ *
+ *   out[h * out_stride_h + t * out_stride_t + d] =
+ *       pool[bt[t / block_size], h, t % block_size, d]   for t < length
+ *
+ * Bit-exact for every dtype.  K and V outputs share strides.
+ */
+int32_t mie_kv_gather(const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                      int64_t pool_stride_head, int32_t num_blocks,
+                      const int32_t* block_table, int32_t length, void* k_out,
+                      void* v_out, int64_t out_stride_h, int64_t out_stride_t,
+                      int32_t num_heads, int32_t head_dim, int32_t block_size,
+                      int32_t dtype, void* stream);
+
+/*
+ * Direct paged decode attention for `batch` sequences with one query token
+ * each.  Replaces paged_attention.decode (paged_attention.py:113-154) and
+ * _paged_decode_kernel (paged_attention.py:46-110), which computes for one
+ * sequence, per head,  out = softmax(q . K^T * scale) . V  over logical tokens
+ * [0, ctx_len) read in place through the block table:
+ *
+ *   out[b, h, :] = sum_t softmax_t(scale * <q[b, h, :], K_b[t, h, :]>) V_b[t, h, :]
+ *
+ * with ctx_len(b) = min(ctx_lens[b], max_ctx_len) if `ctx_lens` is non-NULL
+ * (device int32[batch]) else `ctx_len` for every sequence; ctx_len(b) == 0
+ * writes zeros (what scaled_dot_product_attention returns for no keys).
+ * q, K and V share `dtype` (F32 or BF16); `out_dtype` is F32 or `dtype`.
+ * Accumulation is fp32 throughout.
+ *
+ * Split context: the tokens of each sequence are cut into partitions of
+ * `partition_tokens` tokens (0 = choose automatically; otherwise a power of two
+ * that is a multiple of the kernel tile, see mie_paged_decode_plan).  When a
+ * sequence needs more than one partition, per-partition (max, sum, acc[D])
+ * partials go to `workspace` and a second launch merges them (log-sum-exp);
+ * a sequence with one partition is written by the first launch directly.
+ * `workspace` must hold mie_paged_decode_plan()'s workspace_bytes; it may be
+ * NULL when that is 0.  Nothing in the workspace needs clearing.
+ */
+int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                         const void* k_pool, const void* v_pool,
+                         int64_t pool_stride_block, int64_t pool_stride_head,
+                         int32_t num_blocks, const int32_t* block_tables,
+                         int64_t block_table_stride, const int32_t* ctx_lens,
+                         int32_t ctx_len, int32_t max_ctx_len, int32_t batch,
+                         int32_t num_heads, int32_t head_dim, int32_t block_size,
+                         float scale, void* out, int64_t out_stride_b,
+                         int64_t out_stride_h, int32_t out_dtype, void* workspace,
+                         int64_t workspace_bytes, int32_t partition_tokens,
+                         int32_t dtype, void* stream);
+
+/*
+ * Host-only planning query for mie_paged_decode (no device work).  Given the
+ * launch shape it returns the partition size the decode will use
+ * (`partition_tokens` = 0 asks for the automatic choice) and the workspace
+ * bytes it needs (0 when every sequence fits one partition).
+ */
+int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32_t head_dim,
+                              int32_t max_ctx_len, int32_t dtype,
+                              int32_t partition_tokens,
+                              int32_t* partition_tokens_out,
+                              int64_t* workspace_bytes_out);
+
+/* 1 if mie_paged_decode is built for (head_dim, dtype), else 0. */
+int32_t mie_paged_decode_supported(int32_t head_dim, int32_t dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIE_PAGED_KV_H */

@@ -1,0 +1,106 @@
+// Shared helpers for the gfx950 paged-KV kernels: error state, element sizes,
+// fast division by a runtime block size, bf16 <-> f32 conversion and the
+// 64-lane wavefront reductions the decode kernels use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mie_paged_kv.h"
+
+namespace mie {
+
+// Records `msg` as this thread's last error and returns `code`.
+int32_t fail(int32_t code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+inline int elt_size(int32_t dtype) {
+  switch (dtype) {
+    case MIE_DTYPE_F32: return 4;
+    case MIE_DTYPE_BF16: return 2;
+    case MIE_DTYPE_F16: return 2;
+    case MIE_DTYPE_F64: return 8;
+    default: return 0;
+  }
+}
+
+// Maps a launch failure to MIE_ERR_LAUNCH with the runtime's message.
+int32_t check_launch(const char* what);
+
+// Unsigned division by a runtime divisor d >= 1 for numerators n < 2^31:
+//   q = (umulhi(n, magic) + n) >> shift,  shift = ceil(log2 d),
+//   magic = floor(2^32 * (2^shift - d) / d) + 1
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, round-up variant).  n + umulhi(n, magic) < 2^32
+// holds because n < 2^31 and umulhi(n, magic) <= n.
+struct FastDiv {
+  uint32_t d;
+  uint32_t magic;
+  uint32_t shift;
+
+  static FastDiv make(uint32_t divisor) {
+    FastDiv f;
+    f.d = divisor;
+    uint32_t s = 0;
+    while ((1ull << s) < divisor) ++s;
+    f.shift = s;
+    f.magic = static_cast<uint32_t>(((1ull << 32) * ((1ull << s) - divisor)) / divisor + 1);
+    return f;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    return (__umulhi(n, magic) + n) >> shift;
+  }
+};
+
+// ---- bf16 <-> f32 ---------------------------------------------------------
+// A bf16 value is the high half of the f32 with the same sign/exponent, so the
+// widening is a shift; narrowing rounds to nearest even (NaN kept quiet).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+// ---- wavefront reductions -------------------------------------------------
+// DPP controls (CDNA3/4 ISA): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141 (lane i <-> 7-i within 8), row_mirror = 0x140
+// (i <-> 15-i within 16).  Applied in this order each stage pairs lanes whose
+// partial sums cover disjoint halves, so after log2(N) stages every lane of an
+// aligned N-lane group holds the group total.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over aligned groups of N lanes (N a power of two <= 64); all 64 lanes of
+// the wave must be active.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp<0xB1>(x);
+  if constexpr (N >= 4) x += dpp<0x4E>(x);
+  if constexpr (N >= 8) x += dpp<0x141>(x);
+  if constexpr (N >= 16) x += dpp<0x140>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace mie

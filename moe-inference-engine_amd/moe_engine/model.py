@@ -1,0 +1,436 @@
+"""miniMoE inference host with contiguous and paged KV caches.
+
+Drop-in for the reference engine's src/moe_engine/model.py: the classes,
+constructor arguments, attributes, state-dict names and error messages are the
+reference's, so callers and checkpoints move over unchanged.  What differs is
+underneath the paged cache on a ROCm device:
+
+  * PagedKVCache.write  -> one mie_kv_append launch (K and V, decode or prefill)
+  * PagedKVCache.read   -> one mie_kv_gather launch (K and V)
+  * direct decode       -> mie_paged_decode (moe_engine.paged_attention)
+
+A paged pool on a ROCm device requires the HIP library and raises at
+construction without it.  Pools on the CPU use PyTorch indexing, which is the
+reference's own CPU behaviour for this device.
+
+Random initialisation consumes the RNG in the reference's module order
+(token and positional embeddings, output projection, then per block:
+attention out_proj, in_proj xavier, the experts' two linears each, router), so
+a seeded model has the reference's weights.
+"""
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from moe_engine import _native, kv_ops, paged_attention
+
+EOS_TOKEN_ID = 50256
+ATTENTION_MODES = ("auto", "direct", "gather")
+MOE_MODES = ("auto", "direct", "reference")
+
+
+@dataclass
+class ModelConfig:
+    """Reference fields (model.py:18-27) plus `ffn_dim`, the expert hidden size.
+
+    ffn_dim None keeps the reference's hard-coded 4 * hidden_dim (model.py:489).
+    """
+
+    max_seq_length: int = 1024
+    vocab_size: int = 50304
+    num_layers: int = 6
+    hidden_dim: int = 768
+    moe_multiplier: float = 0.01  # checkpoint compatibility only
+    num_experts: int = 8
+    top_k: int = 2
+    num_heads: int = 8
+    ffn_dim: Optional[int] = None
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_dim // self.num_heads
+
+    @property
+    def expert_hidden_dim(self) -> int:
+        return 4 * self.hidden_dim if self.ffn_dim is None else self.ffn_dim
+
+
+class KVCache:
+    """Contiguous K/V storage [layer, batch, head, max_seq, head_dim] (model.py:30-58).
+
+    The comparator for the paged path: write is a slice store, read a view.
+    """
+
+    def __init__(self, config: ModelConfig, batch_size: int, device, dtype=torch.float32):
+        shape = (config.num_layers, batch_size, config.num_heads, config.max_seq_length, config.head_dim)
+        self.k = torch.zeros(shape, device=device, dtype=dtype)
+        self.v = torch.zeros(shape, device=device, dtype=dtype)
+        self.position = 0
+
+    def write(self, layer_idx, position, k, v):
+        end = position + k.shape[2]
+        self.k[layer_idx, :, :, position:end] = k
+        self.v[layer_idx, :, :, position:end] = v
+
+    def read(self, layer_idx, length):
+        return self.k[layer_idx, :, :, :length], self.v[layer_idx, :, :, :length]
+
+
+class BlockAllocator:
+    """Shared block pools and a LIFO free list (model.py:61-105).
+
+    attention_mode chooses how caches from this pool attend while decoding:
+      "gather" - rebuild contiguous K/V, then PyTorch attention (the oracle),
+      "direct" - require the HIP kernel that reads blocks in place,
+      "auto"   - direct when supported, else gather.
+    """
+
+    def __init__(
+        self,
+        config: ModelConfig,
+        num_blocks: int,
+        block_size: int,
+        device,
+        dtype=torch.float32,
+        attention_mode: str = "auto",
+    ):
+        if attention_mode not in ATTENTION_MODES:
+            raise ValueError(f"unknown attention_mode {attention_mode!r}")
+        self.attention_mode = attention_mode
+        self.num_blocks = num_blocks
+        self.block_size = block_size
+        self.num_heads = config.num_heads
+        self.head_dim = config.head_dim
+        shape = (config.num_layers, num_blocks, config.num_heads, block_size, self.head_dim)
+        self.k_pool = torch.zeros(shape, device=device, dtype=dtype)
+        self.v_pool = torch.zeros(shape, device=device, dtype=dtype)
+        # On a ROCm device every paged tensor operation is a HIP kernel; there
+        # is no PyTorch substitute, so a missing library fails here, loudly.
+        self.on_device = _native.is_rocm_device(self.k_pool)
+        if self.on_device:
+            _native.lib()
+        self.free_blocks = list(range(num_blocks))
+
+    def allocate(self) -> int:
+        if not self.free_blocks:
+            raise RuntimeError("no free KV cache blocks left")
+        return self.free_blocks.pop()
+
+    def free(self, block_ids: list) -> None:
+        self.free_blocks.extend(block_ids)
+
+    def new_cache(self) -> "PagedKVCache":
+        return PagedKVCache(self)
+
+
+class PagedKVCache:
+    """One sequence's block table over a shared allocator (model.py:108-208)."""
+
+    def __init__(self, allocator: BlockAllocator):
+        self.allocator = allocator
+        self.attention_mode = allocator.attention_mode
+        self.block_table: list = []
+        self.position = 0
+        # Device mirror of block_table for the kernels.  Only the first
+        # len(block_table) entries are meaningful; new entries are appended as
+        # blocks are reserved (one small host-to-device copy per block_size
+        # tokens), never rebuilt.
+        self.block_table_device = torch.zeros(
+            allocator.num_blocks, dtype=torch.int32, device=allocator.k_pool.device
+        )
+        self._write_index_key = None  # (position, seq_len) of cached CPU indices
+
+    def _reserve(self, num_tokens: int) -> None:
+        """Hold enough blocks for `num_tokens`, all or nothing (model.py:125-143)."""
+        needed = -(-num_tokens // self.allocator.block_size)
+        taken = []
+        try:
+            while len(self.block_table) + len(taken) < needed:
+                taken.append(self.allocator.allocate())
+        except RuntimeError:
+            self.allocator.free(taken)
+            raise
+        if taken:
+            start = len(self.block_table)
+            self.block_table.extend(taken)
+            self.block_table_device[start : start + len(taken)] = torch.tensor(
+                taken, dtype=torch.int32, device=self.block_table_device.device
+            )
+
+    def _block_for(self, token_pos: int):
+        size = self.allocator.block_size
+        return self.block_table[token_pos // size], token_pos % size
+
+    def _write_indices(self, position, seq_len):
+        """(physical block, slot) index tensors for a multi-token CPU write,
+        built once per step and reused by every layer (model.py:149-165)."""
+        if self._write_index_key != (position, seq_len):
+            size = self.allocator.block_size
+            pos = torch.arange(position, position + seq_len, device=self.block_table_device.device)
+            self._write_index = (self.block_table_device[pos // size].long(), pos % size)
+            self._write_index_key = (position, seq_len)
+        return self._write_index
+
+    def write(self, layer_idx, position, k, v):
+        """Append k, v [1, H, S, D] at logical positions position..position+S-1."""
+        if k.shape[0] != 1:
+            raise ValueError("PagedKVCache holds one sequence; use batch size 1")
+        seq_len = k.shape[2]
+        self._reserve(position + seq_len)
+        alloc = self.allocator
+        if alloc.on_device:
+            kv_ops.append(alloc.k_pool, alloc.v_pool, layer_idx, k, v, self.block_table_device, position=position)
+            return
+        if seq_len == 1:
+            block_id, slot = self._block_for(position)
+            alloc.k_pool[layer_idx, block_id, :, slot] = k[0, :, 0]
+            alloc.v_pool[layer_idx, block_id, :, slot] = v[0, :, 0]
+            return
+        blocks, slots = self._write_indices(position, seq_len)
+        alloc.k_pool[layer_idx, blocks, :, slots] = k[0].transpose(0, 1)
+        alloc.v_pool[layer_idx, blocks, :, slots] = v[0].transpose(0, 1)
+
+    def read(self, layer_idx, length):
+        """Contiguous K, V [1, H, length, D] of logical positions 0..length-1."""
+        alloc = self.allocator
+        if alloc.on_device:
+            return kv_ops.gather(alloc.k_pool, alloc.v_pool, layer_idx, self.block_table_device, length)
+        ids = self.block_table[: -(-length // alloc.block_size)]
+
+        def rebuild(pool):
+            tiles = pool[layer_idx, ids]  # [nb, H, BS, D]
+            return tiles.transpose(0, 1).reshape(alloc.num_heads, -1, alloc.head_dim)[:, :length].unsqueeze(0)
+
+        return rebuild(alloc.k_pool), rebuild(alloc.v_pool)
+
+    def free(self):
+        """Return every block and reset; stale mirror entries are never read."""
+        self.allocator.free(self.block_table)
+        self.block_table = []
+        self.position = 0
+        self._write_index_key = None
+
+
+class CachedAttention(nn.Module):
+    """Causal self-attention over an external cache (model.py:211-269)."""
+
+    def __init__(self, dim: int, num_heads: int):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.in_proj_weight = nn.Parameter(torch.empty(3 * dim, dim))
+        self.in_proj_bias = nn.Parameter(torch.empty(3 * dim))
+        self.out_proj = nn.Linear(dim, dim)
+        nn.init.xavier_uniform_(self.in_proj_weight)
+        nn.init.zeros_(self.in_proj_bias)
+
+    def forward(self, x, cache, layer_idx, position: int):
+        batch, seq_len, dim = x.shape
+        qkv = F.linear(x, self.in_proj_weight, self.in_proj_bias)
+        # [batch, seq, 3*dim] -> three [batch, head, seq, head_dim] views
+        q, k, v = (
+            t.view(batch, seq_len, self.num_heads, self.head_dim).transpose(1, 2) for t in qkv.chunk(3, dim=-1)
+        )
+
+        mode = getattr(cache, "attention_mode", "gather")
+        use_kernel = mode != "gather" and paged_attention.is_supported(x, self.head_dim)
+        if mode == "direct" and not use_kernel:
+            # Raised before the write below reserves blocks, so a rejected
+            # forward leaves the cache untouched.
+            raise RuntimeError(
+                "attention_mode='direct' needs a ROCm device, the HIP paged-KV library, "
+                "float32 or bfloat16 and a built head_dim; use 'auto' for automatic "
+                "fallback or 'gather' for the oracle path"
+            )
+
+        cache.write(layer_idx, position, k, v)
+        assert position == 0 or seq_len == 1, "prefill must start at position 0"
+
+        if mode != "gather" and position == 0:
+            # At position 0 the whole history is the K/V just projected.
+            out = F.scaled_dot_product_attention(q, k, v, is_causal=seq_len > 1)
+        elif use_kernel:
+            out = paged_attention.decode(q, cache, layer_idx, context_len=position + 1)
+        else:
+            keys, values = cache.read(layer_idx, position + seq_len)
+            out = F.scaled_dot_product_attention(q, keys, values, is_causal=seq_len > 1)
+
+        out = out.transpose(1, 2).reshape(batch, seq_len, dim)
+        return self.out_proj(out)
+
+
+class Expert(nn.Module):
+    def __init__(self, dim, hidden_dim):
+        super().__init__()
+        self.net = nn.Sequential(nn.Linear(dim, hidden_dim), nn.GELU(), nn.Linear(hidden_dim, dim))
+
+    def forward(self, x):
+        return self.net(x)
+
+
+class MoEFeedForward(nn.Module):
+    """Top-k mixture of experts, the reference's PyTorch path (model.py:443-461).
+
+    The reference's fused Triton MoE decode ("direct") is outside this build's
+    paged-KV scope: mode 'direct' is accepted for interface compatibility and
+    rejected by the decode preflight before any cache mutation, as the
+    reference does when its kernel cannot run (model.py:408-432).
+    """
+
+    def __init__(self, dim, hidden_dim, num_experts, top_k, mode="auto"):
+        super().__init__()
+        if mode not in MOE_MODES:
+            raise ValueError(f"unknown MoE mode {mode!r}")
+        self.mode = mode
+        self.dim = dim
+        self.hidden_dim = hidden_dim
+        self.top_k = top_k
+        self.num_experts = num_experts
+        self.experts = nn.ModuleList(Expert(dim, hidden_dim) for _ in range(num_experts))
+        self.router = nn.Linear(dim, num_experts, bias=False)
+
+    def set_mode(self, mode: str) -> None:
+        if mode not in MOE_MODES:
+            raise ValueError(f"unknown MoE mode {mode!r}")
+        self.mode = mode
+
+    @staticmethod
+    def _raise_direct_unsupported() -> None:
+        raise RuntimeError(
+            "MoE mode 'direct' needs a fused MoE decode kernel, which this build does not "
+            "provide; use 'auto' or 'reference' for the PyTorch path"
+        )
+
+    def preflight_direct_decode(self, *, batch_size: int) -> None:
+        if self.mode == "direct":
+            self._raise_direct_unsupported()
+
+    def uses_direct(self, x: torch.Tensor, *, decode: bool) -> bool:
+        if decode and self.mode == "direct":
+            self._raise_direct_unsupported()
+        return False
+
+    def _forward_reference(self, x: torch.Tensor) -> torch.Tensor:
+        batch, seq_len, dim = x.shape
+        flat = x.reshape(-1, dim)
+        with torch.autocast(device_type=x.device.type, enabled=False):
+            logits = F.linear(flat.float(), self.router.weight.float())
+            top_logits, top_ids = torch.topk(logits, k=self.top_k, dim=-1)
+            top_weights = F.softmax(top_logits, dim=-1)
+        out = torch.zeros_like(flat)
+        for expert_id, expert in enumerate(self.experts):
+            rows, slot = torch.where(top_ids == expert_id)
+            if rows.numel() == 0:
+                continue
+            weight = top_weights[rows, slot].unsqueeze(-1).to(flat.dtype)
+            out.index_add_(0, rows, weight * expert(flat[rows]))
+        return out.reshape(batch, seq_len, dim)
+
+    def forward(self, x, *, decode=False):
+        self.uses_direct(x, decode=decode)
+        return self._forward_reference(x)
+
+
+class TransformerMoEBlock(nn.Module):
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.attention = CachedAttention(config.hidden_dim, config.num_heads)
+        self.moe = MoEFeedForward(config.hidden_dim, config.expert_hidden_dim, config.num_experts, config.top_k)
+        self.attn_norm = nn.LayerNorm(config.hidden_dim)
+        self.moe_norm = nn.LayerNorm(config.hidden_dim)
+
+    def forward(self, x, cache, layer_idx, position):
+        x = x + self.attention(self.attn_norm(x), cache, layer_idx, position)
+        normed = self.moe_norm(x)
+        return x + self.moe(normed, decode=position > 0 and normed.shape[1] == 1)
+
+
+class Model(nn.Module):
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.config = config
+        self.max_seq_length = config.max_seq_length
+        self.token_embedding = nn.Embedding(config.vocab_size, config.hidden_dim)
+        self.positional_embedding = nn.Embedding(config.max_seq_length, config.hidden_dim)
+        self.output_projection = nn.Linear(config.hidden_dim, config.vocab_size)
+        self.MoEBlocks = nn.ModuleList(TransformerMoEBlock(config) for _ in range(config.num_layers))
+        self.final_norm = nn.LayerNorm(config.hidden_dim)
+        self.output_projection.weight = self.token_embedding.weight  # tied
+
+    def new_cache(self, batch_size: int = 1) -> KVCache:
+        weight = self.token_embedding.weight
+        return KVCache(self.config, batch_size, weight.device, weight.dtype)
+
+    def set_moe_mode(self, mode: str) -> "Model":
+        for block in self.MoEBlocks:
+            block.moe.set_mode(mode)
+        return self
+
+    def new_block_allocator(self, num_blocks: int, block_size: int = 16, attention_mode: str = "auto") -> BlockAllocator:
+        """A block pool on the model's device and dtype (model.py:529-541)."""
+        weight = self.token_embedding.weight
+        return BlockAllocator(self.config, num_blocks, block_size, weight.device, weight.dtype, attention_mode)
+
+    def forward(self, token_ids, cache):
+        batch, seq_len = token_ids.shape
+        position = cache.position
+        assert position + seq_len <= self.max_seq_length, "KV cache is full"
+        # A forced-direct MoE must fail before layer 0 writes K/V or reserves a block.
+        if position > 0 and seq_len == 1:
+            for block in self.MoEBlocks:
+                block.moe.preflight_direct_decode(batch_size=batch)
+
+        pos = torch.arange(position, position + seq_len, device=token_ids.device)
+        x = self.token_embedding(token_ids) + self.positional_embedding(pos)
+        for i, block in enumerate(self.MoEBlocks):
+            x = block(x, cache, i, position)
+        cache.position += seq_len
+        return self.output_projection(self.final_norm(x))
+
+    @torch.no_grad()
+    def generate(self, token_ids, max_new_tokens, temperature=1.0, top_k=None, cache=None):
+        """Generate one sequence; the caller owns a supplied cache (model.py:567-621)."""
+        if not math.isfinite(temperature) or temperature < 0:
+            raise ValueError("temperature must be a finite non-negative number")
+        if top_k is not None and top_k <= 0:
+            raise ValueError("top_k must be positive")
+        if max_new_tokens < 1:
+            raise ValueError("max_new_tokens must be at least 1")
+        if token_ids.dim() == 1:
+            token_ids = token_ids.unsqueeze(0)
+        token_ids = token_ids.to(self.token_embedding.weight.device).long()
+        if token_ids.shape[0] != 1:
+            raise ValueError("generate() handles one sequence; use batch size 1")
+        if token_ids.shape[1] == 0:
+            raise ValueError("prompt must contain at least one token")
+        if token_ids.shape[1] > self.max_seq_length:
+            raise ValueError(f"prompt is {token_ids.shape[1]} tokens; max_seq_length is {self.max_seq_length}")
+        if cache is None:
+            cache = self.new_cache(batch_size=1)
+        if cache.position != 0:
+            raise ValueError("generate() needs a fresh cache")
+
+        out = token_ids
+        step_input = token_ids
+        for _ in range(max_new_tokens):
+            logits = self(step_input, cache)[:, -1, :]
+            if temperature == 0:
+                next_token = torch.argmax(logits, dim=-1, keepdim=True)
+            else:
+                logits = logits / temperature
+                if top_k is not None:
+                    kth = torch.topk(logits, min(top_k, logits.size(-1))).values[:, [-1]]
+                    logits[logits < kth] = -float("inf")
+                next_token = torch.multinomial(F.softmax(logits, dim=-1), num_samples=1)
+            if next_token == EOS_TOKEN_ID:
+                return out
+            out = torch.cat((out, next_token), dim=1)
+            step_input = next_token
+            if cache.position >= self.max_seq_length:
+                break  # the sampled token has not entered the cache
+        return out

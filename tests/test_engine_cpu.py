@@ -1,0 +1,285 @@
+"""Host-side engine semantics on the CPU (no GPU needed).
+
+Mirrors the reference's CPU-runnable tests of the paged path
+(tests/test_parity.py, tests/test_paged_attention.py:188-282,
+tests/test_fused_moe.py:167-197): allocator reclaim and rollback, batch
+rejection, dtype following, generate() validation, the prefill fast path,
+fail-before-mutate for a forced 'direct' that cannot run, and the device
+mirror of the block table.  The product's CPU paged cache is also compared
+with the oracle's closed forms.
+"""
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from moe_engine import paged_attention
+from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig, PagedKVCache
+from oracle import paged_ref as ref
+
+TINY = dict(max_seq_length=32, vocab_size=96, num_layers=2, hidden_dim=32, num_experts=4, top_k=2)
+TINY128 = dict(TINY, max_seq_length=128)
+
+
+def make_engine(**overrides):
+    torch.manual_seed(0)
+    return Model(ModelConfig(**dict(TINY, **overrides))).eval()
+
+
+def stepwise(engine, ids, cache, prefill):
+    with torch.no_grad():
+        steps = [engine(ids[:, :prefill], cache)[:, -1]]
+        for t in range(prefill, ids.shape[1]):
+            steps.append(engine(ids[:, t : t + 1], cache)[:, -1])
+    return torch.stack(steps, dim=1)
+
+
+def test_cached_decode_matches_full_forward():
+    engine = make_engine()
+    ids = torch.randint(0, TINY["vocab_size"], (1, 16))
+    with torch.no_grad():
+        full = engine(ids, engine.new_cache())
+    torch.testing.assert_close(stepwise(engine, ids, engine.new_cache(), 4), full[:, 3:], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("mode", ["gather", "auto"])
+def test_paged_decode_matches_full_forward(mode):
+    engine = make_engine()
+    ids = torch.randint(0, TINY["vocab_size"], (1, 16))
+    with torch.no_grad():
+        full = engine(ids, engine.new_cache())
+    cache = engine.new_block_allocator(num_blocks=8, block_size=4, attention_mode=mode).new_cache()
+    torch.testing.assert_close(stepwise(engine, ids, cache, 4), full[:, 3:], atol=1e-4, rtol=1e-4)
+
+
+def test_paged_cache_shares_pool_without_leaking():
+    engine = make_engine()
+    ids_a = torch.randint(0, TINY["vocab_size"], (1, 16))
+    ids_b = torch.randint(0, TINY["vocab_size"], (1, 16))
+    allocator = engine.new_block_allocator(num_blocks=8, block_size=4)
+    cache_a, cache_b = allocator.new_cache(), allocator.new_cache()
+    with torch.no_grad():
+        full_a = engine(ids_a, engine.new_cache())
+        full_b = engine(ids_b, engine.new_cache())
+        engine(ids_a[:, :4], cache_a)
+        engine(ids_b[:, :4], cache_b)
+        for t in range(4, 16):  # interleaved, so the two tables alternate in the pool
+            logits_a = engine(ids_a[:, t : t + 1], cache_a)
+            logits_b = engine(ids_b[:, t : t + 1], cache_b)
+    assert not set(cache_a.block_table) & set(cache_b.block_table)
+    torch.testing.assert_close(logits_a[:, -1], full_a[:, -1], atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(logits_b[:, -1], full_b[:, -1], atol=1e-4, rtol=1e-4)
+
+
+def test_block_allocator_reclaims_freed_blocks():
+    engine = make_engine()
+    ids = torch.randint(0, TINY["vocab_size"], (1, 8))
+    allocator = engine.new_block_allocator(num_blocks=2, block_size=4)
+    cache_a, cache_b = allocator.new_cache(), allocator.new_cache()
+    with torch.no_grad():
+        engine(ids, cache_a)
+        with pytest.raises(RuntimeError, match="no free KV cache blocks left"):
+            engine(ids[:, :1], cache_b)
+        cache_a.free()
+        engine(ids[:, :1], cache_b)
+
+
+def test_failed_allocation_rolls_back():
+    engine = make_engine()
+    allocator = engine.new_block_allocator(num_blocks=1, block_size=4)
+    cache = allocator.new_cache()
+    ids = torch.randint(0, TINY["vocab_size"], (1, 8))  # needs two blocks
+    with torch.no_grad():
+        with pytest.raises(RuntimeError, match="no free KV cache blocks left"):
+            engine(ids, cache)
+        assert cache.block_table == [] and cache.position == 0 and allocator.free_blocks == [0]
+        engine(ids[:, :4], cache)  # still usable
+
+
+def test_allocation_order_matches_oracle_lifo():
+    engine = make_engine()
+    allocator = engine.new_block_allocator(num_blocks=9, block_size=4)
+    random.Random(5).shuffle(allocator.free_blocks)
+    oracle_alloc = ref.LifoAllocator(9)
+    oracle_alloc.free_blocks = list(allocator.free_blocks)
+    cache = allocator.new_cache()
+    table = []
+    with torch.no_grad():
+        engine(torch.randint(0, 96, (1, 7)), cache)
+        ref.reserve(table, oracle_alloc, 7, 4)
+        for n in range(8, 20):
+            engine(torch.randint(0, 96, (1, 1)), cache)
+            ref.reserve(table, oracle_alloc, n, 4)
+    assert cache.block_table == table
+    assert allocator.free_blocks == oracle_alloc.free_blocks
+    assert cache.block_table_device[: len(table)].tolist() == table
+
+
+def test_paged_cache_rejects_batches():
+    engine = make_engine()
+    allocator = engine.new_block_allocator(num_blocks=8, block_size=4)
+    with torch.no_grad(), pytest.raises(ValueError, match="batch size 1"):
+        engine(torch.randint(0, 96, (2, 4)), allocator.new_cache())
+
+
+def test_generate_stops_at_context_limit():
+    engine = make_engine()
+    prompt = torch.randint(0, TINY["vocab_size"], (TINY["max_seq_length"] - 2,))
+    out = engine.generate(prompt, max_new_tokens=10, temperature=0)
+    assert out.shape[1] == TINY["max_seq_length"] + 1  # the last token never enters the cache
+
+
+def test_generate_validates_prompt_and_cache():
+    engine = make_engine()
+    with pytest.raises(ValueError, match="max_seq_length"):
+        engine.generate(torch.randint(0, 96, (TINY["max_seq_length"] + 1,)), max_new_tokens=1)
+    allocator = engine.new_block_allocator(num_blocks=8, block_size=4)
+    used = allocator.new_cache()
+    prompt = torch.randint(0, 96, (1, 4))
+    with torch.no_grad():
+        engine(prompt, used)
+    before = list(used.block_table)
+    with pytest.raises(ValueError, match="fresh cache"):
+        engine.generate(prompt, max_new_tokens=1, cache=used)
+    assert used.block_table == before
+
+
+def test_generate_validates_arguments():
+    engine = make_engine()
+    prompt = torch.randint(0, 96, (4,))
+    for kwargs in (dict(temperature=-1), dict(temperature=float("nan")), dict(top_k=0), dict(max_new_tokens=0)):
+        args = {"max_new_tokens": 4, **kwargs}
+        with pytest.raises(ValueError):
+            engine.generate(prompt, **args)
+
+
+def test_paged_cache_follows_model_dtype():
+    engine = make_engine().double()
+    ids = torch.randint(0, 96, (1, 8))
+    with torch.no_grad():
+        full = engine(ids, engine.new_cache())
+        cache = engine.new_block_allocator(num_blocks=2, block_size=4).new_cache()
+        engine(ids[:, :4], cache)
+        step = engine(ids[:, 4:5], cache)
+    assert step.dtype == torch.float64 and cache.allocator.k_pool.dtype == torch.float64
+    torch.testing.assert_close(step[:, -1], full[:, 4], atol=1e-4, rtol=1e-4)
+
+
+def test_auto_mode_matches_gather_mode_on_cpu():
+    engine = make_engine(max_seq_length=128)
+    ids = torch.randint(0, 96, (1, 16))
+    logits = {}
+    for mode in ("gather", "auto"):
+        cache = engine.new_block_allocator(num_blocks=16, block_size=4, attention_mode=mode).new_cache()
+        logits[mode] = stepwise(engine, ids, cache, 8)
+    torch.testing.assert_close(logits["auto"], logits["gather"], atol=1e-5, rtol=1e-5)
+
+
+def test_prefill_fast_path_matches_contiguous():
+    engine = make_engine(max_seq_length=128)
+    ids = torch.randint(0, 96, (1, 19))  # partial last block
+    with torch.no_grad():
+        contiguous = engine(ids, engine.new_cache())
+        paged = engine(ids, engine.new_block_allocator(num_blocks=16, block_size=4).new_cache())
+    torch.testing.assert_close(paged, contiguous, atol=1e-5, rtol=1e-5)
+
+
+def assert_cache_untouched(cache, allocator, num_blocks):
+    assert cache.position == 0
+    assert cache.block_table == []
+    assert sorted(allocator.free_blocks) == list(range(num_blocks))
+    assert (cache.block_table_device == 0).all()
+    assert cache._write_index_key is None
+
+
+def test_direct_mode_raises_without_rocm_before_mutating():
+    engine = make_engine()
+    allocator = engine.new_block_allocator(num_blocks=8, block_size=4, attention_mode="direct")
+    cache = allocator.new_cache()
+    with torch.no_grad(), pytest.raises(RuntimeError, match="direct"):
+        engine(torch.randint(0, 96, (1, 5)), cache)
+    assert_cache_untouched(cache, allocator, 8)
+
+
+def test_invalid_attention_mode_rejected():
+    with pytest.raises(ValueError, match="attention_mode"):
+        make_engine().new_block_allocator(num_blocks=4, block_size=4, attention_mode="turbo")
+
+
+def test_device_block_table_mirrors_python_table():
+    engine = make_engine()
+    allocator = engine.new_block_allocator(num_blocks=16, block_size=4)
+    random.Random(1).shuffle(allocator.free_blocks)
+    cache = allocator.new_cache()
+    ids = torch.randint(0, 96, (1, 10))
+    with torch.no_grad():
+        engine(ids, cache)  # 10 tokens -> 3 blocks
+        for t in range(3):  # crosses into a 4th block
+            engine(ids[:, t : t + 1], cache)
+    assert len(cache.block_table) == 4
+    assert cache.block_table_device[:4].tolist() == cache.block_table
+
+
+def test_forced_direct_moe_preflight_preserves_paged_cache_at_block_boundary():
+    engine = make_engine()
+    allocator = engine.new_block_allocator(num_blocks=4, block_size=4)
+    cache = allocator.new_cache()
+    ids = torch.randint(0, 96, (1, 4))
+    with torch.no_grad():
+        engine(ids, cache)
+    snapshot = (
+        cache.position,
+        list(cache.block_table),
+        sorted(allocator.free_blocks),
+        cache._write_index_key,
+        cache.block_table_device.clone(),
+        allocator.k_pool.clone(),
+        allocator.v_pool.clone(),
+    )
+    engine.set_moe_mode("direct")
+    with torch.no_grad(), pytest.raises(RuntimeError, match="direct"):
+        engine(ids[:, :1], cache)  # the next token would open a new block
+    assert cache.position == snapshot[0] and cache.block_table == snapshot[1]
+    assert sorted(allocator.free_blocks) == snapshot[2] and cache._write_index_key == snapshot[3]
+    for now, then in zip((cache.block_table_device, allocator.k_pool, allocator.v_pool), snapshot[4:]):
+        assert torch.equal(now, then)
+
+
+@pytest.mark.parametrize("block_size", [1, 4, 16])
+def test_cpu_paged_cache_matches_oracle_closed_forms(block_size):
+    """The product's CPU write/read against the oracle's append_rows/gather_rows."""
+    cfg = ModelConfig(**TINY128)
+    allocator = BlockAllocator(cfg, num_blocks=40, block_size=block_size, device="cpu")
+    random.Random(block_size).shuffle(allocator.free_blocks)
+    cache = PagedKVCache(allocator)
+    g = torch.Generator().manual_seed(block_size)
+    H, D, ctx = cfg.num_heads, cfg.head_dim, 2 * block_size + 5
+    k = torch.randn(1, H, ctx, D, generator=g)
+    v = torch.randn(1, H, ctx, D, generator=g)
+    ok, ov = allocator.k_pool.numpy().copy(), allocator.v_pool.numpy().copy()
+    cache.write(1, 0, k[:, :, : ctx - 2], v[:, :, : ctx - 2])
+    cache.write(1, ctx - 2, k[:, :, ctx - 2 : ctx - 1], v[:, :, ctx - 2 : ctx - 1])
+    cache.write(1, ctx - 1, k[:, :, ctx - 1 :], v[:, :, ctx - 1 :])
+    ref.append_rows(ok, ov, 1, cache.block_table, 0, k[0].numpy(), v[0].numpy())
+    assert np.array_equal(allocator.k_pool.numpy(), ok) and np.array_equal(allocator.v_pool.numpy(), ov)
+    rk, rv = cache.read(1, ctx)
+    assert np.array_equal(rk[0].numpy(), ref.gather_rows(ok, 1, cache.block_table, ctx))
+    assert np.array_equal(rv[0].numpy(), ref.gather_rows(ov, 1, cache.block_table, ctx))
+
+
+def test_is_supported_is_false_off_device():
+    x = torch.zeros(1, 1, 32)
+    assert not paged_attention.is_supported(x)
+    assert not paged_attention.is_supported(x.double(), head_dim=64)
+
+
+def test_contiguous_kvcache_is_a_view():
+    cfg = ModelConfig(**TINY)
+    cache = KVCache(cfg, 1, "cpu")
+    k = torch.randn(1, cfg.num_heads, 3, cfg.head_dim)
+    cache.write(0, 2, k, -k)
+    rk, rv = cache.read(0, 5)
+    assert torch.equal(rk[:, :, 2:], k) and torch.equal(rv[:, :, 2:], -k)
+    assert rk.data_ptr() == cache.k.data_ptr()
