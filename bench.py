@@ -46,7 +46,26 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
+    p.add_argument(
+        "--copy-calibration-mib",
+        type=int,
+        default=0,
+        help="first run 10 plain device copies of this many MiB (reads and writes that many bytes "
+        "each), to scale hardware byte counters against a kernel of known traffic",
+    )
     return p.parse_args()
+
+
+def copy_calibration(torch, mib):
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 10 copies of {n * 4} bytes")
+    del src, dst
+    torch.cuda.empty_cache()
 
 
 def log(*parts):
@@ -77,7 +96,9 @@ def run_config4(torch, args):
     heads, dim = 12, 64
     attn_bytes = workloads.attention_bytes(w.lens, heads, dim, 16, 2)
     app_bytes = workloads.append_bytes(len(w.lens), heads, dim, 2)
-    part, ws_bytes = _native.decode_plan(len(w.lens), heads, dim, w.max_len, torch.bfloat16, args.partition_tokens)
+    part, ws_bytes = _native.decode_plan(
+        len(w.lens), heads, dim, 16, w.max_len, torch.bfloat16, args.partition_tokens
+    )
 
     def append():
         kv_ops.append(w.k_pool, w.v_pool, 0, k_new, v_new, w.block_tables, positions=positions)
@@ -192,7 +213,7 @@ def secondary_config2(torch):
     w = workloads.make_workload([2048] * 64, block_size=16, num_blocks=64 * 128, dtype=torch.bfloat16, seed=1)
     nbytes = workloads.attention_bytes([2048], 12, 64, 16, 2)
     k0, v0 = w.k_pool[0], w.v_pool[0]
-    tables = [w.block_tables[b].contiguous() for b in range(64)]
+    tables = [w.block_tables[b : b + 1] for b in range(64)]  # [1, 128] rows
     qs = [w.q[b : b + 1] for b in range(64)]
     warm = timed_us(torch, lambda: paged_attention.decode_layer(qs[0], k0, v0, tables[0], context_len=2048))
     it = [0]
@@ -336,6 +357,8 @@ def main():
     if not torch.cuda.is_available():
         sys.exit("bench.py needs a ROCm GPU")
     torch.cuda.set_device(0)
+    if args.copy_calibration_mib > 0:
+        copy_calibration(torch, args.copy_calibration_mib)
     log("config 4: building workload")
     main_res = run_config4(torch, args)
     log(f"config 4: {main_res['value']:.1f} GB/s, attention {main_res['roofline']['achieved']} GB/s")

@@ -62,7 +62,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 1
+#define MIE_ABI_VERSION 2
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -153,7 +153,7 @@ int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
  * bytes it needs (0 when every sequence fits one partition).
  */
 int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32_t head_dim,
-                              int32_t max_ctx_len, int32_t dtype,
+                              int32_t block_size, int32_t max_ctx_len, int32_t dtype,
                               int32_t partition_tokens,
                               int32_t* partition_tokens_out,
                               int64_t* workspace_bytes_out);

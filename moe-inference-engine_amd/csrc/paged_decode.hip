@@ -9,14 +9,24 @@
 // partition, so its waves walk the same block-table entries and neighbouring
 // (block, head) tiles.  grid = (partitions, ceil(H / WAVES), batch); work items
 // past a sequence's last partition exit at once, so ragged batches need no
-// host-side work list and no device-to-host read of the lengths.
+// host-side work list and no device-to-host read of the lengths.  Partitions
+// are short (about 128-512 tokens) so the hardware dispatcher keeps refilling
+// CUs with fresh work items and the kernel ends without a long tail.
 //
 // Lane layout.  A token's head_dim row is split into NV slices of VEC elements
 // (VB = 16 bytes for f32 and bf16), held by LPT = next_pow2(NV) consecutive
-// lanes; one wave load therefore reads TPL = 64 / LPT whole token rows, and for
-// block_size >= TPL those rows are one contiguous run of the (block, head)
-// tile: a fully coalesced 1 KiB access.  A tile is ROWS such loads of K and of
-// V, all issued before any arithmetic.
+// lanes; one wave load reads TPL = 64 / LPT whole token rows, and for
+// block_size a multiple of TPL those rows are one contiguous run of the
+// (block, head) tile: a fully coalesced 1 KiB access.  A tile is ROWS such
+// loads of K and of V.  Tiles are software pipelined: the loads of tile i+1 are
+// issued before tile i is consumed.  K/V loads carry the non-temporal hint
+// (each byte is read once; measured ~15 % faster on config 4 than plain loads).
+//
+// Block ids.  When the block size is a power of two that is a multiple of TPL
+// and a partition spans at most 64 blocks (the FAST path, the common case), the
+// partition's block ids are read once, one per lane, and each row's id is a
+// readlane (a scalar) - no table load on the per-tile critical path.  Other
+// shapes read the table per row with a fast division by the block size.
 //
 // Online softmax.  Each TPL-lane group keeps its own running (max, sum, acc)
 // over the tokens it reads, so the per-tile work needs no cross-group
@@ -27,8 +37,8 @@
 //
 // Split context.  With more than one partition per sequence the work item
 // writes its (max, sum, acc[D]) partial to the workspace and a second kernel
-// merges the partials of each (sequence, head); a sequence that fits one
-// partition is normalised and written by the first kernel.
+// merges the partials of each (sequence, head) in one pass; a sequence that
+// fits one partition is normalised and written by the first kernel.
 #include <math.h>
 
 #include "mie_common.h"
@@ -37,8 +47,16 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWaves = 4;            // heads (wavefronts) per workgroup
+constexpr int kWindow = 64;          // FAST path: block ids held one per lane
+// Automatic partition size: the smallest power of two (>= the tile) that keeps
+// the grid at or below kTargetItems wavefronts AND every sequence at or below
+// kMaxParts partitions.  The first bound keeps partitions short enough for the
+// dispatcher to balance; the second bounds the merge work per (sequence, head).
+// Fitted on MI355X: config 4 (64 x U[512, 8192]) is fastest at 128 tokens,
+// 8 x 131072 at 512-1024, 1 x 131072 at 512.
 constexpr int kSinglePassCtx = 256;  // auto plan: one partition up to this context
-constexpr int kTargetItems = 16384;  // auto plan: grid work items to aim below
+constexpr int kTargetItems = 49152;  // auto plan: grid wavefronts to stay below
+constexpr int kMaxParts = 256;       // auto plan: partitions per sequence to stay below
 
 constexpr int next_pow2(int x) {
   int p = 1;
@@ -70,20 +88,36 @@ struct Geometry {
 
 template <int NW> struct Words { uint32_t w[NW]; };
 
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 template <int NW>
 __device__ __forceinline__ Words<NW> load_words(const char* p) {
   Words<NW> r;
   if constexpr (NW == 4) {
-    const uint4 x = *reinterpret_cast<const uint4*>(p);
+    const u32x4_t x = *reinterpret_cast<const u32x4_t*>(p);
     r.w[0] = x.x; r.w[1] = x.y; r.w[2] = x.z; r.w[3] = x.w;
   } else {
-    const uint2 x = *reinterpret_cast<const uint2*>(p);
+    const u32x2_t x = *reinterpret_cast<const u32x2_t*>(p);
     r.w[0] = x.x; r.w[1] = x.y;
   }
   return r;
 }
 
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// Streaming load of data read exactly once (global_load ... nt).
+template <int NW>
+__device__ __forceinline__ Words<NW> load_words_nt(const char* p) {
+  Words<NW> r;
+  if constexpr (NW == 4) {
+    const u32x4_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    r.w[0] = x.x; r.w[1] = x.y; r.w[2] = x.z; r.w[3] = x.w;
+  } else {
+    const u32x2_t x = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p));
+    r.w[0] = x.x; r.w[1] = x.y;
+  }
+  return r;
+}
 
 struct DecodeArgs {
   const char* q;
@@ -116,60 +150,37 @@ __device__ __forceinline__ int seq_ctx(const DecodeArgs& a, int b) {
   return c < a.max_ctx ? c : a.max_ctx;
 }
 
-// Writes VEC consecutive outputs starting at `dst` (element pointer math done
-// by the caller) in f32 or the kernel's dtype.
-template <int DT, int VEC>
+// Writes N consecutive outputs at element offset `elem_off` of `base`, in f32
+// or in the kernel's dtype (N a multiple of 4).
+template <int DT, int N>
 __device__ __forceinline__ void store_out(char* base, int64_t elem_off, const float* val, bool f32) {
   if (f32 || DT == MIE_DTYPE_F32) {
     float* p = reinterpret_cast<float*>(base) + elem_off;
 #pragma unroll
-    for (int i = 0; i < VEC; i += 4) {
-      if constexpr (VEC >= 4) {
-        *reinterpret_cast<float4*>(p + i) = make_float4(val[i], val[i + 1], val[i + 2], val[i + 3]);
-      }
-    }
+    for (int i = 0; i < N; i += 4)
+      *reinterpret_cast<float4*>(p + i) = make_float4(val[i], val[i + 1], val[i + 2], val[i + 3]);
   } else {
     uint32_t* p = reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(base) + elem_off);
-    if constexpr (VEC == 8) {
-      *reinterpret_cast<uint4*>(p) =
-          make_uint4(mie::pack_bf16x2(val[0], val[1]), mie::pack_bf16x2(val[2], val[3]),
-                     mie::pack_bf16x2(val[4], val[5]), mie::pack_bf16x2(val[6], val[7]));
-    } else {
-      *reinterpret_cast<uint2*>(p) =
-          make_uint2(mie::pack_bf16x2(val[0], val[1]), mie::pack_bf16x2(val[2], val[3]));
-    }
+#pragma unroll
+    for (int i = 0; i < N; i += 4)
+      *reinterpret_cast<uint2*>(p + i / 2) =
+          make_uint2(mie::pack_bf16x2(val[i], val[i + 1]), mie::pack_bf16x2(val[i + 2], val[i + 3]));
   }
 }
 
-template <int DT, int D>
-__global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a) {
+// One work item: sequence b (ctx tokens, ctx > 0), head h, partition `part`,
+// computed by one full wavefront.
+template <int DT, int D, bool FAST>
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, int part, int ctx, int lane) {
   using G = Geometry<DT, D>;
   constexpr int ELT = G::ELT, VEC = G::VEC, NW = G::NW, LPT = G::LPT, TPL = G::TPL;
   constexpr int ROWS = G::ROWS, TILE = G::TILE;
+  constexpr int64_t ROW_BYTES = static_cast<int64_t>(D) * ELT;
 
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int h = blockIdx.y * kWaves + wave;
-  if (h >= a.H) return;
-  const int b = blockIdx.z;
-  const int part = blockIdx.x;
-  const int ctx = seq_ctx(a, b);
   const int nparts = (ctx + (1 << a.part_shift) - 1) >> a.part_shift;
-
   const int g = lane / LPT;   // token group within a wave load
   const int jl = lane % LPT;  // slice of the head_dim row
   const bool jv = jl < G::NV;
-
-  if (ctx == 0) {  // no keys: scaled_dot_product_attention returns zeros
-    if (part == 0 && g == 0 && jv) {
-      float zero[VEC];
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) zero[i] = 0.f;
-      store_out<DT, VEC>(a.out, b * a.o_sb + h * a.o_sh + jl * VEC, zero, a.out_f32);
-    }
-    return;
-  }
-  if (part >= nparts) return;
   const int t_begin = part << a.part_shift;
   const int t_end = min(ctx, t_begin + (1 << a.part_shift));
 
@@ -190,39 +201,57 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
   const char* vbase = a.v + lane_off;
   const int64_t blk_bytes = a.kv_sblk * ELT;
 
+  bool bad = false;
+  int fb = 0;
+  int32_t ids = 0;
+  if constexpr (FAST) {  // the partition's block ids, one per lane
+    fb = t_begin >> a.bs.shift;
+    const int nblk = ((t_end - 1) >> a.bs.shift) - fb + 1;  // <= kWindow by the plan
+    const uint32_t idx = static_cast<uint32_t>(fb + lane);
+    const bool mine = lane < nblk;
+    ids = (mine && idx < a.bt_cap) ? bt[idx] : -1;
+    bad = __any(mine && (ids < 0 || ids >= a.num_blocks));
+  }
+
+  auto issue = [&](int t0, Words<NW>* kr, Words<NW>* vr) {
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) { kr[r].w[w] = 0u; vr[r].w[w] = 0u; }
+      if constexpr (FAST) {
+        const int tr = t0 + r * TPL;  // first token of the row (wave-uniform)
+        if (tr < t_end && !bad) {
+          const int phys = __builtin_amdgcn_readlane(ids, (tr >> a.bs.shift) - fb);
+          const int64_t off = phys * blk_bytes + static_cast<int64_t>((tr & (a.bs.d - 1)) + g) * ROW_BYTES;
+          if (jv && tr + g < t_end) {
+            kr[r] = load_words_nt<NW>(kbase + off);
+            vr[r] = load_words_nt<NW>(vbase + off);
+          }
+        }
+      } else {
+        const int t = t0 + r * TPL + g;
+        if (t < t_end) {
+          const uint32_t blk = a.bs.div(static_cast<uint32_t>(t));
+          const uint32_t slot = static_cast<uint32_t>(t) - blk * a.bs.d;
+          const int32_t phys = blk < a.bt_cap ? bt[blk] : -1;
+          if (phys < 0 || phys >= a.num_blocks) {
+            bad = true;
+          } else if (jv) {
+            const int64_t off = phys * blk_bytes + static_cast<int64_t>(slot) * ROW_BYTES;
+            kr[r] = load_words_nt<NW>(kbase + off);
+            vr[r] = load_words_nt<NW>(vbase + off);
+          }
+        }
+      }
+    }
+  };
+
   float m = -INFINITY, l = 0.f;
   float acc[VEC];
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
-  bool bad = false;
 
-  for (int t0 = t_begin; t0 < t_end; t0 += TILE) {
-    Words<NW> kr[ROWS], vr[ROWS];
-    bool valid[ROWS];
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-      const int t = t0 + r * TPL + g;
-      bool ok = t < t_end;
-      int64_t off = 0;
-      if (ok) {
-        const uint32_t blk = a.bs.div(static_cast<uint32_t>(t));
-        const uint32_t slot = static_cast<uint32_t>(t) - blk * a.bs.d;
-        const int32_t phys = blk < a.bt_cap ? bt[blk] : -1;
-        if (phys < 0 || phys >= a.num_blocks) {
-          bad = true;
-          ok = false;
-        }
-        off = phys * blk_bytes + static_cast<int64_t>(slot) * (D * ELT);
-      }
-      valid[r] = ok;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) { kr[r].w[w] = 0u; vr[r].w[w] = 0u; }
-      if (ok && jv) {
-        kr[r] = load_words<NW>(kbase + off);
-        vr[r] = load_words<NW>(vbase + off);
-      }
-    }
-
+  auto consume = [&](int t0, const Words<NW>* kr, const Words<NW>* vr) {
     float s[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -231,17 +260,15 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
 #pragma unroll
         for (int w = 0; w < NW; ++w)
           part_dot = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kr[r].w[w]),
-                                                     __builtin_bit_cast(bf16x2_t, qw.w[w]),
-                                                     part_dot, false);
+                                                     __builtin_bit_cast(bf16x2_t, qw.w[w]), part_dot, false);
         s[r] = mie::group_sum<LPT>(part_dot) * a.qk_scale;
       } else {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) part_dot = fmaf(__uint_as_float(kr[r].w[i]), qf[i], part_dot);
         s[r] = mie::group_sum<LPT>(part_dot);
       }
-      s[r] = valid[r] ? s[r] : -INFINITY;
+      s[r] = t0 + r * TPL + g < t_end ? s[r] : -INFINITY;
     }
-
     float tmax = s[0];
 #pragma unroll
     for (int r = 1; r < ROWS; ++r) tmax = fmaxf(tmax, s[r]);
@@ -272,6 +299,17 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
       }
     }
     m = m_new;
+  };
+
+  // Two register sets: tile i+1 is in flight while tile i is consumed.
+  Words<NW> kA[ROWS], vA[ROWS], kB[ROWS], vB[ROWS];
+  issue(t_begin, kA, vA);
+  for (int t0 = t_begin; t0 < t_end; t0 += 2 * TILE) {
+    if (t0 + TILE < t_end) issue(t0 + TILE, kB, vB);
+    consume(t0, kA, vA);
+    if (t0 + TILE >= t_end) break;
+    if (t0 + 2 * TILE < t_end) issue(t0 + 2 * TILE, kA, vA);
+    consume(t0 + TILE, kB, vB);
   }
 
   // Merge the TPL token groups (lanes jl, jl + LPT, ...) with log-sum-exp.
@@ -288,7 +326,7 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
     for (int i = 0; i < VEC; ++i) acc[i] = acc[i] * ca + __shfl_xor(acc[i], off) * cb;
     m = mn;
   }
-  bad = __any(bad);
+  if constexpr (!FAST) bad = __any(bad);
 
   if (g != 0 || !jv) return;
   if (nparts == 1) {
@@ -301,7 +339,8 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
     const int64_t item = (static_cast<int64_t>(b) * a.H + h) * a.max_parts + part;
     float* dst = a.ws_acc + item * D + jl * VEC;
 #pragma unroll
-    for (int i = 0; i < VEC; i += 4) *reinterpret_cast<float4*>(dst + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
+    for (int i = 0; i < VEC; i += 4)
+      *reinterpret_cast<float4*>(dst + i) = make_float4(acc[i], acc[i + 1], acc[i + 2], acc[i + 3]);
     if (jl == 0) {
       a.ws_ml[2 * item] = bad ? NAN : m;
       a.ws_ml[2 * item + 1] = l;
@@ -309,83 +348,134 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
   }
 }
 
-// Merge the partition partials of one (sequence, head):
+// Writes zeros for a sequence with no keys (what scaled_dot_product_attention
+// returns for an empty key set).
+template <int DT, int D>
+__device__ __forceinline__ void zero_item(const DecodeArgs& a, int b, int h, int lane) {
+  using G = Geometry<DT, D>;
+  const int jl = lane % G::LPT;
+  if (lane / G::LPT != 0 || jl >= G::NV) return;
+  float zero[G::VEC];
+#pragma unroll
+  for (int i = 0; i < G::VEC; ++i) zero[i] = 0.f;
+  store_out<DT, G::VEC>(a.out, b * a.o_sb + h * a.o_sh + jl * G::VEC, zero, a.out_f32);
+}
+
+// grid = (max partitions, ceil(H / WAVES), batch); items past a sequence's
+// last partition exit.
+template <int DT, int D, bool FAST>
+__global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.y * kWaves + wave;
+  if (h >= a.H) return;
+  const int b = blockIdx.z;
+  const int part = blockIdx.x;
+  const int ctx = seq_ctx(a, b);
+  if (ctx == 0) {
+    if (part == 0) zero_item<DT, D>(a, b, h, lane);
+    return;
+  }
+  if (part >= (ctx + (1 << a.part_shift) - 1) >> a.part_shift) return;
+  decode_item<DT, D, FAST>(a, b, h, part, ctx, lane);
+}
+
+// Merge the partition partials of one (sequence, head) in one pass:
 //   M = max_i m_i,  w_i = 2^(m_i - M),  out = sum_i w_i acc_i / sum_i w_i l_i.
-// 256 threads: COLS = D columns x RROWS partition lanes, combined through LDS.
+// 256 threads = COLS column threads (4 elements each) x PL partition lanes.
+// Each thread folds its partitions (i = pl, pl + PL, ...) into a running
+// (m, l, acc) with the same rescaling as the main kernel, so all partial loads
+// are independent; the PL states of a column are then merged through LDS.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void paged_decode_reduce_kernel(DecodeArgs a) {
-  constexpr int RROWS = 256 / D > 0 ? 256 / D : 1;
-  __shared__ float red[256];
-  __shared__ float stat[2];
+  constexpr int COLS = D / 4;
+  constexpr int PL = 256 / COLS;
+  __shared__ float s_m[256], s_l[256];
+  __shared__ float4 s_acc[256];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
   const int ctx = seq_ctx(a, b);
   const int nparts = (ctx + (1 << a.part_shift) - 1) >> a.part_shift;
   if (nparts <= 1) return;
   const int tid = threadIdx.x;
+  const int col = tid % COLS;
+  const int pl = tid / COLS;
   const int64_t base = (static_cast<int64_t>(b) * a.H + h) * a.max_parts;
   const float* ml = a.ws_ml + 2 * base;
+  const float* accs = a.ws_acc + base * D + col * 4;
 
-  // Global max, then the weighted sum of the partition sums (wave 0 only).
-  if (tid < 64) {
-    float mx = -INFINITY;
-    for (int i = tid; i < nparts; i += 64) mx = fmaxf(mx, ml[2 * i]);
-    mx = mie::wave_max(mx);
-    const float mr = mx == -INFINITY ? 0.f : mx;
-    float ls = 0.f;
-    for (int i = tid; i < nparts; i += 64) ls += ml[2 * i + 1] * mie::fast_exp2(ml[2 * i] - mr);
-    ls = mie::wave_sum(ls);
-    if (tid == 0) {
-      stat[0] = mr;
-      stat[1] = ls;
+  float m = -INFINITY, l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (pl < PL) {
+#pragma unroll 4
+    for (int i = pl; i < nparts; i += PL) {
+      const float mi = ml[2 * i];
+      const float li = ml[2 * i + 1];
+      const float4 ai = *reinterpret_cast<const float4*>(accs + static_cast<int64_t>(i) * D);
+      const float mn = fmaxf(m, mi);
+      const float mr = mn == -INFINITY ? 0.f : mn;
+      const float ca = mie::fast_exp2(m - mr);
+      const float cb = mie::fast_exp2(mi - mr);
+      l = l * ca + li * cb;
+      acc.x = acc.x * ca + ai.x * cb;
+      acc.y = acc.y * ca + ai.y * cb;
+      acc.z = acc.z * ca + ai.z * cb;
+      acc.w = acc.w * ca + ai.w * cb;
+      m = mn;
     }
   }
+  s_m[tid] = m;
+  s_l[tid] = l;
+  s_acc[tid] = acc;
   __syncthreads();
-  const float mr = stat[0];
-  const float inv = 1.f / stat[1];
-
-  const int col = tid % D;
-  const int row = tid / D;
-  float accv = 0.f;
-  if (row < RROWS) {
-    const float* acc = a.ws_acc + base * D + col;
-    for (int i = row; i < nparts; i += RROWS) accv += acc[static_cast<int64_t>(i) * D] * mie::fast_exp2(ml[2 * i] - mr);
+  if (tid >= COLS) return;
+  float mx = -INFINITY;
+  for (int r = 0; r < PL; ++r) mx = fmaxf(mx, s_m[r * COLS + tid]);
+  const float mr = mx == -INFINITY ? 0.f : mx;
+  float lt = 0.f;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < PL; ++r) {
+    const float w = mie::fast_exp2(s_m[r * COLS + tid] - mr);
+    const float4 v = s_acc[r * COLS + tid];
+    lt += s_l[r * COLS + tid] * w;
+    o[0] += v.x * w;
+    o[1] += v.y * w;
+    o[2] += v.z * w;
+    o[3] += v.w * w;
   }
-  red[tid] = accv;
-  __syncthreads();
-  if (tid < D) {
-    float sum = 0.f;
-    for (int r = 0; r < RROWS; ++r) sum += red[r * D + tid];
-    sum *= inv;
-    const int64_t o = b * a.o_sb + h * a.o_sh + tid;
-    if (a.out_f32 || DT == MIE_DTYPE_F32) {
-      reinterpret_cast<float*>(a.out)[o] = sum;
-    } else {
-      reinterpret_cast<uint16_t*>(a.out)[o] = static_cast<uint16_t>(mie::f32_to_bf16_bits(sum));
-    }
-  }
+  const float inv = 1.f / lt;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] *= inv;
+  store_out<DT, 4>(a.out, b * a.o_sb + h * a.o_sh + tid * 4, o, a.out_f32);
 }
 
 // ---- host side --------------------------------------------------------------
 
-template <int DT, int D>
-constexpr int tile_of() { return Geometry<DT, D>::TILE; }
-
 // Head dims built for each dtype.  Each needs D % VEC == 0 (VEC = 4 for f32,
-// min(8, D) for bf16) and D <= 256.
+// min(8, D) for bf16), D % 4 == 0 and D <= 256.
 #define MIE_FOR_EACH_HEAD_DIM(X) X(4) X(8) X(16) X(32) X(64) X(96) X(128) X(256)
 
-int tile_for(int dtype, int head_dim) {
-#define MIE_TILE_CASE(DD)                                            \
-  case DD:                                                           \
-    return dtype == MIE_DTYPE_F32 ? tile_of<MIE_DTYPE_F32, DD>()     \
-                                  : tile_of<MIE_DTYPE_BF16, DD>();
-  if (dtype != MIE_DTYPE_F32 && dtype != MIE_DTYPE_BF16) return 0;
+struct KernelShape {
+  int tile;  // tokens per tile; 0 = (dtype, head_dim) not built
+  int tpl;   // tokens per wave load
+};
+
+template <int DT, int D>
+constexpr KernelShape shape_of() {
+  return KernelShape{Geometry<DT, D>::TILE, Geometry<DT, D>::TPL};
+}
+
+KernelShape shape_for(int dtype, int head_dim) {
+#define MIE_SHAPE_CASE(DD)                                         \
+  case DD:                                                         \
+    return dtype == MIE_DTYPE_F32 ? shape_of<MIE_DTYPE_F32, DD>()  \
+                                  : shape_of<MIE_DTYPE_BF16, DD>();
+  if (dtype != MIE_DTYPE_F32 && dtype != MIE_DTYPE_BF16) return KernelShape{0, 0};
   switch (head_dim) {
-    MIE_FOR_EACH_HEAD_DIM(MIE_TILE_CASE)
-    default: return 0;
+    MIE_FOR_EACH_HEAD_DIM(MIE_SHAPE_CASE)
+    default: return KernelShape{0, 0};
   }
-#undef MIE_TILE_CASE
+#undef MIE_SHAPE_CASE
 }
 
 int ilog2(uint32_t x) {
@@ -394,55 +484,75 @@ int ilog2(uint32_t x) {
   return s;
 }
 
-int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t max_ctx, int32_t dtype,
-             int32_t requested, int32_t* part_out, int64_t* ws_out, int32_t* max_parts_out) {
-  const int tile = tile_for(dtype, head_dim);
-  if (tile == 0)
+bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+
+struct Plan {
+  int32_t part;
+  int32_t max_parts;
+  int64_t ws_bytes;
+  bool fast;
+};
+
+int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size, int32_t max_ctx,
+             int32_t dtype, int32_t requested, Plan* out) {
+  const KernelShape ks = shape_for(dtype, head_dim);
+  if (ks.tile == 0)
     return mie::fail(MIE_ERR_UNSUPPORTED, "mie_paged_decode: head_dim %d dtype %d not built", head_dim,
                      dtype);
-  if (batch < 0 || num_heads <= 0 || max_ctx < 0)
-    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: bad shape batch=%d heads=%d max_ctx=%d", batch,
-                     num_heads, max_ctx);
+  if (batch < 0 || num_heads <= 0 || max_ctx < 0 || block_size <= 0)
+    return mie::fail(MIE_ERR_INVALID,
+                     "mie_paged_decode: bad shape batch=%d heads=%d block_size=%d max_ctx=%d", batch,
+                     num_heads, block_size, max_ctx);
+  const bool fast_blocks = is_pow2(block_size) && block_size % ks.tpl == 0;
+  const int64_t fast_cap = static_cast<int64_t>(kWindow) * block_size;  // FAST: <= kWindow blocks
   int64_t part;
   if (requested > 0) {
-    if ((requested & (requested - 1)) != 0 || requested % tile != 0)
+    if (!is_pow2(requested) || requested % ks.tile != 0)
       return mie::fail(MIE_ERR_INVALID,
                        "mie_paged_decode: partition_tokens %d must be a power of two and a multiple "
                        "of the %d-token tile",
-                       requested, tile);
+                       requested, ks.tile);
     part = requested;
   } else if (max_ctx <= kSinglePassCtx) {
-    part = tile;
+    part = ks.tile;
     while (part < max_ctx) part <<= 1;
   } else {
-    part = tile;
+    part = ks.tile;
     const int64_t rows = static_cast<int64_t>(batch) * num_heads;
-    while (part < max_ctx && rows * ((max_ctx + part - 1) / part) > kTargetItems) part <<= 1;
+    while (part < max_ctx && (rows * ((max_ctx + part - 1) / part) > kTargetItems ||
+                              (max_ctx + part - 1) / part > kMaxParts))
+      part <<= 1;
+    if (fast_blocks && part > fast_cap && ks.tile <= fast_cap) part = fast_cap;
   }
   if (part > (int64_t{1} << 30)) part = int64_t{1} << 30;
   const int64_t max_parts = max_ctx > 0 ? (max_ctx + part - 1) / part : 1;
   if (max_parts > 0x7fffffff) return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: too many partitions");
-  *part_out = static_cast<int32_t>(part);
-  *max_parts_out = static_cast<int32_t>(max_parts);
-  *ws_out = max_parts > 1 ? static_cast<int64_t>(batch) * num_heads * max_parts * (head_dim + 2) * 4 : 0;
+  out->part = static_cast<int32_t>(part);
+  out->max_parts = static_cast<int32_t>(max_parts);
+  out->ws_bytes = max_parts > 1 ? static_cast<int64_t>(batch) * num_heads * max_parts * (head_dim + 2) * 4 : 0;
+  out->fast = fast_blocks && part <= fast_cap;
   return MIE_OK;
 }
 
 template <int DT, int D>
-int32_t launch(DecodeArgs& a, int batch, hipStream_t st) {
+int32_t launch(DecodeArgs& a, int batch, bool fast, hipStream_t st) {
   const dim3 grid(a.max_parts, (a.H + kWaves - 1) / kWaves, batch);
-  paged_decode_kernel<DT, D><<<grid, 64 * kWaves, 0, st>>>(a);
+  if (fast) {
+    paged_decode_kernel<DT, D, true><<<grid, 64 * kWaves, 0, st>>>(a);
+  } else {
+    paged_decode_kernel<DT, D, false><<<grid, 64 * kWaves, 0, st>>>(a);
+  }
   int32_t rc = mie::check_launch("paged_decode_kernel");
   if (rc != MIE_OK || a.max_parts <= 1) return rc;
   paged_decode_reduce_kernel<DT, D><<<dim3(a.H, batch), 256, 0, st>>>(a);
   return mie::check_launch("paged_decode_reduce_kernel");
 }
 
-int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, hipStream_t st) {
-#define MIE_LAUNCH_CASE(DD)                                                          \
-  case DD:                                                                           \
-    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, st)          \
-                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, st);
+int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, hipStream_t st) {
+#define MIE_LAUNCH_CASE(DD)                                                             \
+  case DD:                                                                              \
+    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, st)       \
+                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, st);
   switch (head_dim) {
     MIE_FOR_EACH_HEAD_DIM(MIE_LAUNCH_CASE)
     default: return mie::fail(MIE_ERR_UNSUPPORTED, "mie_paged_decode: head_dim %d not built", head_dim);
@@ -455,19 +565,18 @@ bool aligned(const void* p, int n) { return reinterpret_cast<uintptr_t>(p) % n =
 }  // namespace
 
 extern "C" int32_t mie_paged_decode_supported(int32_t head_dim, int32_t dtype) {
-  return tile_for(dtype, head_dim) != 0 ? 1 : 0;
+  return shape_for(dtype, head_dim).tile != 0 ? 1 : 0;
 }
 
 extern "C" int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32_t head_dim,
-                                         int32_t max_ctx_len, int32_t dtype, int32_t partition_tokens,
-                                         int32_t* partition_tokens_out, int64_t* workspace_bytes_out) {
-  int32_t part = 0, max_parts = 0;
-  int64_t ws = 0;
-  const int32_t rc = plan(batch, num_heads, head_dim, max_ctx_len, dtype, partition_tokens, &part, &ws,
-                          &max_parts);
+                                         int32_t block_size, int32_t max_ctx_len, int32_t dtype,
+                                         int32_t partition_tokens, int32_t* partition_tokens_out,
+                                         int64_t* workspace_bytes_out) {
+  Plan p;
+  const int32_t rc = plan(batch, num_heads, head_dim, block_size, max_ctx_len, dtype, partition_tokens, &p);
   if (rc != MIE_OK) return rc;
-  if (partition_tokens_out) *partition_tokens_out = part;
-  if (workspace_bytes_out) *workspace_bytes_out = ws;
+  if (partition_tokens_out) *partition_tokens_out = p.part;
+  if (workspace_bytes_out) *workspace_bytes_out = p.ws_bytes;
   return MIE_OK;
 }
 
@@ -481,15 +590,12 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
                                     int64_t out_stride_h, int32_t out_dtype, void* workspace,
                                     int64_t workspace_bytes, int32_t partition_tokens, int32_t dtype,
                                     void* stream) {
-  int32_t part = 0, max_parts = 0;
-  int64_t ws = 0;
-  int32_t rc = plan(batch, num_heads, head_dim, max_ctx_len, dtype, partition_tokens, &part, &ws,
-                    &max_parts);
+  Plan p;
+  int32_t rc = plan(batch, num_heads, head_dim, block_size, max_ctx_len, dtype, partition_tokens, &p);
   if (rc != MIE_OK) return rc;
   if (batch == 0) return MIE_OK;
-  if (block_size <= 0 || num_blocks <= 0)
-    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: block_size=%d num_blocks=%d", block_size,
-                     num_blocks);
+  if (num_blocks <= 0)
+    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: num_blocks=%d", num_blocks);
   if (!ctx_lens && (ctx_len < 0 || ctx_len > max_ctx_len))
     return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: ctx_len %d outside [0, max_ctx_len=%d]", ctx_len,
                      max_ctx_len);
@@ -503,21 +609,22 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
   if (pool_stride_head < static_cast<int64_t>(block_size) * head_dim ||
       pool_stride_block < static_cast<int64_t>(num_heads) * pool_stride_head)
     return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: pool strides overlap");
-  if (ws > 0 && (!workspace || workspace_bytes < ws || !aligned(workspace, 16)))
+  if (p.ws_bytes > 0 && (!workspace || workspace_bytes < p.ws_bytes || !aligned(workspace, 16)))
     return mie::fail(MIE_ERR_WORKSPACE, "mie_paged_decode: needs a 16-byte aligned workspace of %lld bytes",
-                     static_cast<long long>(ws));
+                     static_cast<long long>(p.ws_bytes));
 
   // Every vector access must be naturally aligned: lane loads are 8 or 16
-  // bytes, outputs are written VEC elements at a time.
+  // bytes, outputs are written 4 or VEC elements at a time.
   const int elt = mie::elt_size(dtype);
+  const int oelt = mie::elt_size(out_dtype);
   const int vec = dtype == MIE_DTYPE_F32 ? 4 : (head_dim < 8 ? head_dim : 8);
   const int vb = vec * elt;
-  const int ob = vec * mie::elt_size(out_dtype);
+  const int ob = 4 * oelt;
   const bool ok_align = aligned(q, vb) && aligned(k_pool, vb) && aligned(v_pool, vb) &&
                         (q_stride_b * elt) % vb == 0 && (q_stride_h * elt) % vb == 0 &&
                         (pool_stride_block * elt) % vb == 0 && (pool_stride_head * elt) % vb == 0 &&
-                        aligned(out, ob) && (out_stride_b * mie::elt_size(out_dtype)) % ob == 0 &&
-                        (out_stride_h * mie::elt_size(out_dtype)) % ob == 0;
+                        aligned(out, vec * oelt) && (out_stride_b * oelt) % (vec * oelt) == 0 &&
+                        (out_stride_h * oelt) % (vec * oelt) == 0 && (vec * oelt) % ob == 0;
   if (!ok_align) return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: misaligned q / pool / out");
 
   DecodeArgs a;
@@ -542,14 +649,14 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
   a.o_sb = out_stride_b;
   a.o_sh = out_stride_h;
   a.out_f32 = out_dtype == MIE_DTYPE_F32 && dtype != MIE_DTYPE_F32 ? 1 : 0;
-  a.max_parts = max_parts;
-  a.part_shift = ilog2(static_cast<uint32_t>(part));
-  if (max_parts > 1) {
+  a.max_parts = p.max_parts;
+  a.part_shift = ilog2(static_cast<uint32_t>(p.part));
+  if (p.max_parts > 1) {
     a.ws_acc = static_cast<float*>(workspace);
-    a.ws_ml = a.ws_acc + static_cast<int64_t>(batch) * num_heads * max_parts * head_dim;
+    a.ws_ml = a.ws_acc + static_cast<int64_t>(batch) * num_heads * p.max_parts * head_dim;
   } else {
     a.ws_acc = nullptr;
     a.ws_ml = nullptr;
   }
-  return dispatch(dtype, head_dim, a, batch, static_cast<hipStream_t>(stream));
+  return dispatch(dtype, head_dim, a, batch, p.fast, static_cast<hipStream_t>(stream));
 }

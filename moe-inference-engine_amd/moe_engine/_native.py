@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -66,7 +66,7 @@ _SIGNATURES = {
     ),
     "mie_paged_decode_plan": (
         _i32,
-        [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
+        [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     ),
     "mie_paged_decode_supported": (_i32, [_i32, _i32]),
 }
@@ -142,13 +142,13 @@ def decode_supported(head_dim: int, dtype: torch.dtype) -> bool:
 
 
 @lru_cache(maxsize=1024)
-def decode_plan(batch, num_heads, head_dim, max_ctx_len, dtype, partition_tokens):
+def decode_plan(batch, num_heads, head_dim, block_size, max_ctx_len, dtype, partition_tokens):
     """(partition_tokens, workspace_bytes) the decode launch will use."""
     part = _i32(0)
     ws = _i64(0)
     check(
         lib().mie_paged_decode_plan(
-            batch, num_heads, head_dim, max_ctx_len, dtype_code(dtype), partition_tokens,
+            batch, num_heads, head_dim, block_size, max_ctx_len, dtype_code(dtype), partition_tokens,
             ctypes.byref(part), ctypes.byref(ws),
         ),
         "mie_paged_decode_plan",

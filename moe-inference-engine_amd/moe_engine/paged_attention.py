@@ -117,7 +117,9 @@ def decode_layer(
         raise ValueError("out must be [batch, heads, head_dim] with unit inner stride")
     if scale is None:
         scale = 1.0 / math.sqrt(head_dim)
-    _, ws_bytes = _native.decode_plan(batch, heads, head_dim, int(max_context_len), q.dtype, int(partition_tokens))
+    _, ws_bytes = _native.decode_plan(
+        batch, heads, head_dim, block_size, int(max_context_len), q.dtype, int(partition_tokens)
+    )
     ws = _workspace(ws_bytes, q.device)
     _native.check(
         lib.mie_paged_decode(
@@ -146,7 +148,7 @@ def decode(q: torch.Tensor, cache, layer_idx: int, context_len: int) -> torch.Te
     allocator = cache.allocator
     num_heads, head_dim = q.shape[1], q.shape[3]
     out = decode_layer(
-        q[0, :, 0],
+        q[:, :, 0],
         allocator.k_pool[layer_idx],
         allocator.v_pool[layer_idx],
         cache.block_table_device,

@@ -44,21 +44,21 @@ def test_decode_plan_host_query():
     import torch
 
     # Short contexts run as one partition and need no workspace.
-    part, ws = _native.decode_plan(1, 12, 64, 96, torch.bfloat16, 0)
+    part, ws = _native.decode_plan(1, 12, 64, 16, 96, torch.bfloat16, 0)
     assert part >= 96 and ws == 0
     # Long contexts split; the workspace holds (m, l, acc[D]) per partition.
-    part, ws = _native.decode_plan(8, 12, 64, 131072, torch.bfloat16, 0)
+    part, ws = _native.decode_plan(8, 12, 64, 16, 131072, torch.bfloat16, 0)
     parts = -(-131072 // part)
     assert parts > 1 and ws == 8 * 12 * parts * (64 + 2) * 4
     # An explicit partition size is honoured when it is a power of two multiple of the tile.
-    assert _native.decode_plan(2, 12, 64, 4096, torch.float32, 1024) == (1024, 2 * 12 * 4 * 66 * 4)
+    assert _native.decode_plan(2, 12, 64, 16, 4096, torch.float32, 1024) == (1024, 2 * 12 * 4 * 66 * 4)
 
 
 def test_decode_plan_rejects_bad_partition_and_unbuilt_shapes():
     import torch
 
     with pytest.raises(RuntimeError, match="partition_tokens"):
-        _native.decode_plan(1, 12, 64, 4096, torch.bfloat16, 100)
+        _native.decode_plan(1, 12, 64, 16, 4096, torch.bfloat16, 100)
     assert not _native.decode_supported(72, torch.bfloat16)
     assert not _native.decode_supported(64, torch.float64)
     assert _native.decode_supported(96, torch.float32) and _native.decode_supported(4, torch.bfloat16)

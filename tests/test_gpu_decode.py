@@ -90,11 +90,11 @@ def test_kernel_handles_other_block_sizes(block_size, dtype):
         cache, written = filled_cache(TINY, context_len, block_size, dtype=dtype)
         q = torch.randn(1, 8, 1, 4, generator=torch.Generator().manual_seed(context_len)).to(dtype)
         got = paged_attention.decode_layer(
-            q[0, :, 0].cuda(), cache.allocator.k_pool[0], cache.allocator.v_pool[0], cache.block_table_device,
+            q[:, :, 0].cuda(), cache.allocator.k_pool[0], cache.allocator.v_pool[0], cache.block_table_device,
             context_len=context_len, out_dtype=torch.float32,
         )
         atol = 1e-5 if dtype == torch.float32 else 2e-3
-        np.testing.assert_allclose(got.cpu().numpy(), oracle(q, written[0]), rtol=0, atol=atol)
+        np.testing.assert_allclose(got[0].cpu().numpy(), oracle(q, written[0]), rtol=0, atol=atol)
 
 
 def test_kernel_matches_oracle_on_every_layer():
@@ -185,7 +185,7 @@ def test_config5_long_context_split(batch, ctx, block_size, dtype):
     partitions merged by the reduce launch."""
     print_case("config5", batch, ctx, block_size, dtype)
     w = make_workload([ctx] * batch, block_size=block_size, dtype=dtype, seed=5, heavy_fraction=0.01)
-    part, ws = _native.decode_plan(batch, 12, 64, ctx, dtype, 0)
+    part, ws = _native.decode_plan(batch, 12, 64, block_size, ctx, dtype, 0)
     assert ws > 0 and part < ctx, "long contexts must take the split path"
     atol = 1e-5 if dtype == torch.float32 else 2e-3
     batches = [0, batch - 1] if batch > 1 else None
@@ -198,7 +198,7 @@ def test_partition_sizes_agree(dtype):
     oracle's answer: the log-sum-exp merge is exact up to rounding."""
     lens = [1, 31, 32, 33, 1000, 4095, 4096]
     w = make_workload(lens, block_size=16, dtype=dtype, seed=7, heavy_fraction=0.01)
-    tile, _ = _native.decode_plan(len(lens), 12, 64, 1, dtype, 0)
+    tile, _ = _native.decode_plan(len(lens), 12, 64, 16, 1, dtype, 0)
     atol = 1e-5 if dtype == torch.float32 else 2e-3
     sizes = []
     p = tile

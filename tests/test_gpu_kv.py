@@ -89,7 +89,7 @@ def test_batched_append_with_device_positions(dtype):
     """One launch appends a token to each of B sequences at their own positions."""
     gen = torch.Generator().manual_seed(5)
     B, H, D, BS, NB = 6, 12, 64, 16, 64
-    positions = [0, 15, 16, 17, 100, 255]
+    positions = [0, 15, 16, 17, 100, 127]  # rows hold 8 blocks = 128 tokens
     perm = torch.randperm(NB, generator=gen)
     tables = perm[: B * 8].view(B, 8).to(torch.int32)
     k_pool = randn((2, NB, H, BS, D), dtype, gen).cuda()
@@ -105,13 +105,14 @@ def test_batched_append_with_device_positions(dtype):
 
 
 def test_append_skips_out_of_range_block_ids():
-    """A table entry past the pool is bounds-checked in the kernel: that row is
-    not written, every other row is."""
+    """A table entry past the pool, or a position past the table row, is
+    bounds-checked in the kernel: that row is not written, every other row is."""
     k_pool = torch.zeros(1, 4, 2, 4, 8, device="cuda")
     v_pool = torch.zeros_like(k_pool)
-    tables = torch.tensor([[1], [99]], dtype=torch.int32, device="cuda")
-    k_new = torch.ones(2, 2, 1, 8, device="cuda")
-    kv_ops.append(k_pool, v_pool, 0, k_new, -k_new, tables, position=2)
+    tables = torch.tensor([[1], [99], [2]], dtype=torch.int32, device="cuda")
+    k_new = torch.ones(3, 2, 1, 8, device="cuda")
+    positions = torch.tensor([2, 2, 4], dtype=torch.int32, device="cuda")  # 4 // 4 = block 1: past the row
+    kv_ops.append(k_pool, v_pool, 0, k_new, -k_new, tables, positions=positions)
     assert k_pool[0, 1, :, 2].eq(1).all() and v_pool[0, 1, :, 2].eq(-1).all()
     assert k_pool.sum().item() == 16 and v_pool.sum().item() == -16
 
