@@ -281,61 +281,17 @@ def secondary_config5(torch):
     return res
 
 
-def secondary_e2e(torch, rounds=3, new_tokens=64):
-    """BASELINE config 1 on the GPU: per-token greedy decode latency of the
-    contiguous, paged-gather and paged-direct systems in interleaved rounds
-    (reference benchmarks/ab_compare.py:49-144), prompt excluded."""
-    from moe_engine.model import Model, ModelConfig
+def secondary_e2e(torch, rounds=5, new_tokens=64):
+    """BASELINE config 1 on the GPU (random init from seed 0, fp32, block 16,
+    32-token prompt): per-token greedy decode latency of the contiguous,
+    paged-gather and paged-direct systems in interleaved rounds with a paired
+    Student-t interval (moe_engine.harness.ab_compare)."""
+    from moe_engine import harness
 
-    torch.manual_seed(0)
-    cfg = ModelConfig(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
-                      num_experts=8, top_k=2, ffn_dim=2048)
-    model = Model(cfg).to("cuda").eval()
-    prompt = torch.randint(0, cfg.vocab_size, (1, 32), generator=torch.Generator().manual_seed(0)).cuda()
-    systems = ["contiguous", "paged-gather", "paged-direct"]
-
-    def run(system):
-        cache = model.new_cache() if system == "contiguous" else model.new_block_allocator(
-            num_blocks=64, block_size=16, attention_mode=system[6:]).new_cache()
-        steps, tokens = [], []
-        with torch.no_grad():
-            logits = model(prompt, cache)
-            nxt = logits[:, -1].argmax(-1, keepdim=True)
-            for _ in range(new_tokens):
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                logits = model(nxt, cache)
-                nxt = logits[:, -1].argmax(-1, keepdim=True)
-                torch.cuda.synchronize()
-                steps.append(time.perf_counter() - t0)
-                tokens.append(int(nxt))
-        if system != "contiguous":
-            cache.free()
-        return steps, tokens
-
-    for s in systems:
-        run(s)  # warm-up
-    per = {s: [] for s in systems}
-    toks = {}
-    for r in range(rounds):
-        order = systems[r % 3 :] + systems[: r % 3]
-        for s in order:
-            steps, tokens = run(s)
-            per[s].append(steps)
-            toks[s] = tokens
-    out = {}
-    for s in systems:
-        pooled = sorted(t for steps in per[s] for t in steps)
-        out[s] = {"median_ms": round(pooled[len(pooled) // 2] * 1e3, 3),
-                  "mean_ms": round(sum(pooled) / len(pooled) * 1e3, 3)}
-    deltas = [
-        (sum(d) / len(d) - sum(c) / len(c)) * 1e3 for d, c in zip(per["paged-direct"], per["contiguous"])
-    ]
-    out["direct_minus_contiguous_mean_ms"] = round(sum(deltas) / len(deltas), 3)
-    out["tokens_identical"] = toks["paged-direct"] == toks["contiguous"] == toks["paged-gather"]
-    out["rounds"] = rounds
-    out["new_tokens"] = new_tokens
-    return out
+    model = harness.make_model(harness.CONFIG1, seed=0, device="cuda")
+    gen = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, harness.CONFIG1["vocab_size"], (32,), generator=gen).cuda()
+    return harness.ab_compare(model, prompt, rounds=rounds, new_tokens=new_tokens)
 
 
 def main():

@@ -118,8 +118,13 @@ def is_rocm_device(t: torch.Tensor) -> bool:
     return t.is_cuda and torch.version.hip is not None
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Raw hipStream_t of the current torch stream on `t`'s device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

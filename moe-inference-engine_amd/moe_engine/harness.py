@@ -1,0 +1,242 @@
+"""Latency harnesses for the paged decode path (random-init miniMoE models).
+
+Counterparts of the reference's benchmarks, with random-init weights because
+the real checkpoint and tokenizer are not available here:
+
+  attention_micro  one layer's decode attention, us per call, for contiguous
+                   read + SDPA, paged gather + SDPA and paged direct
+                   (benchmarks/attention_micro.py:27-85)
+  context_sweep    decode step latency against context length per system
+                   (benchmarks/context_sweep.py:50-113)
+  ab_compare       interleaved rounds of every system with a rotating start,
+                   paired per-round deltas and a Student-t 95 % interval
+                   (benchmarks/ab_compare.py:49-198)
+
+System names are the reference's: "contiguous", "paged-gather",
+"paged-direct".  Run as a module for a JSON report:
+
+    python -m moe_engine.harness ab --rounds 5 --new-tokens 64
+"""
+
+import argparse
+import json
+import math
+import statistics
+import time
+
+import torch
+import torch.nn.functional as F
+
+from moe_engine import paged_attention
+from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig
+
+SYSTEMS = ("contiguous", "paged-gather", "paged-direct")
+
+# the miniMoE-shaped decoder.
+CONFIG1 = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
+               num_experts=8, top_k=2, ffn_dim=2048)
+
+
+def sync(device) -> None:
+    if torch.device(device).type == "cuda":
+        torch.cuda.synchronize()
+
+
+def time_calls(fn, sync_fn, iters=200, warmup=20) -> float:
+    """Average microseconds per call over back-to-back calls (no per-call sync)."""
+    for _ in range(warmup):
+        fn()
+    sync_fn()
+    start = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    sync_fn()
+    return (time.perf_counter() - start) / iters * 1e6
+
+
+def make_model(config=None, seed=0, device="cuda", dtype=torch.float32):
+    torch.manual_seed(seed)
+    return Model(ModelConfig(**(config or CONFIG1))).to(device, dtype).eval()
+
+
+def make_cache(model, system, block_size=16):
+    """A fresh cache for `system`; paged pools hold one max-length sequence
+    (scripts/serve.py:147-155)."""
+    if system == "contiguous":
+        return model.new_cache()
+    num_blocks = -(-model.max_seq_length // block_size)
+    return model.new_block_allocator(num_blocks, block_size, attention_mode=system[len("paged-"):]).new_cache()
+
+
+def release(cache):
+    if hasattr(cache, "free"):
+        cache.free()
+
+
+def attention_micro(config=None, contexts=(16, 64, 256, 1024), device="cuda", dtype=torch.float32, iters=200):
+    """One layer's decode attention in isolation, us per call."""
+    cfg = ModelConfig(**(config or CONFIG1))
+    max_ctx = cfg.max_seq_length
+    contiguous = KVCache(cfg, 1, device, dtype)
+    allocator = BlockAllocator(cfg, max_ctx // 16, 16, device, dtype)
+    paged = allocator.new_cache()
+    torch.manual_seed(0)
+    shape = (1, cfg.num_heads, max_ctx, cfg.head_dim)
+    k = torch.randn(shape, device=device, dtype=dtype)
+    v = torch.randn(shape, device=device, dtype=dtype)
+    contiguous.write(0, 0, k, v)
+    paged.write(0, 0, k, v)
+    q = torch.randn(1, cfg.num_heads, 1, cfg.head_dim, device=device, dtype=dtype)
+    s = lambda: sync(device)  # noqa: E731
+    results = {}
+    for ctx in contexts:
+        row = {
+            "contiguous_read_sdpa_us": time_calls(lambda: F.scaled_dot_product_attention(q, *contiguous.read(0, ctx)), s, iters),
+            "paged_gather_sdpa_us": time_calls(lambda: F.scaled_dot_product_attention(q, *paged.read(0, ctx)), s, iters),
+        }
+        if paged_attention.is_supported(q, cfg.head_dim):
+            row["paged_direct_kernel_us"] = time_calls(lambda: paged_attention.decode(q, paged, 0, ctx), s, iters)
+        results[ctx] = {key: round(val, 2) for key, val in row.items()}
+    return results
+
+
+def run_round(model, cache, prompt_ids, new_tokens):
+    """One prefill and `new_tokens` greedy decode steps; returns
+    (prefill seconds, per-step seconds, generated tokens)."""
+    device = prompt_ids.device
+    tokens = []
+    with torch.no_grad():
+        sync(device)
+        start = time.perf_counter()
+        logits = model(prompt_ids.unsqueeze(0), cache)
+        sync(device)
+        prefill_s = time.perf_counter() - start
+        step_input = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+        steps = []
+        for _ in range(new_tokens):
+            sync(device)
+            start = time.perf_counter()
+            logits = model(step_input, cache)
+            step_input = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+            sync(device)
+            steps.append(time.perf_counter() - start)
+            tokens.append(int(step_input))
+    return prefill_s, steps, tokens
+
+
+def paired_t_summary(deltas):
+    """Mean and two-sided 95 % Student-t interval of paired per-round deltas (ms)."""
+    n = len(deltas)
+    mean = sum(deltas) / n
+    if n < 2:
+        return {"per_round_delta_ms": deltas, "mean_delta_ms": round(mean, 4), "ci95_ms": None}
+    from scipy.stats import t as student_t
+
+    half = student_t.ppf(0.975, n - 1) * math.sqrt(statistics.variance(deltas) / n)
+    return {
+        "per_round_delta_ms": [round(d, 4) for d in deltas],
+        "mean_delta_ms": round(mean, 4),
+        "ci95_ms": [round(mean - half, 4), round(mean + half, 4)],
+    }
+
+
+def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, block_size=16):
+    """Interleaved rounds of every system, rotating which starts each round."""
+    systems = list(systems)
+
+    def run(system):
+        cache = make_cache(model, system, block_size)
+        try:
+            return run_round(model, cache, prompt_ids, new_tokens)
+        finally:
+            release(cache)
+
+    for system in systems:  # warm-up outside the timed rounds
+        run(system)
+    results = {s: {"prefill_s": [], "rounds": [], "tokens": None} for s in systems}
+    for r in range(rounds):
+        order = systems[r % len(systems):] + systems[: r % len(systems)]
+        for system in order:
+            prefill_s, steps, tokens = run(system)
+            results[system]["prefill_s"].append(prefill_s)
+            results[system]["rounds"].append(steps)
+            results[system]["tokens"] = tokens
+    summary = {}
+    for system in systems:
+        pooled = sorted(t for steps in results[system]["rounds"] for t in steps)
+        summary[system] = {
+            "prefill_ms": round(statistics.median(results[system]["prefill_s"]) * 1e3, 3),
+            "decode_median_ms": round(pooled[len(pooled) // 2] * 1e3, 3),
+            "decode_mean_ms": round(sum(pooled) / len(pooled) * 1e3, 3),
+            "decode_p90_ms": round(pooled[int(len(pooled) * 0.9)] * 1e3, 3),
+            "decode_tok_per_sec": round(len(pooled) / sum(pooled), 2),
+        }
+
+    def mean_steps_ms(system):
+        return [sum(steps) / len(steps) * 1e3 for steps in results[system]["rounds"]]
+
+    paired = {}
+    for a, b in (("paged-direct", "contiguous"), ("paged-direct", "paged-gather"), ("paged-gather", "contiguous")):
+        if a in systems and b in systems:
+            paired[f"{a}_minus_{b}"] = paired_t_summary([x - y for x, y in zip(mean_steps_ms(a), mean_steps_ms(b))])
+    tokens = [results[s]["tokens"] for s in systems]
+    return {
+        "summary": summary,
+        "paired_deltas": paired,
+        "tokens_identical": all(t == tokens[0] for t in tokens),
+        "rounds": rounds,
+        "new_tokens": new_tokens,
+        "prompt_tokens": int(prompt_ids.numel()),
+    }
+
+
+def context_sweep(model, contexts=(16, 64, 256, 1024), systems=SYSTEMS, steps=16, block_size=16, filler=0):
+    """Median decode-step latency (ms) at roughly each context length."""
+    device = model.token_embedding.weight.device
+    report = {s: {} for s in systems}
+    for ctx in contexts:
+        for system in systems:
+            prefill = max(1, ctx - steps)
+            cache = make_cache(model, system, block_size)
+            prompt = torch.full((1, prefill), filler, device=device, dtype=torch.long)
+            step = torch.full((1, 1), filler, device=device, dtype=torch.long)
+            times = []
+            with torch.no_grad():
+                model(prompt, cache)
+                for _ in range(min(steps, model.max_seq_length - prefill)):
+                    sync(device)
+                    start = time.perf_counter()
+                    model(step, cache)
+                    sync(device)
+                    times.append(time.perf_counter() - start)
+            release(cache)
+            report[system][ctx] = round(statistics.median(times) * 1e3, 3)
+    return report
+
+
+def main(argv=None):
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("mode", choices=["ab", "micro", "sweep"])
+    parser.add_argument("--rounds", type=int, default=5)
+    parser.add_argument("--new-tokens", type=int, default=64)
+    parser.add_argument("--prompt-tokens", type=int, default=32)
+    parser.add_argument("--contexts", default="16,64,256,1024")
+    parser.add_argument("--systems", default=",".join(SYSTEMS))
+    parser.add_argument("--device", default="cuda")
+    args = parser.parse_args(argv)
+    contexts = [int(c) for c in args.contexts.split(",")]
+    if args.mode == "micro":
+        report = attention_micro(contexts=contexts, device=args.device)
+    else:
+        model = make_model(device=args.device)
+        if args.mode == "ab":
+            gen = torch.Generator().manual_seed(0)
+            prompt = torch.randint(0, CONFIG1["vocab_size"], (args.prompt_tokens,), generator=gen).to(args.device)
+            report = ab_compare(model, prompt, args.systems.split(","), args.rounds, args.new_tokens)
+        else:
+            report = context_sweep(model, contexts, args.systems.split(","))
+    print(json.dumps(report, indent=2))
+
+
+if __name__ == "__main__":
+    main()

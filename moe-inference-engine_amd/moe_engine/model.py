@@ -114,6 +114,16 @@ class BlockAllocator:
         self.on_device = _native.is_rocm_device(self.k_pool)
         if self.on_device:
             _native.lib()
+        # Launch constants shared by every call on this pool (element strides
+        # inside one layer, dtype code); pointers are read per call.
+        self._launch = None
+        if self.on_device and dtype in _native.DTYPE_CODES:
+            self._launch = (
+                self.k_pool.stride(0) * self.k_pool.element_size(),  # layer stride, bytes
+                self.k_pool.stride(1),  # block stride, elements
+                self.k_pool.stride(2),  # head stride, elements
+                _native.DTYPE_CODES[dtype],
+            )
         self.free_blocks = list(range(num_blocks))
 
     def allocate(self) -> int:
@@ -184,6 +194,29 @@ class PagedKVCache:
         self._reserve(position + seq_len)
         alloc = self.allocator
         if alloc.on_device:
+            ks = k.stride()
+            if (
+                alloc._launch is not None
+                and ks == v.stride()
+                and ks[3] == 1
+                and k.dtype == alloc.k_pool.dtype
+                and k.shape[1] == alloc.num_heads
+                and k.shape[3] == alloc.head_dim
+                and k.device == alloc.k_pool.device
+                and 0 <= layer_idx < alloc.k_pool.shape[0]
+            ):
+                # Lean path for the engine's own calls: one C call, one launch.
+                layer_bytes, sblk, shead, code = alloc._launch
+                off = layer_idx * layer_bytes
+                rc = _native.lib().mie_kv_append(
+                    alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off, sblk, shead, alloc.num_blocks,
+                    k.data_ptr(), v.data_ptr(), ks[0], ks[1], ks[2],
+                    self.block_table_device.data_ptr(), 0, None, position,
+                    1, seq_len, alloc.num_heads, alloc.head_dim, alloc.block_size, code, _native.stream_of(k),
+                )
+                if rc:
+                    _native.check(rc, "mie_kv_append")
+                return
             kv_ops.append(alloc.k_pool, alloc.v_pool, layer_idx, k, v, self.block_table_device, position=position)
             return
         if seq_len == 1:

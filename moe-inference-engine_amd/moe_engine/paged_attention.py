@@ -147,6 +147,40 @@ def decode(q: torch.Tensor, cache, layer_idx: int, context_len: int) -> torch.Te
     """
     allocator = cache.allocator
     num_heads, head_dim = q.shape[1], q.shape[3]
+    launch = getattr(allocator, "_launch", None)
+    qs = q.stride()
+    if (
+        launch is not None
+        and qs[3] == 1
+        and q.dtype == allocator.k_pool.dtype
+        and q.shape == (1, allocator.num_heads, 1, allocator.head_dim)
+        and q.device == allocator.k_pool.device
+        and 0 <= layer_idx < allocator.k_pool.shape[0]
+        and 0 <= context_len <= allocator.num_blocks * allocator.block_size
+    ):
+        # Lean path for the engine's own calls: the launch constants are the
+        # allocator's, the plan is cached, one C call.
+        layer_bytes, sblk, shead, code = launch
+        part, ws_bytes = _native.decode_plan(
+            1, num_heads, head_dim, allocator.block_size, context_len, q.dtype, 0
+        )
+        out = torch.empty((1, num_heads, 1, head_dim), dtype=q.dtype, device=q.device)
+        ws = _workspace(ws_bytes, q.device)
+        off = layer_idx * layer_bytes
+        rc = _native.lib().mie_paged_decode(
+            q.data_ptr(), qs[0], qs[1],
+            allocator.k_pool.data_ptr() + off, allocator.v_pool.data_ptr() + off, sblk, shead, allocator.num_blocks,
+            cache.block_table_device.data_ptr(), 0,
+            None, context_len, context_len,
+            1, num_heads, head_dim, allocator.block_size,
+            1.0 / math.sqrt(head_dim),
+            out.data_ptr(), num_heads * head_dim, head_dim, code,
+            _native.ptr(ws), ws_bytes, 0,
+            code, _native.stream_of(q),
+        )
+        if rc:
+            _native.check(rc, "mie_paged_decode")
+        return out
     out = decode_layer(
         q[:, :, 0],
         allocator.k_pool[layer_idx],
