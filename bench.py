@@ -106,7 +106,7 @@ def run_config4(torch, args):
     def attend():
         paged_attention.decode_batched(
             w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
-            out=out, partition_tokens=args.partition_tokens,
+            out=out, partition_tokens=args.partition_tokens, context_lens_host=w.lens,
         )
 
     for _ in range(args.warmup):
@@ -271,7 +271,9 @@ def secondary_config5(torch):
         nbytes = workloads.attention_bytes(w.lens, 12, 64, 32, 2)
         us = timed_us(
             torch,
-            lambda: paged_attention.decode_batched(w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len),
+            lambda: paged_attention.decode_batched(
+                w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, context_lens_host=w.lens
+            ),
             iters=20,
         )
         res[f"b{batch}_c131072_us"] = round(us, 2)

@@ -62,7 +62,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 2
+#define MIE_ABI_VERSION 3
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -122,6 +122,10 @@ int32_t mie_kv_gather(const void* k_pool, const void* v_pool, int64_t pool_strid
  * with ctx_len(b) = min(ctx_lens[b], max_ctx_len) if `ctx_lens` is non-NULL
  * (device int32[batch]) else `ctx_len` for every sequence; ctx_len(b) == 0
  * writes zeros (what scaled_dot_product_attention returns for no keys).
+ * `ctx_lens_host` (optional, host int32[batch]) is a host copy of the same
+ * lengths: with it the launch holds exactly the batch's work items, without it
+ * the launch is sized for max_ctx_len and the surplus workgroups exit.  When
+ * given, its work-item count must not be below that of ctx_lens.
  * q, K and V share `dtype` (F32 or BF16); `out_dtype` is F32 or `dtype`.
  * Accumulation is fp32 throughout.
  *
@@ -139,6 +143,7 @@ int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          int64_t pool_stride_block, int64_t pool_stride_head,
                          int32_t num_blocks, const int32_t* block_tables,
                          int64_t block_table_stride, const int32_t* ctx_lens,
+                         const int32_t* ctx_lens_host,
                          int32_t ctx_len, int32_t max_ctx_len, int32_t batch,
                          int32_t num_heads, int32_t head_dim, int32_t block_size,
                          float scale, void* out, int64_t out_stride_b,

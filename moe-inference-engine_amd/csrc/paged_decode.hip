@@ -7,10 +7,13 @@
 // Work decomposition.  One 64-lane wavefront owns one (sequence, head,
 // partition) work item; a workgroup holds WAVES heads of the same sequence and
 // partition, so its waves walk the same block-table entries and neighbouring
-// (block, head) tiles.  grid = (partitions, ceil(H / WAVES), batch); work items
-// past a sequence's last partition exit at once, so ragged batches need no
-// host-side work list and no device-to-host read of the lengths.  Partitions
-// are short (about 128-512 tokens) so the hardware dispatcher keeps refilling
+// (block, head) tiles.  For batches up to kFlatMaxBatch the workgroups form a
+// flat list of exactly the batch's work items (each maps its index with a
+// prefix scan over the sequence lengths on the device), sized exactly when the
+// caller passes a host copy of the lengths - a grid padded to the longest
+// sequence spends ~18 % of a ragged batch's time on workgroups that only exit.
+// Larger batches use grid = (partitions, ceil(H / WAVES), batch).  Partitions
+// are short (a few hundred tokens) so the hardware dispatcher keeps refilling
 // CUs with fresh work items and the kernel ends without a long tail.
 //
 // Lane layout.  A token's head_dim row is split into NV slices of VEC elements
@@ -49,14 +52,21 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kWaves = 4;            // heads (wavefronts) per workgroup
 constexpr int kWindow = 64;          // FAST path: block ids held one per lane
 // Automatic partition size: the smallest power of two (>= the tile) that keeps
-// the grid at or below kTargetItems wavefronts AND every sequence at or below
-// kMaxParts partitions.  The first bound keeps partitions short enough for the
-// dispatcher to balance; the second bounds the merge work per (sequence, head).
-// Fitted on MI355X: config 4 (64 x U[512, 8192]) is fastest at 128 tokens,
-// 8 x 131072 at 512-1024, 1 x 131072 at 512.
+// B * H * ceil(max_ctx / P) at or below kTargetItems wavefronts AND every
+// sequence at or below kMaxParts partitions.  The first bound keeps enough
+// short work items for the dispatcher to balance; the second bounds the merge
+// work per (sequence, head).  Fitted on MI355X with the flat work list:
+// config 4 (64 x U[512, 8192]) and 64 x 4352 are fastest at 512 tokens,
+// 8 x 131072 at 1024, 1 x 131072 at 512.
 constexpr int kSinglePassCtx = 256;  // auto plan: one partition up to this context
-constexpr int kTargetItems = 49152;  // auto plan: grid wavefronts to stay below
+constexpr int kTargetItems = 12288;  // auto plan: wavefronts to stay below
 constexpr int kMaxParts = 256;       // auto plan: partitions per sequence to stay below
+// Occupancy floor for the main kernels: every built shape fits 4 waves/SIMD
+// (<= 128 VGPRs) without spills; at 3 waves/SIMD config 4 runs ~8 % slower.
+constexpr int kMinWaves = 4;
+// Batches up to this size use the flat work list (its per-workgroup scan reads
+// ceil(B / 64) chunks of lengths); larger batches use the grid form.
+constexpr int kFlatMaxBatch = 512;
 
 constexpr int next_pow2(int x) {
   int p = 1;
@@ -361,10 +371,11 @@ __device__ __forceinline__ void zero_item(const DecodeArgs& a, int b, int h, int
   store_out<DT, G::VEC>(a.out, b * a.o_sb + h * a.o_sh + jl * G::VEC, zero, a.out_f32);
 }
 
-// grid = (max partitions, ceil(H / WAVES), batch); items past a sequence's
-// last partition exit.
+// Grid form: grid = (max partitions, ceil(H / WAVES), batch); workgroups past
+// a sequence's last partition exit.  Used for batches above kFlatMaxBatch.
 template <int DT, int D, bool FAST>
-__global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
+void paged_decode_grid_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int h = blockIdx.y * kWaves + wave;
@@ -378,6 +389,54 @@ __global__ __launch_bounds__(64 * kWaves) void paged_decode_kernel(DecodeArgs a)
   }
   if (part >= (ctx + (1 << a.part_shift) - 1) >> a.part_shift) return;
   decode_item<DT, D, FAST>(a, b, h, part, ctx, lane);
+}
+
+// Flat form: blockIdx.x enumerates the batch's real work items, sequence by
+// sequence, head group by head group, partition fastest; a sequence with
+// ctx == 0 has one item per head group (it writes zeros).  Each wave maps its
+// item with a 64-lane inclusive prefix scan of the per-sequence item counts,
+// 64 sequences per step, so no workgroup exists for a partition past a
+// sequence's end.  When the launch is an upper bound rather than the exact
+// count, the surplus workgroups find no item and exit.
+template <int DT, int D, bool FAST>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
+void paged_decode_flat_kernel(DecodeArgs a, int batch, int head_groups) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int item = blockIdx.x;
+  const int shift = a.part_shift;
+  int base = 0;  // items of the sequences before this chunk
+  for (int c0 = 0; c0 < batch; c0 += 64) {
+    const int bb = c0 + lane;
+    const int ctx = bb < batch ? seq_ctx(a, bb) : 0;
+    const int parts = max(1, (ctx + (1 << shift) - 1) >> shift);
+    const int n = bb < batch ? parts * head_groups : 0;
+    int incl = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(incl, off);
+      if (lane >= off) incl += y;
+    }
+    const int chunk_items = __shfl(incl, 63);
+    if (item < base + chunk_items) {
+      const int owner = __ffsll(static_cast<unsigned long long>(__ballot(incl > item - base))) - 1;
+      const int local = item - base - (__shfl(incl, owner) - __shfl(n, owner));
+      const int seq_parts = __shfl(parts, owner);
+      const int hg = local / seq_parts;
+      const int part = local - hg * seq_parts;
+      const int h = hg * kWaves + wave;
+      if (h >= a.H) return;
+      const int b = c0 + owner;
+      const int seq_ctx_len = __shfl(ctx, owner);
+      if (seq_ctx_len == 0) {
+        zero_item<DT, D>(a, b, h, lane);
+        return;
+      }
+      decode_item<DT, D, FAST>(a, b, h, part, seq_ctx_len, lane);
+      return;
+    }
+    base += chunk_items;
+  }
 }
 
 // Merge the partition partials of one (sequence, head) in one pass:
@@ -534,13 +593,24 @@ int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_s
   return MIE_OK;
 }
 
+// flat_items > 0: the flat work list with that many workgroups; 0: the grid form.
 template <int DT, int D>
-int32_t launch(DecodeArgs& a, int batch, bool fast, hipStream_t st) {
-  const dim3 grid(a.max_parts, (a.H + kWaves - 1) / kWaves, batch);
-  if (fast) {
-    paged_decode_kernel<DT, D, true><<<grid, 64 * kWaves, 0, st>>>(a);
+int32_t launch(DecodeArgs& a, int batch, bool fast, int64_t flat_items, hipStream_t st) {
+  const int head_groups = (a.H + kWaves - 1) / kWaves;
+  if (flat_items > 0) {
+    const dim3 grid(static_cast<uint32_t>(flat_items));
+    if (fast) {
+      paged_decode_flat_kernel<DT, D, true><<<grid, 64 * kWaves, 0, st>>>(a, batch, head_groups);
+    } else {
+      paged_decode_flat_kernel<DT, D, false><<<grid, 64 * kWaves, 0, st>>>(a, batch, head_groups);
+    }
   } else {
-    paged_decode_kernel<DT, D, false><<<grid, 64 * kWaves, 0, st>>>(a);
+    const dim3 grid(a.max_parts, head_groups, batch);
+    if (fast) {
+      paged_decode_grid_kernel<DT, D, true><<<grid, 64 * kWaves, 0, st>>>(a);
+    } else {
+      paged_decode_grid_kernel<DT, D, false><<<grid, 64 * kWaves, 0, st>>>(a);
+    }
   }
   int32_t rc = mie::check_launch("paged_decode_kernel");
   if (rc != MIE_OK || a.max_parts <= 1) return rc;
@@ -548,11 +618,12 @@ int32_t launch(DecodeArgs& a, int batch, bool fast, hipStream_t st) {
   return mie::check_launch("paged_decode_reduce_kernel");
 }
 
-int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, hipStream_t st) {
-#define MIE_LAUNCH_CASE(DD)                                                             \
-  case DD:                                                                              \
-    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, st)       \
-                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, st);
+int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, int64_t flat_items,
+                 hipStream_t st) {
+#define MIE_LAUNCH_CASE(DD)                                                                     \
+  case DD:                                                                                      \
+    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, flat_items, st)   \
+                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, flat_items, st);
   switch (head_dim) {
     MIE_FOR_EACH_HEAD_DIM(MIE_LAUNCH_CASE)
     default: return mie::fail(MIE_ERR_UNSUPPORTED, "mie_paged_decode: head_dim %d not built", head_dim);
@@ -584,7 +655,8 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
                                     const void* k_pool, const void* v_pool, int64_t pool_stride_block,
                                     int64_t pool_stride_head, int32_t num_blocks,
                                     const int32_t* block_tables, int64_t block_table_stride,
-                                    const int32_t* ctx_lens, int32_t ctx_len, int32_t max_ctx_len,
+                                    const int32_t* ctx_lens, const int32_t* ctx_lens_host,
+                                    int32_t ctx_len, int32_t max_ctx_len,
                                     int32_t batch, int32_t num_heads, int32_t head_dim,
                                     int32_t block_size, float scale, void* out, int64_t out_stride_b,
                                     int64_t out_stride_h, int32_t out_dtype, void* workspace,
@@ -658,5 +730,24 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
     a.ws_acc = nullptr;
     a.ws_ml = nullptr;
   }
-  return dispatch(dtype, head_dim, a, batch, p.fast, static_cast<hipStream_t>(stream));
+  // Work items for the flat form: exact when the lengths are known on the host
+  // (a host copy, or one scalar length), otherwise the grid's upper bound.
+  int64_t flat_items = 0;
+  if (batch <= kFlatMaxBatch) {
+    const int64_t head_groups = (num_heads + kWaves - 1) / kWaves;
+    auto items_of = [&](int64_t c) {
+      c = c < 0 ? 0 : (c > max_ctx_len ? max_ctx_len : c);
+      const int64_t parts = (c + p.part - 1) / p.part;
+      return (parts > 0 ? parts : 1) * head_groups;
+    };
+    if (!ctx_lens) {
+      flat_items = batch * items_of(ctx_len);
+    } else if (ctx_lens_host) {
+      for (int b = 0; b < batch; ++b) flat_items += items_of(ctx_lens_host[b]);
+    } else {
+      flat_items = static_cast<int64_t>(batch) * p.max_parts * head_groups;
+    }
+    if (flat_items > 0x7fffffff) flat_items = 0;  // beyond a 1-D grid: use the grid form
+  }
+  return dispatch(dtype, head_dim, a, batch, p.fast, flat_items, static_cast<hipStream_t>(stream));
 }

@@ -18,6 +18,7 @@ context_len is a host int, as in the reference (paged_attention.py:116-118):
 the single-sequence path never reads a device value.
 """
 
+import ctypes
 import math
 
 import torch
@@ -59,12 +60,15 @@ def decode_layer(
     out: torch.Tensor = None,
     out_dtype: torch.dtype = None,
     partition_tokens: int = 0,
+    context_lens_host=None,
 ) -> torch.Tensor:
     """Decode attention for q [B, H, D] over one layer's pools [NB, H, BS, D].
 
     Either `context_len` (one host int for every sequence) or `context_lens`
     (int32 device [B]) with `max_context_len` (a host upper bound that sizes the
-    launch).  block_tables is int32 [B, max_blocks], or 1-D when B == 1.
+    launch).  `context_lens_host`, a host sequence of the same lengths, lets
+    the launch hold exactly the batch's work items (no idle workgroups on
+    ragged batches).  block_tables is int32 [B, max_blocks], or 1-D when B == 1.
     Returns out [B, H, D] in `out_dtype` (q's dtype or float32).
     """
     lib = _native.lib()
@@ -96,6 +100,7 @@ def decode_layer(
         if block_tables.shape[0] != batch or block_tables.stride(1) != 1:
             raise ValueError("block tables must be [batch, max_blocks] with unit inner stride")
         bt_stride = block_tables.stride(0)
+    host_lens = None
     if context_lens is None:
         if context_len is None:
             raise ValueError("pass context_len or context_lens")
@@ -109,6 +114,10 @@ def decode_layer(
         context_lens = context_lens.contiguous()
         ctx_ptr = context_lens.data_ptr()
         context_len = 0
+        if context_lens_host is not None:
+            if len(context_lens_host) != batch:
+                raise ValueError("context_lens_host must hold one length per sequence")
+            host_lens = (ctypes.c_int32 * batch)(*(int(c) for c in context_lens_host))
     if out_dtype is None:
         out_dtype = q.dtype if out is None else out.dtype
     if out is None:
@@ -126,7 +135,7 @@ def decode_layer(
             q.data_ptr(), q.stride(0), q.stride(1),
             k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), nb,
             block_tables.data_ptr(), bt_stride,
-            ctx_ptr, int(context_len), int(max_context_len),
+            ctx_ptr, host_lens, int(context_len), int(max_context_len),
             batch, heads, head_dim, block_size,
             float(scale),
             out.data_ptr(), out.stride(0), out.stride(1), _native.dtype_code(out.dtype),
@@ -171,7 +180,7 @@ def decode(q: torch.Tensor, cache, layer_idx: int, context_len: int) -> torch.Te
             q.data_ptr(), qs[0], qs[1],
             allocator.k_pool.data_ptr() + off, allocator.v_pool.data_ptr() + off, sblk, shead, allocator.num_blocks,
             cache.block_table_device.data_ptr(), 0,
-            None, context_len, context_len,
+            None, None, context_len, context_len,
             1, num_heads, head_dim, allocator.block_size,
             1.0 / math.sqrt(head_dim),
             out.data_ptr(), num_heads * head_dim, head_dim, code,

@@ -72,6 +72,6 @@ def test_invalid_arguments_fail_before_launch():
     rc = lib.mie_kv_gather(0, 0, 64, 64, 1, 0, 5, 0, 0, 0, 0, 1, 4, 16, 0, 0)
     assert rc == 1 and b"null pointer" in lib.mie_last_error()
     rc = lib.mie_paged_decode(
-        0, 0, 0, 0, 0, 0, 0, 1, 0, 0, 0, 10, 5, 1, 1, 64, 16, 1.0, 0, 0, 0, 0, 0, 0, 0, 1, 0
+        0, 0, 0, 0, 0, 0, 0, 1, 0, 0, 0, None, 10, 5, 1, 1, 64, 16, 1.0, 0, 0, 0, 0, 0, 0, 0, 1, 0
     )
     assert rc == 1 and b"ctx_len" in lib.mie_last_error()

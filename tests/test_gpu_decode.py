@@ -112,6 +112,9 @@ def test_kernel_matches_oracle_on_every_layer():
 
 
 def check_workload(w, out_f32_atol=2e-3, partition_tokens=0, batches=None):
+    """float32 output from a launch sized by max_context_len (surplus
+    workgroups exit), then output in the input dtype from a launch sized
+    exactly from host lengths; both against the float64 oracle."""
     want = oracle_outputs(w, batches)
     sel = slice(None) if batches is None else list(batches)
     dt = w.q.dtype
@@ -120,12 +123,14 @@ def check_workload(w, out_f32_atol=2e-3, partition_tokens=0, batches=None):
         out_dtype=torch.float32, partition_tokens=partition_tokens,
     )
     np.testing.assert_allclose(got32.cpu().numpy()[sel], want, rtol=0, atol=out_f32_atol)
-    if dt != torch.float32:
-        got = paged_attention.decode_batched(
-            w.q, w.k_pool, w.v_pool, w.layer, w.block_tables, w.context_lens, w.max_len,
-            partition_tokens=partition_tokens,
-        )
-        assert got.dtype == dt
+    got = paged_attention.decode_batched(
+        w.q, w.k_pool, w.v_pool, w.layer, w.block_tables, w.context_lens, w.max_len,
+        partition_tokens=partition_tokens, context_lens_host=w.lens,
+    )
+    assert got.dtype == dt
+    if dt == torch.float32:
+        np.testing.assert_allclose(got.cpu().numpy()[sel], want, rtol=0, atol=out_f32_atol)
+    else:
         assert bf16_close(got.float().cpu().numpy()[sel], want)
     return got32
 
