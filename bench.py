@@ -249,14 +249,23 @@ def secondary_config3(torch):
     outv = torch.empty_like(outk)
     append_us = timed_us(torch, lambda: [kv_ops.append(k_pool, v_pool, l, new, new, table, position=C - 1) for l in range(L)]) / L
     gather_us = timed_us(torch, lambda: [kv_ops.gather(k_pool, v_pool, l, table, C, outk, outv) for l in range(L)], iters=20) / L
+    # Prefill scatter: the whole context written through the table in one launch per layer.
+    prefill = torch.randn(1, H, C, D, device="cuda").to(torch.bfloat16)
+    prefill_us = timed_us(
+        torch, lambda: [kv_ops.append(k_pool, v_pool, l, prefill, prefill, table, position=0) for l in range(L)], iters=20
+    ) / L
     gb = workloads.gather_bytes(C, H, D, 2)
+    pb = workloads.append_bytes(C, H, D, 2)  # C tokens, K and V read and written
     del k_pool, v_pool
     torch.cuda.empty_cache()
     return {
         "append_us_per_layer": round(append_us, 2),
+        "append_note": "one token per layer through the full-validation wrapper: host-bound (kernel ~4 us in the rocprof trace)",
         "gather_us_per_layer": round(gather_us, 2),
         "gather_gbs": round(gb / gather_us / 1e3, 1),
         "gather_bytes_per_layer": gb,
+        "prefill_scatter_us_per_layer": round(prefill_us, 2),
+        "prefill_scatter_gbs": round(pb / prefill_us / 1e3, 1),
         "context": C,
     }
 

@@ -166,6 +166,33 @@ int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32_t head_dim
 /* 1 if mie_paged_decode is built for (head_dim, dtype), else 0. */
 int32_t mie_paged_decode_supported(int32_t head_dim, int32_t dtype);
 
+/*
+ * Fused top-k mixture of experts for ONE decode token, float32, with no
+ * device-to-host synchronisation.  Replaces MoEFeedForward's PyTorch path for
+ * a single token (model.py:443-461; its torch.where syncs once per expert) and
+ * the reference's Triton fused MoE decode (fused_moe.py:274-380):
+ *
+ *   logits = router_weight[E, dim] . x;  ids = top_k experts by logit (lower id
+ *   on ties);  w = softmax(logits[ids]);
+ *   out = sum over ids in increasing id, starting from 0, of
+ *         w_e * (w2[e] . GELU(w1[e] . x + b1[e]) + b2[e])
+ *
+ * with GELU the exact erf form, w1[e] [hidden, dim], b1[e] [hidden], w2[e]
+ * [dim, hidden], b2[e] [dim], all contiguous.  w1, b1, w2, b2 are HOST arrays of
+ * num_experts device pointers (num_experts <= 64, top_k <= 8); x, the weight
+ * matrices and `workspace` are 16-byte aligned; dim and hidden are multiples
+ * of 4.  `workspace` holds mie_moe_decode_workspace_bytes(top_k, hidden)
+ * bytes; nothing in it needs clearing.  Three launches on `stream`.
+ */
+int32_t mie_moe_decode(const void* x, const void* router_weight, const void* const* w1,
+                       const void* const* b1, const void* const* w2, const void* const* b2,
+                       int32_t num_experts, int32_t top_k, int32_t dim, int32_t hidden,
+                       void* out, void* workspace, int64_t workspace_bytes, int32_t dtype,
+                       void* stream);
+
+/* Workspace bytes mie_moe_decode needs (0 for invalid arguments). */
+int64_t mie_moe_decode_workspace_bytes(int32_t top_k, int32_t hidden);
+
 #ifdef __cplusplus
 }
 #endif

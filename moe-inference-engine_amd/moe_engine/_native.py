@@ -69,6 +69,14 @@ _SIGNATURES = {
         [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     ),
     "mie_paged_decode_supported": (_i32, [_i32, _i32]),
+    "mie_moe_decode": (
+        _i32,
+        [_c_void_p, _c_void_p,  # x, router weight
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # host arrays of w1, b1, w2, b2 pointers
+         _i32, _i32, _i32, _i32,  # experts, top_k, dim, hidden
+         _c_void_p, _c_void_p, _i64, _i32, _c_void_p],  # out, workspace, bytes, dtype, stream
+    ),
+    "mie_moe_decode_workspace_bytes": (_i64, [_i32, _i32]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

@@ -19,6 +19,7 @@ attention out_proj, in_proj xavier, the experts' two linears each, router), so
 a seeded model has the reference's weights.
 """
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -307,12 +308,14 @@ class Expert(nn.Module):
 
 
 class MoEFeedForward(nn.Module):
-    """Top-k mixture of experts, the reference's PyTorch path (model.py:443-461).
+    """Top-k mixture of experts (model.py:285-481).
 
-    The reference's fused Triton MoE decode ("direct") is outside this build's
-    paged-KV scope: mode 'direct' is accepted for interface compatibility and
-    rejected by the decode preflight before any cache mutation, as the
-    reference does when its kernel cannot run (model.py:408-432).
+    Prefill, and decode in mode 'reference', run the reference's PyTorch path
+    (model.py:443-461).  One-token decode in mode 'auto' or 'direct' runs the
+    fused HIP kernels (mie_moe_decode) where they apply: a ROCm device, the HIP
+    library, float32, one token.  'auto' falls back to the PyTorch path
+    elsewhere; a forced 'direct' that cannot run raises before any cache
+    mutation, through the model's decode preflight (model.py:408-441).
     """
 
     def __init__(self, dim, hidden_dim, num_experts, top_k, mode="auto"):
@@ -326,27 +329,57 @@ class MoEFeedForward(nn.Module):
         self.num_experts = num_experts
         self.experts = nn.ModuleList(Expert(dim, hidden_dim) for _ in range(num_experts))
         self.router = nn.Linear(dim, num_experts, bias=False)
+        # Fixed decode workspace (selected ids, weights, hidden activations);
+        # non-persistent, so checkpoints and state-dict keys are unchanged.
+        self.register_buffer(
+            "_direct_workspace", torch.empty(256 + top_k * hidden_dim * 4, dtype=torch.uint8), persistent=False
+        )
 
     def set_mode(self, mode: str) -> None:
         if mode not in MOE_MODES:
             raise ValueError(f"unknown MoE mode {mode!r}")
         self.mode = mode
 
+    def _configuration_supported(self, device, dtype, batch_size) -> bool:
+        return (
+            _native.HAS_HIP
+            and device.type == "cuda"
+            and torch.version.hip is not None
+            and dtype == torch.float32
+            and batch_size == 1
+            and 0 < self.top_k <= min(8, self.num_experts)
+            and self.num_experts <= 64
+            and self.dim % 4 == 0
+            and self.hidden_dim % 4 == 0
+        )
+
+    def _direct_supported(self, x: torch.Tensor) -> bool:
+        return x.shape[0] * x.shape[1] == 1 and self._configuration_supported(x.device, x.dtype, 1)
+
     @staticmethod
     def _raise_direct_unsupported() -> None:
         raise RuntimeError(
-            "MoE mode 'direct' needs a fused MoE decode kernel, which this build does not "
-            "provide; use 'auto' or 'reference' for the PyTorch path"
+            "MoE mode 'direct' needs one-token batch-one float32 decode on a ROCm device with the HIP "
+            "library (at most 64 experts, top-k at most 8, dimensions multiples of 4); use 'auto' for "
+            "automatic fallback or 'reference' for the PyTorch oracle"
         )
 
     def preflight_direct_decode(self, *, batch_size: int) -> None:
-        if self.mode == "direct":
+        """Reject an unsupported forced decode before any cache mutation."""
+        if self.mode != "direct":
+            return
+        w = self.router.weight
+        if not self._configuration_supported(w.device, w.dtype, batch_size):
             self._raise_direct_unsupported()
 
     def uses_direct(self, x: torch.Tensor, *, decode: bool) -> bool:
-        if decode and self.mode == "direct":
+        """Resolve reference / direct / auto without reading device results."""
+        if not decode or self.mode == "reference":
+            return False
+        supported = self._direct_supported(x)
+        if self.mode == "direct" and not supported:
             self._raise_direct_unsupported()
-        return False
+        return supported
 
     def _forward_reference(self, x: torch.Tensor) -> torch.Tensor:
         batch, seq_len, dim = x.shape
@@ -364,8 +397,27 @@ class MoEFeedForward(nn.Module):
             out.index_add_(0, rows, weight * expert(flat[rows]))
         return out.reshape(batch, seq_len, dim)
 
+    def _forward_direct(self, x: torch.Tensor) -> torch.Tensor:
+        x = x.contiguous()
+        ptrs = ctypes.c_void_p * self.num_experts
+        w1 = ptrs(*[e.net[0].weight.data_ptr() for e in self.experts])
+        b1 = ptrs(*[e.net[0].bias.data_ptr() for e in self.experts])
+        w2 = ptrs(*[e.net[2].weight.data_ptr() for e in self.experts])
+        b2 = ptrs(*[e.net[2].bias.data_ptr() for e in self.experts])
+        out = torch.empty_like(x)
+        ws = self._direct_workspace
+        rc = _native.lib().mie_moe_decode(
+            x.data_ptr(), self.router.weight.data_ptr(), w1, b1, w2, b2,
+            self.num_experts, self.top_k, self.dim, self.hidden_dim,
+            out.data_ptr(), ws.data_ptr(), ws.numel(), 0, _native.stream_of(x),
+        )
+        if rc:
+            _native.check(rc, "mie_moe_decode")
+        return out
+
     def forward(self, x, *, decode=False):
-        self.uses_direct(x, decode=decode)
+        if self.uses_direct(x, decode=decode):
+            return self._forward_direct(x)
         return self._forward_reference(x)
 
 
