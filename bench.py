@@ -270,6 +270,30 @@ def secondary_config3(torch):
     }
 
 
+def secondary_moe(torch):
+    """Fused MoE decode at config 1's shape: d 768, FFN 2048, top-2
+    of 8, float32.  Bytes per call: the router and the two selected experts'
+    W1, b1, W2, b2, read once."""
+    from moe_engine.model import MoEFeedForward
+
+    torch.manual_seed(0)
+    layer = MoEFeedForward(768, 2048, 8, 2).to("cuda").eval()
+    layer.set_mode("direct")
+    x = torch.randn(1, 1, 768, device="cuda")
+    nbytes = 4 * (8 * 768 + 2 * (2048 * 768 + 2048 + 768 * 2048 + 768))
+    with torch.no_grad():
+        us = timed_us(torch, lambda: layer(x, decode=True), iters=200, warmup=20)
+        layer.set_mode("reference")
+        ref_us = timed_us(torch, lambda: layer(x, decode=True), iters=50, warmup=5)
+    return {
+        "fused_us_per_call": round(us, 2),
+        "fused_gbs": round(nbytes / us / 1e3, 1),
+        "pytorch_path_us_per_call": round(ref_us, 2),
+        "bytes_per_call": nbytes,
+        "note": "back-to-back calls through the Python module (three launches each)",
+    }
+
+
 def secondary_config5(torch):
     """Long-context split decode, bf16, block 32: batch 1 and 8 at 131072."""
     from moe_engine import paged_attention, workloads
@@ -295,14 +319,16 @@ def secondary_config5(torch):
 def secondary_e2e(torch, rounds=5, new_tokens=64):
     """BASELINE config 1 on the GPU (random init from seed 0, fp32, block 16,
     32-token prompt): per-token greedy decode latency of the contiguous,
-    paged-gather and paged-direct systems in interleaved rounds with a paired
-    Student-t interval (moe_engine.harness.ab_compare)."""
+    paged-gather, paged-direct and paged-direct-graph (decode steps replayed
+    from a HIP graph) systems in interleaved rounds with paired Student-t
+    intervals (moe_engine.harness.ab_compare)."""
     from moe_engine import harness
 
     model = harness.make_model(harness.CONFIG1, seed=0, device="cuda")
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, harness.CONFIG1["vocab_size"], (32,), generator=gen).cuda()
-    return harness.ab_compare(model, prompt, rounds=rounds, new_tokens=new_tokens)
+    systems = harness.SYSTEMS + (harness.GRAPH_SYSTEM,)
+    return harness.ab_compare(model, prompt, systems, rounds=rounds, new_tokens=new_tokens)
 
 
 def main():
@@ -345,6 +371,7 @@ def main():
             ("config2_single_layer", secondary_config2),
             ("config3_append_gather", secondary_config3),
             ("config5_long_context", secondary_config5),
+            ("fused_moe_decode", secondary_moe),
             ("config1_e2e_decode", secondary_e2e),
         ):
             log(f"secondary {name}")

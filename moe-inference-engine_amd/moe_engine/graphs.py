@@ -1,0 +1,164 @@
+"""Whole decode steps captured as HIP graphs (paged-direct cache, greedy).
+
+A decode step of the engine launches ~15 kernels per layer; on the eager path
+the host spends longer issuing them than the GPU spends running them.  Here
+one step - embeddings, every layer (QKV projection, HIP KV append, HIP paged
+decode, fused HIP MoE), final norm, output projection - is captured once and
+replayed for every later token; the greedy argmax runs eagerly after each
+replay.
+
+Everything that changes from step to step lives on the device: the token fed
+in (the previous step's argmax, written to a fixed buffer), the position of the
+new token and the context length (incremented by the graph).  The paged cache
+is put in graph mode (PagedKVCache.graph_pos / graph_ctx), so the append and
+the decode read those device values and the decode launch is sized for the
+pool's capacity.  The host keeps only the block bookkeeping: before each
+replay it reserves the block the new token needs (one host-to-device copy of
+one block id every block_size tokens) - the replay itself never allocates.
+
+Only greedy decoding (temperature 0) over a PagedKVCache whose attention can
+run the direct kernel is captured; everything else uses Model.generate.
+"""
+
+import torch
+
+from moe_engine import paged_attention
+from moe_engine.model import EOS_TOKEN_ID, PagedKVCache
+
+
+class GraphedDecoder:
+    """Replays one greedy decode step of `model` over `cache` as a HIP graph.
+
+    The cache must already hold the prompt (cache.position > 0).  prime(token)
+    sets the token to decode next; each step() appends it, attends, and leaves
+    the next greedy token in `next_token` (and the logits in `logits`).  From
+    the second step on `logits` is the graph's output buffer, overwritten by
+    the next replay: clone it if it must outlive the step.
+    """
+
+    def __init__(self, model, cache, partition_tokens=128):
+        if not isinstance(cache, PagedKVCache) or cache.attention_mode == "gather":
+            raise ValueError("graph decode needs a paged cache whose attention mode is 'auto' or 'direct'")
+        weight = model.token_embedding.weight
+        if not paged_attention.is_supported(weight, model.config.head_dim):
+            raise RuntimeError("graph decode needs the direct paged kernel (ROCm device, float32 or bfloat16)")
+        for block in model.MoEBlocks:
+            # The PyTorch MoE path selects rows with data-dependent shapes (a
+            # host synchronization), which a graph cannot hold.
+            moe = block.moe
+            if moe.mode == "reference" or not moe._configuration_supported(weight.device, weight.dtype, 1):
+                raise RuntimeError("graph decode needs the fused MoE decode kernel (mode 'auto' or 'direct', float32)")
+        if cache.position <= 0:
+            raise ValueError("prefill the cache before building a graphed decoder")
+        self.model = model
+        self.cache = cache
+        device = weight.device
+        self.token = torch.zeros(1, 1, dtype=torch.long, device=device)
+        self.pos = torch.zeros(1, dtype=torch.int32, device=device)
+        self.ctx = torch.zeros(1, dtype=torch.int32, device=device)
+        self.partition_tokens = partition_tokens
+        self.graph = None
+        self._graph_out = None
+        self.logits = None
+        self.next_token = None
+        self.replays = 0
+
+    def _graph_mode(self, on):
+        c = self.cache
+        c.graph_pos = self.pos if on else None
+        c.graph_ctx = self.ctx if on else None
+        c.graph_partition_tokens = self.partition_tokens if on else 0
+
+    def _forward_body(self):
+        """The captured part: one forward step and the device position update."""
+        logits = self.model(self.token, self.cache)[:, -1, :]
+        self.pos.add_(1)
+        self.ctx.add_(1)
+        return logits
+
+    def _select(self, logits):
+        """Greedy pick, run eagerly after every replay: torch's argmax over a
+        wide row reduces across workgroups and clears its semaphores with a
+        memset, which a graph must not hold."""
+        nxt = torch.argmax(logits, dim=-1, keepdim=True)
+        self.token.copy_(nxt)
+        return nxt
+
+    @torch.no_grad()
+    def prime(self, token):
+        """Set the token to decode next (a [1, 1] or [1] integer tensor) and
+        the device position from the cache."""
+        self.token.copy_(token.reshape(1, 1))
+        p = self.cache.position
+        self.pos.fill_(p)
+        self.ctx.fill_(p + 1)
+
+    @torch.no_grad()
+    def step(self):
+        cache = self.cache
+        if cache.position >= self.model.max_seq_length:
+            raise RuntimeError("KV cache is full")
+        cache._reserve(cache.position + 1)
+        self._graph_mode(True)
+        try:
+            if self.graph is None:
+                # The first step runs eagerly on the stream the capture will use
+                # (so every library handle it records exists already); its
+                # results are returned.
+                side = torch.cuda.Stream()
+                side.wait_stream(torch.cuda.current_stream())
+                with torch.cuda.stream(side):
+                    self.logits = self._forward_body()
+                torch.cuda.synchronize()
+                position = cache.position
+                if position < self.model.max_seq_length:
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph, stream=side):
+                        self._graph_out = self._forward_body()
+                    # Capture records the work without running it: restore the
+                    # host position its forward advanced.
+                    cache.position = position
+                    self.graph = graph
+            else:
+                self.graph.replay()
+                cache.position += 1
+                self.replays += 1
+                self.logits = self._graph_out
+            self.next_token = self._select(self.logits)
+        finally:
+            self._graph_mode(False)
+        return self.next_token
+
+
+@torch.no_grad()
+def generate_graphed(model, token_ids, max_new_tokens, cache, partition_tokens=128):
+    """Greedy generation with the same results and stopping rules as
+    Model.generate(..., temperature=0, cache=cache) (model.py:567-621), with
+    decode steps replayed from a HIP graph."""
+    if max_new_tokens < 1:
+        raise ValueError("max_new_tokens must be at least 1")
+    if token_ids.dim() == 1:
+        token_ids = token_ids.unsqueeze(0)
+    token_ids = token_ids.to(model.token_embedding.weight.device).long()
+    if token_ids.shape[0] != 1 or token_ids.shape[1] == 0:
+        raise ValueError("generate_graphed() handles one non-empty sequence")
+    if token_ids.shape[1] > model.max_seq_length:
+        raise ValueError(f"prompt is {token_ids.shape[1]} tokens; max_seq_length is {model.max_seq_length}")
+    if cache.position != 0:
+        raise ValueError("generate_graphed() needs a fresh cache")
+    out = [token_ids]
+    logits = model(token_ids, cache)[:, -1, :]
+    next_token = torch.argmax(logits, dim=-1, keepdim=True)
+    decoder = None
+    for step in range(max_new_tokens):
+        if next_token.item() == EOS_TOKEN_ID:
+            break
+        out.append(next_token.clone())
+        if step == max_new_tokens - 1 or cache.position >= model.max_seq_length:
+            break  # the last token is never fed back (Model.generate does the same)
+        if decoder is None:
+            # Each step leaves the next token in the decoder's device buffer.
+            decoder = GraphedDecoder(model, cache, partition_tokens)
+            decoder.prime(next_token)
+        next_token = decoder.step()
+    return torch.cat(out, dim=1)

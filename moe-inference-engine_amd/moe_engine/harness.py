@@ -13,7 +13,9 @@ the real checkpoint and tokenizer are not available here:
                    (benchmarks/ab_compare.py:49-198)
 
 System names are the reference's: "contiguous", "paged-gather",
-"paged-direct".  Run as a module for a JSON report:
+"paged-direct", plus "paged-direct-graph": paged-direct with each decode step
+replayed from one captured HIP graph (moe_engine.graphs), captured once in the
+warm-up and reused for every later round.  Run as a module for a JSON report:
 
     python -m moe_engine.harness ab --rounds 5 --new-tokens 64
 """
@@ -31,6 +33,7 @@ from moe_engine import paged_attention
 from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig
 
 SYSTEMS = ("contiguous", "paged-gather", "paged-direct")
+GRAPH_SYSTEM = "paged-direct-graph"
 
 # the miniMoE-shaped decoder.
 CONFIG1 = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
@@ -65,7 +68,8 @@ def make_cache(model, system, block_size=16):
     if system == "contiguous":
         return model.new_cache()
     num_blocks = -(-model.max_seq_length // block_size)
-    return model.new_block_allocator(num_blocks, block_size, attention_mode=system[len("paged-"):]).new_cache()
+    mode = "direct" if system == GRAPH_SYSTEM else system[len("paged-"):]
+    return model.new_block_allocator(num_blocks, block_size, attention_mode=mode).new_cache()
 
 
 def release(cache):
@@ -124,6 +128,38 @@ def run_round(model, cache, prompt_ids, new_tokens):
     return prefill_s, steps, tokens
 
 
+def run_round_graphed(model, state, prompt_ids, new_tokens):
+    """run_round for GRAPH_SYSTEM.  `state` holds one paged-direct cache and its
+    GraphedDecoder across rounds: the cache is freed between rounds (its
+    device block table, which the graph reads, stays), so the graph captured
+    in the first round is replayed in every later one."""
+    from moe_engine.graphs import GraphedDecoder
+
+    cache = state["cache"]
+    device = prompt_ids.device
+    tokens = []
+    with torch.no_grad():
+        sync(device)
+        start = time.perf_counter()
+        logits = model(prompt_ids.unsqueeze(0), cache)
+        sync(device)
+        prefill_s = time.perf_counter() - start
+        step_input = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+        if state.get("decoder") is None:
+            state["decoder"] = GraphedDecoder(model, cache)
+        decoder = state["decoder"]
+        decoder.prime(step_input)
+        steps = []
+        for _ in range(new_tokens):
+            sync(device)
+            start = time.perf_counter()
+            step_input = decoder.step()
+            sync(device)
+            steps.append(time.perf_counter() - start)
+            tokens.append(int(step_input))
+    return prefill_s, steps, tokens
+
+
 def paired_t_summary(deltas):
     """Mean and two-sided 95 % Student-t interval of paired per-round deltas (ms)."""
     n = len(deltas)
@@ -143,8 +179,16 @@ def paired_t_summary(deltas):
 def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, block_size=16):
     """Interleaved rounds of every system, rotating which starts each round."""
     systems = list(systems)
+    graph_state = {}
 
     def run(system):
+        if system == GRAPH_SYSTEM:
+            if "cache" not in graph_state:
+                graph_state["cache"] = make_cache(model, system, block_size)
+            try:
+                return run_round_graphed(model, graph_state, prompt_ids, new_tokens)
+            finally:
+                release(graph_state["cache"])
         cache = make_cache(model, system, block_size)
         try:
             return run_round(model, cache, prompt_ids, new_tokens)
@@ -176,7 +220,8 @@ def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, bloc
         return [sum(steps) / len(steps) * 1e3 for steps in results[system]["rounds"]]
 
     paired = {}
-    for a, b in (("paged-direct", "contiguous"), ("paged-direct", "paged-gather"), ("paged-gather", "contiguous")):
+    for a, b in (("paged-direct", "contiguous"), ("paged-direct", "paged-gather"), ("paged-gather", "contiguous"),
+                 (GRAPH_SYSTEM, "paged-direct"), (GRAPH_SYSTEM, "contiguous")):
         if a in systems and b in systems:
             paired[f"{a}_minus_{b}"] = paired_t_summary([x - y for x, y in zip(mean_steps_ms(a), mean_steps_ms(b))])
     tokens = [results[s]["tokens"] for s in systems]

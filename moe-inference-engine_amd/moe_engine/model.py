@@ -155,6 +155,13 @@ class PagedKVCache:
             allocator.num_blocks, dtype=torch.int32, device=allocator.k_pool.device
         )
         self._write_index_key = None  # (position, seq_len) of cached CPU indices
+        # Graph mode (moe_engine.graphs): device int32 [1] tensors holding the
+        # position of the token being decoded and the context length; the
+        # kernels read them instead of host ints, and blocks are reserved by
+        # the caller before each replay.  None in ordinary use.
+        self.graph_pos = None
+        self.graph_ctx = None
+        self.graph_partition_tokens = 0
 
     def _reserve(self, num_tokens: int) -> None:
         """Hold enough blocks for `num_tokens`, all or nothing (model.py:125-143)."""
@@ -192,8 +199,15 @@ class PagedKVCache:
         if k.shape[0] != 1:
             raise ValueError("PagedKVCache holds one sequence; use batch size 1")
         seq_len = k.shape[2]
-        self._reserve(position + seq_len)
         alloc = self.allocator
+        if self.graph_pos is not None:
+            # Blocks were reserved before the replay; the position is on the device.
+            if seq_len != 1:
+                raise ValueError("graph mode appends one token per step")
+            kv_ops.append(alloc.k_pool, alloc.v_pool, layer_idx, k, v, self.block_table_device[None],
+                          positions=self.graph_pos)
+            return
+        self._reserve(position + seq_len)
         if alloc.on_device:
             ks = k.stride()
             if (
@@ -470,7 +484,11 @@ class Model(nn.Module):
             for block in self.MoEBlocks:
                 block.moe.preflight_direct_decode(batch_size=batch)
 
-        pos = torch.arange(position, position + seq_len, device=token_ids.device)
+        graph_pos = getattr(cache, "graph_pos", None)
+        if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
+            pos = graph_pos.long()
+        else:
+            pos = torch.arange(position, position + seq_len, device=token_ids.device)
         x = self.token_embedding(token_ids) + self.positional_embedding(pos)
         for i, block in enumerate(self.MoEBlocks):
             x = block(x, cache, i, position)

@@ -156,6 +156,20 @@ def decode(q: torch.Tensor, cache, layer_idx: int, context_len: int) -> torch.Te
     """
     allocator = cache.allocator
     num_heads, head_dim = q.shape[1], q.shape[3]
+    graph_ctx = getattr(cache, "graph_ctx", None)
+    if graph_ctx is not None:
+        # HIP-graph decode: the length lives on the device and the launch is
+        # sized for the pool's capacity, so one captured launch serves every step.
+        out = decode_layer(
+            q[:, :, 0],
+            allocator.k_pool[layer_idx],
+            allocator.v_pool[layer_idx],
+            cache.block_table_device,
+            context_lens=graph_ctx,
+            max_context_len=allocator.num_blocks * allocator.block_size,
+            partition_tokens=cache.graph_partition_tokens,
+        )
+        return out.view(1, num_heads, 1, head_dim)
     launch = getattr(allocator, "_launch", None)
     qs = q.stride()
     if (

@@ -1,0 +1,130 @@
+"""Whole decode steps replayed from a HIP graph (moe_engine.graphs) against
+the eager paged-direct path.
+
+Each test replays the captured step many times across block boundaries, with
+eager work of the same model (another sequence in the same block pool) and a
+device synchronization between replays, and checks every replay: its logits
+against the eager step's for the same token and position, and the greedy
+tokens against Model.generate (reference model.py:567-621).  The graph's
+decode launch is sized for the pool's capacity and splits the context into
+128-token partitions, while the eager launch is sized for the exact length,
+so float32 logits agree to rounding, not bit for bit.
+"""
+
+import pytest
+import torch
+
+from conftest import print_case
+from moe_engine.graphs import GraphedDecoder, generate_graphed
+from moe_engine.model import Model, ModelConfig
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(max_seq_length=128, vocab_size=96, num_layers=2, hidden_dim=32, num_experts=4, top_k=2)
+E2E = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
+           num_experts=8, top_k=2, ffn_dim=2048)
+
+
+def tiny_model(dtype=torch.float32):
+    torch.manual_seed(0)
+    return Model(ModelConfig(**TINY)).to("cuda", dtype).eval()
+
+
+@pytest.mark.parametrize("block_size", [4, 16])
+def test_every_replay_matches_eager_step(block_size):
+    print_case("graph replay vs eager", block_size)
+    model = tiny_model()
+    allocator = model.new_block_allocator(num_blocks=80, block_size=block_size, attention_mode="direct")
+    graphed, eager = allocator.new_cache(), allocator.new_cache()
+    prompt = torch.randint(0, TINY["vocab_size"], (1, 9), device="cuda")
+    with torch.no_grad():
+        first = model(prompt, graphed)[:, -1]
+        torch.testing.assert_close(model(prompt, eager)[:, -1], first)
+        decoder = GraphedDecoder(model, graphed)
+        token = first.argmax(-1, keepdim=True)
+        decoder.prime(token)
+        for step in range(100):
+            got = decoder.step()
+            got_logits = decoder.logits.clone()
+            # Eager work between replays: the same step on the other sequence,
+            # whose blocks interleave with the graphed sequence's in the pool.
+            want_logits = model(token, eager)[:, -1]
+            torch.cuda.synchronize()
+            torch.testing.assert_close(got_logits, want_logits, atol=2e-5, rtol=2e-5,
+                                       msg=lambda m: f"step {step}: {m}")
+            token = want_logits.argmax(-1, keepdim=True)
+            assert torch.equal(got, token), f"step {step}"
+            assert graphed.position == eager.position
+    assert decoder.replays == 99
+    assert graphed.block_table != eager.block_table
+    graphed.free()
+    eager.free()
+    assert len(allocator.free_blocks) == allocator.num_blocks
+
+
+def test_generate_graphed_matches_generate():
+    print_case("generate_graphed")
+    model = tiny_model()
+    prompt = torch.randint(0, TINY["vocab_size"], (7,), device="cuda")
+    allocator = model.new_block_allocator(num_blocks=40, block_size=4, attention_mode="direct")
+    cache = allocator.new_cache()
+    want = model.generate(prompt, max_new_tokens=60, temperature=0, cache=cache)
+    cache.free()
+    cache = allocator.new_cache()
+    got = generate_graphed(model, prompt, 60, cache)
+    assert cache.position == want.shape[1] - 1
+    cache.free()
+    assert torch.equal(got, want)
+
+
+def test_graph_decoder_needs_fused_moe():
+    """bf16 MoE and mode 'reference' run the PyTorch expert loop, which
+    synchronizes the host; the decoder refuses them before touching the cache."""
+    for dtype, mode in ((torch.bfloat16, "auto"), (torch.float32, "reference")):
+        model = tiny_model(dtype).set_moe_mode(mode)
+        cache = model.new_block_allocator(num_blocks=8, block_size=4, attention_mode="direct").new_cache()
+        with torch.no_grad():
+            model(torch.zeros(1, 3, dtype=torch.long, device="cuda"), cache)
+        with pytest.raises(RuntimeError, match="fused MoE"):
+            GraphedDecoder(model, cache)
+        assert cache.position == 3
+
+
+def test_generate_graphed_stops_at_max_seq_length():
+    model = tiny_model()
+    prompt = torch.randint(0, TINY["vocab_size"], (100,), device="cuda")
+    allocator = model.new_block_allocator(num_blocks=32, block_size=4, attention_mode="direct")
+    cache = allocator.new_cache()
+    want = model.generate(prompt, max_new_tokens=64, temperature=0, cache=cache)
+    cache.free()
+    cache = allocator.new_cache()
+    got = generate_graphed(model, prompt, 64, cache)
+    assert got.shape[1] == want.shape[1] == TINY["max_seq_length"] + 1
+    assert torch.equal(got, want)
+    assert cache.position == TINY["max_seq_length"]
+
+
+def test_graph_decoder_rejects_gather_cache_and_empty_cache():
+    model = tiny_model()
+    gather = model.new_block_allocator(num_blocks=8, block_size=4, attention_mode="gather").new_cache()
+    with pytest.raises(ValueError, match="graph decode"):
+        GraphedDecoder(model, gather)
+    direct = model.new_block_allocator(num_blocks=8, block_size=4, attention_mode="direct").new_cache()
+    with pytest.raises(ValueError, match="prefill"):
+        GraphedDecoder(model, direct)
+
+
+def test_config1_graphed_tokens_identical_to_eager():
+    """BASELINE config 1 shape, 32-token prompt then 64 greedy tokens."""
+    print_case("config1 graphed")
+    torch.manual_seed(0)
+    model = Model(ModelConfig(**E2E)).to("cuda").eval()
+    prompt = torch.randint(0, E2E["vocab_size"], (32,), device="cuda")
+    allocator = model.new_block_allocator(num_blocks=64, block_size=16, attention_mode="direct")
+    cache = allocator.new_cache()
+    want = model.generate(prompt, max_new_tokens=64, temperature=0, cache=cache)
+    cache.free()
+    cache = allocator.new_cache()
+    got = generate_graphed(model, prompt, 64, cache)
+    cache.free()
+    assert torch.equal(got, want)
