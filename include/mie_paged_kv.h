@@ -9,6 +9,8 @@
  *   mie_kv_gather     <- PagedKVCache.read      src/moe_engine/model.py:186-201
  *   mie_paged_decode  <- paged_attention.decode src/moe_engine/paged_attention.py:113-154
  *                        and _paged_decode_kernel src/moe_engine/paged_attention.py:46-110
+ *   mie_moe_route     <- fused_moe.route         src/moe_engine/fused_moe.py:274-309
+ *   mie_moe_decode    <- fused_moe.decode        src/moe_engine/fused_moe.py:312-380
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -62,7 +64,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 3
+#define MIE_ABI_VERSION 4
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -167,31 +169,44 @@ int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32_t head_dim
 int32_t mie_paged_decode_supported(int32_t head_dim, int32_t dtype);
 
 /*
+ * Router and top-k of the fused MoE decode for ONE token, float32
+ * (fused_moe.route, fused_moe.py:274-309):
+ *
+ *   router_logits[e] = router_weight[e, :] . x            e < num_experts
+ *   expert_ids[s]    = the top_k experts, largest logit first, lower id on ties
+ *   route_weights[s] = softmax over the selected logits, in the same order
+ *
+ * x [dim] and router_weight [num_experts, dim] contiguous and 16-byte aligned,
+ * dim a multiple of 4, num_experts <= 64, top_k <= 8.  One launch.
+ */
+int32_t mie_moe_route(const void* x, const void* router_weight, int32_t num_experts,
+                      int32_t top_k, int32_t dim, void* router_logits, void* expert_ids,
+                      void* route_weights, int32_t dtype, void* stream);
+
+/*
  * Fused top-k mixture of experts for ONE decode token, float32, with no
  * device-to-host synchronisation.  Replaces MoEFeedForward's PyTorch path for
  * a single token (model.py:443-461; its torch.where syncs once per expert) and
- * the reference's Triton fused MoE decode (fused_moe.py:274-380):
+ * serves the reference's Triton fused MoE decode (fused_moe.py:312-380):
+ * mie_moe_route, then
  *
- *   logits = router_weight[E, dim] . x;  ids = top_k experts by logit (lower id
- *   on ties);  w = softmax(logits[ids]);
- *   out = sum over ids in increasing id, starting from 0, of
- *         w_e * (w2[e] . GELU(w1[e] . x + b1[e]) + b2[e])
+ *   hidden_act[s] = GELU(w1[e_s] . x + b1[e_s])          e_s = expert_ids[s]
+ *   out = sum over the slots in increasing e_s, from 0, of
+ *         round(route_weights[s] * (w2[e_s] . hidden_act[s] + b2[e_s]))
  *
- * with GELU the exact erf form, w1[e] [hidden, dim], b1[e] [hidden], w2[e]
- * [dim, hidden], b2[e] [dim], all contiguous.  w1, b1, w2, b2 are HOST arrays of
- * num_experts device pointers (num_experts <= 64, top_k <= 8); x, the weight
- * matrices and `workspace` are 16-byte aligned; dim and hidden are multiples
- * of 4.  `workspace` holds mie_moe_decode_workspace_bytes(top_k, hidden)
- * bytes; nothing in it needs clearing.  Three launches on `stream`.
+ * with GELU the exact erf form and the sum in the order and rounding of the
+ * reference's index_add_ loop (model.py:455-460).  Expert weights are the
+ * canonical contiguous storages w1 [E, hidden, dim], b1 [E, hidden], w2 [E,
+ * dim, hidden], b2 [E, dim]; hidden_act is [top_k, hidden], out [dim].  x, the
+ * router weight, w1, w2 and hidden_act are 16-byte aligned; dim and hidden are
+ * multiples of 4.  The routing outputs are those of mie_moe_route.  Three
+ * launches on `stream`; nothing needs clearing beforehand.
  */
-int32_t mie_moe_decode(const void* x, const void* router_weight, const void* const* w1,
-                       const void* const* b1, const void* const* w2, const void* const* b2,
-                       int32_t num_experts, int32_t top_k, int32_t dim, int32_t hidden,
-                       void* out, void* workspace, int64_t workspace_bytes, int32_t dtype,
-                       void* stream);
-
-/* Workspace bytes mie_moe_decode needs (0 for invalid arguments). */
-int64_t mie_moe_decode_workspace_bytes(int32_t top_k, int32_t hidden);
+int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1,
+                       const void* b1, const void* w2, const void* b2, int32_t num_experts,
+                       int32_t top_k, int32_t dim, int32_t hidden, void* router_logits,
+                       void* expert_ids, void* route_weights, void* hidden_act, void* out,
+                       int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -69,14 +69,19 @@ _SIGNATURES = {
         [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     ),
     "mie_paged_decode_supported": (_i32, [_i32, _i32]),
+    "mie_moe_route": (
+        _i32,
+        [_c_void_p, _c_void_p, _i32, _i32, _i32,  # x, router weight, experts, top_k, dim
+         _c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p],  # logits, ids, weights, dtype, stream
+    ),
     "mie_moe_decode": (
         _i32,
         [_c_void_p, _c_void_p,  # x, router weight
-         _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # host arrays of w1, b1, w2, b2 pointers
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # canonical w1, b1, w2, b2 storages
          _i32, _i32, _i32, _i32,  # experts, top_k, dim, hidden
-         _c_void_p, _c_void_p, _i64, _i32, _c_void_p],  # out, workspace, bytes, dtype, stream
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # logits, ids, weights, hidden, out
+         _i32, _c_void_p],  # dtype, stream
     ),
-    "mie_moe_decode_workspace_bytes": (_i64, [_i32, _i32]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

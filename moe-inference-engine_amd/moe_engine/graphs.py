@@ -46,7 +46,7 @@ class GraphedDecoder:
             # The PyTorch MoE path selects rows with data-dependent shapes (a
             # host synchronization), which a graph cannot hold.
             moe = block.moe
-            if moe.mode == "reference" or not moe._configuration_supported(weight.device, weight.dtype, 1):
+            if moe.mode == "reference" or not moe.direct_configuration_supported(1):
                 raise RuntimeError("graph decode needs the fused MoE decode kernel (mode 'auto' or 'direct', float32)")
         if cache.position <= 0:
             raise ValueError("prefill the cache before building a graphed decoder")

@@ -8,6 +8,7 @@ underneath the paged cache on a ROCm device:
   * PagedKVCache.write  -> one mie_kv_append launch (K and V, decode or prefill)
   * PagedKVCache.read   -> one mie_kv_gather launch (K and V)
   * direct decode       -> mie_paged_decode (moe_engine.paged_attention)
+  * one-token MoE       -> mie_moe_decode (moe_engine.fused_moe)
 
 A paged pool on a ROCm device requires the HIP library and raises at
 construction without it.  Pools on the CPU use PyTorch indexing, which is the
@@ -19,7 +20,6 @@ attention out_proj, in_proj xavier, the experts' two linears each, router), so
 a seeded model has the reference's weights.
 """
 
-import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -28,7 +28,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from moe_engine import _native, kv_ops, paged_attention
+from moe_engine import _native, fused_moe, kv_ops, paged_attention
 
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
@@ -326,10 +326,17 @@ class MoEFeedForward(nn.Module):
 
     Prefill, and decode in mode 'reference', run the reference's PyTorch path
     (model.py:443-461).  One-token decode in mode 'auto' or 'direct' runs the
-    fused HIP kernels (mie_moe_decode) where they apply: a ROCm device, the HIP
-    library, float32, one token.  'auto' falls back to the PyTorch path
+    fused HIP kernels (moe_engine.fused_moe) where they apply: a ROCm device,
+    the HIP library, float32, one token.  'auto' falls back to the PyTorch path
     elsewhere; a forced 'direct' that cannot run raises before any cache
     mutation, through the model's decode preflight (model.py:408-441).
+
+    The experts' parameters are views into four canonical contiguous storages
+    (`_expert_storage`: w1 [E, hidden, dim], b1 [E, hidden], w2 [E, dim,
+    hidden], b2 [E, dim]), so the kernels address a selected expert by offset;
+    the views keep the checkpoint's parameter names, and the storages are
+    rebuilt after load_state_dict and after device / dtype conversion
+    (model.py:323-366).
     """
 
     def __init__(self, dim, hidden_dim, num_experts, top_k, mode="auto"):
@@ -343,32 +350,80 @@ class MoEFeedForward(nn.Module):
         self.num_experts = num_experts
         self.experts = nn.ModuleList(Expert(dim, hidden_dim) for _ in range(num_experts))
         self.router = nn.Linear(dim, num_experts, bias=False)
-        # Fixed decode workspace (selected ids, weights, hidden activations);
-        # non-persistent, so checkpoints and state-dict keys are unchanged.
-        self.register_buffer(
-            "_direct_workspace", torch.empty(256 + top_k * hidden_dim * 4, dtype=torch.uint8), persistent=False
-        )
+        # Fixed per-layer decode workspaces; non-persistent, so checkpoints and
+        # state-dict keys are unchanged (model.py:301-321).
+        for name, shape, dtype in (
+            ("_router_logits", (num_experts,), torch.float32),
+            ("_expert_ids", (top_k,), torch.int32),
+            ("_route_weights", (top_k,), torch.float32),
+            ("_expert_hidden", (top_k, hidden_dim), torch.float32),
+            ("_direct_out", (dim,), torch.float32),
+        ):
+            self.register_buffer(name, torch.empty(shape, dtype=dtype), persistent=False)
+        self._pack_expert_parameters()
+        self.register_load_state_dict_post_hook(self._repack_after_load)
+
+    def _pack_group(self, layer_index: int, name: str) -> torch.Tensor:
+        """One storage [E, *shape] whose slices become the experts' parameters."""
+        params = [getattr(expert.net[layer_index], name) for expert in self.experts]
+        if any(p.shape != params[0].shape for p in params):
+            raise ValueError("all experts must have identical parameter shapes")
+        storage = torch.empty((len(params), *params[0].shape), dtype=params[0].dtype, device=params[0].device)
+        with torch.no_grad():
+            for expert, src, dst in zip(self.experts, params, storage):
+                dst.copy_(src)
+                setattr(expert.net[layer_index], name, nn.Parameter(dst, requires_grad=src.requires_grad))
+        return storage
+
+    def _pack_expert_parameters(self) -> None:
+        self._expert_storage = {
+            "w1": self._pack_group(0, "weight"),
+            "b1": self._pack_group(0, "bias"),
+            "w2": self._pack_group(2, "weight"),
+            "b2": self._pack_group(2, "bias"),
+        }
+
+    def _repack_after_load(self, _module, _incompatible_keys) -> None:
+        # load_state_dict copies into the views; assign=True replaces them.
+        self._pack_expert_parameters()
+
+    def _apply(self, fn, recurse=True):
+        # Device / dtype conversion replaces each parameter on its own.
+        result = super()._apply(fn, recurse=recurse)
+        self._pack_expert_parameters()
+        return result
 
     def set_mode(self, mode: str) -> None:
         if mode not in MOE_MODES:
             raise ValueError(f"unknown MoE mode {mode!r}")
         self.mode = mode
 
-    def _configuration_supported(self, device, dtype, batch_size) -> bool:
-        return (
-            _native.HAS_HIP
-            and device.type == "cuda"
-            and torch.version.hip is not None
-            and dtype == torch.float32
-            and batch_size == 1
-            and 0 < self.top_k <= min(8, self.num_experts)
-            and self.num_experts <= 64
-            and self.dim % 4 == 0
-            and self.hidden_dim % 4 == 0
+    def _has_direct_layout(self) -> bool:
+        s = self._expert_storage
+        return fused_moe.has_canonical_layout(
+            self.router.weight, s["w1"], s["b1"], s["w2"], s["b2"],
+            self._router_logits, self._expert_ids, self._route_weights, self._expert_hidden, self._direct_out,
         )
 
     def _direct_supported(self, x: torch.Tensor) -> bool:
-        return x.shape[0] * x.shape[1] == 1 and self._configuration_supported(x.device, x.dtype, 1)
+        return (
+            fused_moe.is_supported(
+                x, num_experts=self.num_experts, top_k=self.top_k, expert_hidden_dim=self.hidden_dim
+            )
+            and self._has_direct_layout()
+        )
+
+    def direct_configuration_supported(self, batch_size: int = 1) -> bool:
+        """Whether one-token decode of this layer can take the fused kernels
+        (metadata only: no input needed)."""
+        w = self.router.weight
+        return (
+            fused_moe.is_configuration_supported(
+                device=w.device, dtype=w.dtype, batch_size=batch_size, hidden_dim=self.dim,
+                num_experts=self.num_experts, top_k=self.top_k, expert_hidden_dim=self.hidden_dim,
+            )
+            and self._has_direct_layout()
+        )
 
     @staticmethod
     def _raise_direct_unsupported() -> None:
@@ -380,10 +435,7 @@ class MoEFeedForward(nn.Module):
 
     def preflight_direct_decode(self, *, batch_size: int) -> None:
         """Reject an unsupported forced decode before any cache mutation."""
-        if self.mode != "direct":
-            return
-        w = self.router.weight
-        if not self._configuration_supported(w.device, w.dtype, batch_size):
+        if self.mode == "direct" and not self.direct_configuration_supported(batch_size):
             self._raise_direct_unsupported()
 
     def uses_direct(self, x: torch.Tensor, *, decode: bool) -> bool:
@@ -412,22 +464,12 @@ class MoEFeedForward(nn.Module):
         return out.reshape(batch, seq_len, dim)
 
     def _forward_direct(self, x: torch.Tensor) -> torch.Tensor:
-        x = x.contiguous()
-        ptrs = ctypes.c_void_p * self.num_experts
-        w1 = ptrs(*[e.net[0].weight.data_ptr() for e in self.experts])
-        b1 = ptrs(*[e.net[0].bias.data_ptr() for e in self.experts])
-        w2 = ptrs(*[e.net[2].weight.data_ptr() for e in self.experts])
-        b2 = ptrs(*[e.net[2].bias.data_ptr() for e in self.experts])
-        out = torch.empty_like(x)
-        ws = self._direct_workspace
-        rc = _native.lib().mie_moe_decode(
-            x.data_ptr(), self.router.weight.data_ptr(), w1, b1, w2, b2,
-            self.num_experts, self.top_k, self.dim, self.hidden_dim,
-            out.data_ptr(), ws.data_ptr(), ws.numel(), 0, _native.stream_of(x),
+        s = self._expert_storage
+        return fused_moe.decode(
+            x, self.router.weight, s["w1"], s["b1"], s["w2"], s["b2"],
+            router_logits=self._router_logits, expert_ids=self._expert_ids, route_weights=self._route_weights,
+            hidden=self._expert_hidden, out=self._direct_out,
         )
-        if rc:
-            _native.check(rc, "mie_moe_decode")
-        return out
 
     def forward(self, x, *, decode=False):
         if self.uses_direct(x, decode=decode):

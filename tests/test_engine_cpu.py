@@ -16,7 +16,7 @@ import pytest
 import torch
 
 from moe_engine import paged_attention
-from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig, PagedKVCache
+from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig, MoEFeedForward, PagedKVCache
 from oracle import paged_ref as ref
 
 TINY = dict(max_seq_length=32, vocab_size=96, num_layers=2, hidden_dim=32, num_experts=4, top_k=2)
@@ -283,3 +283,63 @@ def test_contiguous_kvcache_is_a_view():
     rk, rv = cache.read(0, 5)
     assert torch.equal(rk[:, :, 2:], k) and torch.equal(rv[:, :, 2:], -k)
     assert rk.data_ptr() == cache.k.data_ptr()
+
+
+def assert_canonical_storage(moe, *, device_type, dtype):
+    """Each expert parameter group is one contiguous storage whose slices are
+    the experts' parameters (reference tests/test_fused_moe.py:239-259)."""
+    for key, layer, name in (("w1", 0, "weight"), ("b1", 0, "bias"), ("w2", 2, "weight"), ("b2", 2, "bias")):
+        storage = moe._expert_storage[key]
+        params = [getattr(expert.net[layer], name) for expert in moe.experts]
+        step = params[0].numel() * params[0].element_size()
+        assert storage.device.type == device_type and storage.dtype == dtype
+        assert storage.is_contiguous() and all(p.is_contiguous() for p in params)
+        assert storage.shape == (moe.num_experts, *params[0].shape)
+        assert [p.data_ptr() for p in params] == [storage.data_ptr() + e * step for e in range(moe.num_experts)]
+
+
+def test_canonical_storage_survives_load_and_dtype_apply():
+    moe = MoEFeedForward(32, 128, 4, 2)
+    names = {f"experts.{e}.{layer}.{p}" for e in range(4) for layer in ("net.0", "net.2") for p in ("weight", "bias")}
+    assert set(moe.state_dict()) == names | {"router.weight"}
+    for assign in (False, True):
+        checkpoint = {name: torch.randn_like(p) for name, p in moe.state_dict().items()}
+        moe.load_state_dict(checkpoint, assign=assign)
+        for name, p in moe.state_dict().items():
+            assert torch.equal(p, checkpoint[name])
+        assert_canonical_storage(moe, device_type="cpu", dtype=torch.float32)
+    moe.double()
+    assert_canonical_storage(moe, device_type="cpu", dtype=torch.float64)
+    moe.float()
+    assert_canonical_storage(moe, device_type="cpu", dtype=torch.float32)
+
+
+def test_packed_experts_compute_what_unpacked_experts_compute():
+    torch.manual_seed(0)
+    moe = MoEFeedForward(32, 64, 4, 2)
+    x = torch.randn(1, 5, 32)
+    with torch.no_grad():
+        got = moe(x)
+        logits = moe.router(x[0])
+        top, ids = torch.topk(logits, 2, dim=-1)
+        weights = torch.softmax(top, dim=-1)
+        want = torch.stack(
+            [sum(weights[t, s] * moe.experts[int(ids[t, s])](x[0, t]) for s in range(2)) for t in range(5)]
+        )
+    torch.testing.assert_close(got[0], want, atol=1e-6, rtol=1e-5)
+
+
+def test_moe_auto_falls_back_on_cpu_and_forced_direct_fails():
+    torch.manual_seed(0)
+    moe = MoEFeedForward(32, 128, 4, 2, mode="auto").eval()
+    x = torch.randn(1, 1, 32)
+    with torch.no_grad():
+        torch.testing.assert_close(moe(x, decode=True), moe._forward_reference(x), atol=0, rtol=0)
+    moe.set_mode("direct")
+    with pytest.raises(RuntimeError, match="direct"):
+        moe(x, decode=True)
+    prefill = x.expand(1, 2, 32)
+    with torch.no_grad():
+        torch.testing.assert_close(moe(prefill, decode=False), moe._forward_reference(prefill), atol=0, rtol=0)
+    with pytest.raises(ValueError, match="unknown MoE mode"):
+        moe.set_mode("fast")
