@@ -9,6 +9,8 @@
  *   mie_kv_gather     <- PagedKVCache.read      src/moe_engine/model.py:186-201
  *   mie_paged_decode  <- paged_attention.decode src/moe_engine/paged_attention.py:113-154
  *                        and _paged_decode_kernel src/moe_engine/paged_attention.py:46-110
+ *   mie_qkv_append    <- CachedAttention.forward's QKV projection and
+ *                        cache.write for one decode token  src/moe_engine/model.py:228-247
  *   mie_moe_route     <- fused_moe.route         src/moe_engine/fused_moe.py:274-309
  *   mie_moe_decode    <- fused_moe.decode        src/moe_engine/fused_moe.py:312-380
  *
@@ -64,7 +66,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 4
+#define MIE_ABI_VERSION 5
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -167,6 +169,39 @@ int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32_t head_dim
 
 /* 1 if mie_paged_decode is built for (head_dim, dtype), else 0. */
 int32_t mie_paged_decode_supported(int32_t head_dim, int32_t dtype);
+
+/*
+ * QKV projection of ONE decode token written straight into the pools
+ * (CachedAttention.forward, model.py:228-234, and PagedKVCache.write,
+ * model.py:167-178, in one launch):
+ *
+ *   y   = LayerNorm(x; ln_weight, ln_bias, ln_eps)   (y = x when ln_weight is NULL)
+ *   qkv = w_in[3*dim, dim] . y + b_in                (b_in may be NULL)
+ *   q_out[0:dim]                               = qkv[0:dim]
+ *   k_pool[bt[p/BS], h, p%BS, :] (and v_pool)  = qkv[dim + h*D : dim + (h+1)*D]
+ *                                                (and qkv[2*dim + ...])
+ *
+ * p is *position_dev when that is non-NULL (a device int32, so a captured graph
+ * can advance it), else `position`.  block_table holds block_table_len entries;
+ * a logical block past it or a block id outside [0, num_blocks) skips the K/V
+ * stores, as mie_kv_append does.  The norm is computed in float32 and rounded to
+ * the model dtype, the projection accumulates in float32 and rounds once: the
+ * reference's rounding points.  dim = num_heads * head_dim; x, the norm
+ * parameters, w_in, b_in, q_out and the pools share `dtype` (f32 or bf16);
+ * w_in is 16-byte aligned.  mie_qkv_append_supported(dim, dtype) says whether
+ * the shape is built (dim <= 2048 f32 / 4096 bf16, a multiple of 4 / 8).
+ */
+int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias,
+                       float ln_eps, const void* w_in, const void* b_in, int32_t dim,
+                       void* k_pool, void* v_pool, int64_t pool_stride_block,
+                       int64_t pool_stride_head, int32_t num_blocks,
+                       const int32_t* block_table, int32_t block_table_len,
+                       const int32_t* position_dev, int32_t position, void* q_out,
+                       int32_t num_heads, int32_t head_dim, int32_t block_size,
+                       int32_t dtype, void* stream);
+
+/* 1 if mie_qkv_append is built for (dim, dtype), else 0. */
+int32_t mie_qkv_append_supported(int32_t dim, int32_t dtype);
 
 /*
  * Router and top-k of the fused MoE decode for ONE token, float32

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -69,6 +69,15 @@ _SIGNATURES = {
         [_i32, _i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i32), ctypes.POINTER(_i64)],
     ),
     "mie_paged_decode_supported": (_i32, [_i32, _i32]),
+    "mie_qkv_append": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _f32,  # x, norm weight, norm bias, eps
+         _c_void_p, _c_void_p, _i32,  # w_in, b_in, dim
+         _c_void_p, _c_void_p, _i64, _i64, _i32,  # pools, strides, num_blocks
+         _c_void_p, _i32, _c_void_p, _i32,  # block table, its length, position (device), position
+         _c_void_p, _i32, _i32, _i32, _i32, _c_void_p],  # q_out, heads, head_dim, block_size, dtype, stream
+    ),
+    "mie_qkv_append_supported": (_i32, [_i32, _i32]),
     "mie_moe_route": (
         _i32,
         [_c_void_p, _c_void_p, _i32, _i32, _i32,  # x, router weight, experts, top_k, dim

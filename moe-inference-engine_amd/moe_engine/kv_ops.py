@@ -135,3 +135,86 @@ def gather(
         "mie_kv_gather",
     )
     return out_k, out_v
+
+
+def qkv_append_supported(dim: int, dtype: torch.dtype) -> bool:
+    """Whether mie_qkv_append is built for this model width and dtype."""
+    if not _native.HAS_HIP or dtype not in (torch.float32, torch.bfloat16):
+        return False
+    return bool(_native.lib().mie_qkv_append_supported(int(dim), _native.dtype_code(dtype)))
+
+
+def qkv_append(
+    x: torch.Tensor,
+    in_proj_weight: torch.Tensor,
+    in_proj_bias: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    layer_idx: int,
+    block_table: torch.Tensor,
+    *,
+    position: int = 0,
+    position_dev: torch.Tensor = None,
+    norm_weight: torch.Tensor = None,
+    norm_bias: torch.Tensor = None,
+    norm_eps: float = 1e-5,
+    q_out: torch.Tensor = None,
+) -> torch.Tensor:
+    """QKV projection of one token with K and V stored into their pool slots.
+
+    x holds one token's dim values (any shape of dim elements, contiguous);
+    in_proj_weight [3*dim, dim] and in_proj_bias [3*dim] are the attention's
+    packed projection (reference model.py:218-224); block_table is the
+    sequence's 1-D int32 device table.  The token goes to logical position
+    `position`, or to *position_dev (an int32 device [1]) when given.  With
+    norm_weight the projection applies to LayerNorm(x) (the block's attn_norm).
+    Returns q [1, heads, 1, head_dim] (written into q_out when given); the
+    block for the position must already be reserved.
+    """
+    _check_pools(k_pool, v_pool)
+    kl, vl = _layer(k_pool, layer_idx), _layer(v_pool, layer_idx)
+    nb, heads, block_size, head_dim = kl.shape
+    dim = heads * head_dim
+    dtype = kl.dtype
+    if x.numel() != dim or not x.is_contiguous():
+        raise ValueError(f"x must hold {dim} contiguous values")
+    if in_proj_weight.shape != (3 * dim, dim) or not in_proj_weight.is_contiguous():
+        raise ValueError(f"in_proj_weight must be a contiguous [{3 * dim}, {dim}] matrix")
+    if in_proj_bias is not None and (in_proj_bias.shape != (3 * dim,) or not in_proj_bias.is_contiguous()):
+        raise ValueError(f"in_proj_bias must be a contiguous [{3 * dim}] vector")
+    norm = [t for t in (norm_weight, norm_bias) if t is not None]
+    if norm_bias is not None and norm_weight is None:
+        raise ValueError("a norm bias needs a norm weight")
+    for t in norm:
+        if t.shape != (dim,) or not t.is_contiguous():
+            raise ValueError(f"norm parameters must be contiguous [{dim}] vectors")
+    params = [x, in_proj_weight, *([in_proj_bias] if in_proj_bias is not None else []), *norm]
+    if any(t.dtype != dtype or t.device != kl.device for t in params):
+        raise ValueError("x, the projection and norm parameters must match the pools' dtype and device")
+    if not qkv_append_supported(dim, dtype):
+        raise RuntimeError(f"mie_qkv_append is not built for dim {dim} in {dtype}")
+    if block_table.dtype != torch.int32 or block_table.dim() != 1 or block_table.device != kl.device:
+        raise ValueError("block_table must be a 1-D int32 tensor on the pool's device")
+    if not block_table.is_contiguous():
+        raise ValueError("block_table must be contiguous")
+    if position_dev is not None:
+        if position_dev.dtype != torch.int32 or position_dev.numel() != 1 or position_dev.device != kl.device:
+            raise ValueError("position_dev must be an int32 device tensor of one element")
+    elif not 0 <= position < block_table.numel() * block_size:
+        raise ValueError(f"position {position} outside the block table's {block_table.numel() * block_size} slots")
+    if q_out is None:
+        q_out = torch.empty((1, heads, 1, head_dim), dtype=dtype, device=kl.device)
+    elif q_out.numel() != dim or not q_out.is_contiguous() or q_out.dtype != dtype:
+        raise ValueError(f"q_out must hold {dim} contiguous {dtype} values")
+    _native.check(
+        _native.lib().mie_qkv_append(
+            x.data_ptr(), _native.ptr(norm_weight), _native.ptr(norm_bias), float(norm_eps),
+            in_proj_weight.data_ptr(), _native.ptr(in_proj_bias), dim,
+            kl.data_ptr(), vl.data_ptr(), kl.stride(0), kl.stride(1), nb,
+            block_table.data_ptr(), block_table.numel(), _native.ptr(position_dev), int(position),
+            q_out.data_ptr(), heads, head_dim, block_size,
+            _native.dtype_code(dtype), _native.stream_of(kl),
+        ),
+        "mie_qkv_append",
+    )
+    return q_out.view(1, heads, 1, head_dim)

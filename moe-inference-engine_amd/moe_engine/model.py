@@ -125,6 +125,12 @@ class BlockAllocator:
                 self.k_pool.stride(2),  # head stride, elements
                 _native.DTYPE_CODES[dtype],
             )
+        # One-token decode projects QKV straight into the pools
+        # (mie_qkv_append) when the model width and dtype are built; set to
+        # False to run the reference's projection + append sequence instead.
+        self.fuse_qkv = self._launch is not None and kv_ops.qkv_append_supported(
+            config.num_heads * config.head_dim, dtype
+        )
         self.free_blocks = list(range(num_blocks))
 
     def allocate(self) -> int:
@@ -243,6 +249,32 @@ class PagedKVCache:
         alloc.k_pool[layer_idx, blocks, :, slots] = k[0].transpose(0, 1)
         alloc.v_pool[layer_idx, blocks, :, slots] = v[0].transpose(0, 1)
 
+    def write_projected(self, layer_idx, position, x, in_proj_weight, in_proj_bias, norm=None):
+        """One decode token: q, k, v = in_proj(norm(x)) with k, v stored at
+        `position` (reference model.py:228-234 then :167-178) in one launch
+        (mie_qkv_append).  Returns q [1, H, 1, D].  The caller has checked that
+        the allocator's `fuse_qkv` applies and that x and the parameters share
+        the pools' dtype and device."""
+        alloc = self.allocator
+        if self.graph_pos is None:
+            self._reserve(position + 1)
+        layer_bytes, sblk, shead, code = alloc._launch
+        off = layer_idx * layer_bytes
+        q = torch.empty((1, alloc.num_heads, 1, alloc.head_dim), dtype=alloc.k_pool.dtype, device=x.device)
+        rc = _native.lib().mie_qkv_append(
+            x.data_ptr(),
+            None if norm is None else _native.ptr(norm.weight),
+            None if norm is None else _native.ptr(norm.bias),
+            1e-5 if norm is None else float(norm.eps),
+            in_proj_weight.data_ptr(), _native.ptr(in_proj_bias), alloc.num_heads * alloc.head_dim,
+            alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off, sblk, shead, alloc.num_blocks,
+            self.block_table_device.data_ptr(), alloc.num_blocks, _native.ptr(self.graph_pos), position,
+            q.data_ptr(), alloc.num_heads, alloc.head_dim, alloc.block_size, code, _native.stream_of(x),
+        )
+        if rc:
+            _native.check(rc, "mie_qkv_append")
+        return q
+
     def read(self, layer_idx, length):
         """Contiguous K, V [1, H, length, D] of logical positions 0..length-1."""
         alloc = self.allocator
@@ -276,6 +308,37 @@ class CachedAttention(nn.Module):
         self.out_proj = nn.Linear(dim, dim)
         nn.init.xavier_uniform_(self.in_proj_weight)
         nn.init.zeros_(self.in_proj_bias)
+
+    def fused_decode(self, x, norm, cache, layer_idx, position: int):
+        """attention(norm(x)) for one decode token with the QKV projection
+        stored straight into the paged pools (mie_qkv_append), or None when
+        that path does not apply (then the caller runs forward(norm(x), ...)).
+
+        Applies to a paged cache on a ROCm device whose decode runs the direct
+        kernel, a float32 / bfloat16 model of a built width, and a plain
+        LayerNorm; results equal forward()'s to float32 rounding."""
+        alloc = getattr(cache, "allocator", None)
+        if (
+            position <= 0
+            or alloc is None
+            or not getattr(alloc, "fuse_qkv", False)
+            or cache.attention_mode == "gather"
+            or x.shape[:2] != (1, 1)
+            or not x.is_contiguous()
+            or x.dtype != alloc.k_pool.dtype
+            or x.device != alloc.k_pool.device
+            or self.in_proj_weight.dtype != x.dtype
+            or not isinstance(norm, nn.LayerNorm)
+            or norm.weight is None
+            or norm.weight.dtype != x.dtype
+            or (norm.bias is not None and norm.bias.dtype != x.dtype)
+            or tuple(norm.normalized_shape) != (x.shape[-1],)
+            or not paged_attention.is_supported(x, self.head_dim)
+        ):
+            return None
+        q = cache.write_projected(layer_idx, position, x, self.in_proj_weight, self.in_proj_bias, norm)
+        out = paged_attention.decode(q, cache, layer_idx, context_len=position + 1)
+        return self.out_proj(out.transpose(1, 2).reshape(1, 1, x.shape[-1]))
 
     def forward(self, x, cache, layer_idx, position: int):
         batch, seq_len, dim = x.shape
@@ -486,7 +549,10 @@ class TransformerMoEBlock(nn.Module):
         self.moe_norm = nn.LayerNorm(config.hidden_dim)
 
     def forward(self, x, cache, layer_idx, position):
-        x = x + self.attention(self.attn_norm(x), cache, layer_idx, position)
+        attn = self.attention.fused_decode(x, self.attn_norm, cache, layer_idx, position)
+        if attn is None:
+            attn = self.attention(self.attn_norm(x), cache, layer_idx, position)
+        x = x + attn
         normed = self.moe_norm(x)
         return x + self.moe(normed, decode=position > 0 and normed.shape[1] == 1)
 

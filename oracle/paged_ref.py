@@ -110,6 +110,38 @@ def split_attention_fp64(q, k, v, partition, scale=None):
     return (w[:, :, None] * accs).sum(axis=0) / (w * ls).sum(axis=0)[:, None]
 
 
+# ---- QKV projection of a decode token (model.py:228-234, 478-481) ----------
+
+
+def qkv_project_fp64(x, in_proj_weight, in_proj_bias, heads, norm_weight=None, norm_bias=None, eps=1e-5,
+                     round_norm=None):
+    """q, k, v [H, D] of one token, in float64.
+
+    The block normalises x (attn_norm, a LayerNorm: (x - mean) / sqrt(var + eps)
+    * w + b with the biased variance) when norm_weight is given, then the
+    attention projects it with the packed in_proj (model.py:228-229) and splits
+    the 3*dim outputs into q, k, v in that order, each viewed [H, D]
+    (model.py:230-234).  `round_norm`, when given, maps the normalised vector
+    to the values the model feeds the projection (a bf16 model rounds the norm
+    output to bf16).
+    """
+    y = to_f64(x).reshape(-1)
+    dim = y.shape[0]
+    if norm_weight is not None:
+        mean = y.mean()
+        var = ((y - mean) ** 2).mean()
+        y = (y - mean) / math.sqrt(var + eps) * to_f64(norm_weight)
+        if norm_bias is not None:
+            y = y + to_f64(norm_bias)
+    if round_norm is not None:
+        y = round_norm(y)
+    qkv = to_f64(in_proj_weight) @ y
+    if in_proj_bias is not None:
+        qkv = qkv + to_f64(in_proj_bias)
+    q, k, v = (qkv[i * dim : (i + 1) * dim].reshape(heads, dim // heads) for i in range(3))
+    return q, k, v
+
+
 def gather_sdpa(q, k_pool, v_pool, layer, block_table, context_len):
     """The reference's gather decode path on the CPU: PagedKVCache.read
     (model.py:186-201) then scaled_dot_product_attention (model.py:265-266).

@@ -259,3 +259,68 @@ def test_reserve_rolls_back_on_exhaustion():
         ref.reserve(table, alloc, 8, 4)
     assert table == [] and alloc.free_blocks == [0]
     assert ref.reserve(table, alloc, 4, 4) == [0]
+
+
+# ---- qkv_project_fp64 (model.py:228-234, the block's attn_norm) -------------
+
+
+def torch_qkv64(x, w, b, heads, nw, nb, eps=1e-5):
+    """torch's own LayerNorm and linear in float64, split as CachedAttention does."""
+    x = torch.from_numpy(np.asarray(x, dtype=np.float64))
+    dim = x.numel()
+    y = F.layer_norm(x, (dim,), torch.from_numpy(nw), torch.from_numpy(nb), eps) if nw is not None else x
+    qkv = F.linear(y, torch.from_numpy(w), torch.from_numpy(b) if b is not None else None)
+    return tuple(t.view(heads, dim // heads).numpy() for t in qkv.chunk(3))
+
+
+@pytest.mark.parametrize("norm", [False, True])
+@pytest.mark.parametrize("heads,head_dim", [(2, 8), (12, 64), (3, 5)])
+def test_qkv_projection_matches_torch_float64(norm, heads, head_dim):
+    dim = heads * head_dim
+    x, w, b = rand((dim,), 30) * 3 + 0.5, rand((3 * dim, dim), 31), rand((3 * dim,), 32)
+    nw, nb = (rand((dim,), 33) + 1.0, rand((dim,), 34)) if norm else (None, None)
+    got = ref.qkv_project_fp64(x, w, b, heads, nw, nb)
+    for g, want in zip(got, torch_qkv64(x, w, b, heads, nw, nb)):
+        np.testing.assert_allclose(g, want, rtol=0, atol=1e-12)
+
+
+def test_qkv_projection_known_answers():
+    heads, head_dim = 3, 4
+    dim = heads * head_dim
+    x = np.arange(dim, dtype=np.float64) - 2.5
+    eye = np.eye(dim)
+    # Stacked [I; 2I; 3I] and no bias: q = x, k = 2x, v = 3x, head h = x[h*D:(h+1)*D].
+    q, k, v = ref.qkv_project_fp64(x, np.concatenate([eye, 2 * eye, 3 * eye]), None, heads)
+    np.testing.assert_array_equal(q, x.reshape(heads, head_dim))
+    np.testing.assert_array_equal(k, 2 * x.reshape(heads, head_dim))
+    np.testing.assert_array_equal(v, 3 * x.reshape(heads, head_dim))
+    # A constant x normalises to the norm bias alone.
+    nb = np.linspace(-1, 1, dim)
+    q, _, _ = ref.qkv_project_fp64(np.full(dim, 7.0), np.concatenate([eye] * 3), None, heads, np.full(dim, 5.0), nb)
+    np.testing.assert_allclose(q.reshape(-1), nb, rtol=0, atol=1e-12)
+
+
+def _qkv_unbiased_variance(x, w, b, heads, nw, nb):
+    y = (x - x.mean()) / math.sqrt(x.var(ddof=1) + 1e-5) * nw + nb
+    return ref.qkv_project_fp64(y, w, b, heads)
+
+
+def _qkv_k_v_swapped(x, w, b, heads, nw, nb):
+    q, k, v = ref.qkv_project_fp64(x, w, b, heads, nw, nb)
+    return q, v, k
+
+
+def _qkv_heads_transposed(x, w, b, heads, nw, nb):
+    q, k, v = ref.qkv_project_fp64(x, w, b, heads, nw, nb)
+    d = q.shape[1]
+    return tuple(t.reshape(-1).reshape(d, heads).T for t in (q, k, v))
+
+
+@pytest.mark.parametrize("broken", [_qkv_unbiased_variance, _qkv_k_v_swapped, _qkv_heads_transposed])
+def test_qkv_pin_rejects_planted_mistakes(broken):
+    heads, dim = 4, 32
+    x, w, b = rand((dim,), 40), rand((3 * dim, dim), 41), rand((3 * dim,), 42)
+    nw, nb = rand((dim,), 43) + 1.0, rand((dim,), 44)
+    want = torch_qkv64(x, w, b, heads, nw, nb)
+    got = broken(x, w, b, heads, nw, nb)
+    assert not all(np.allclose(g, t, rtol=0, atol=1e-6) for g, t in zip(got, want))
