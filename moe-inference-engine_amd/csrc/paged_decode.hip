@@ -58,7 +58,6 @@ constexpr int kWindow = 64;          // FAST path: block ids held one per lane
 // work per (sequence, head).  Fitted on MI355X with the flat work list:
 // config 4 (64 x U[512, 8192]) and 64 x 4352 are fastest at 512 tokens,
 // 8 x 131072 at 1024, 1 x 131072 at 512.
-constexpr int kSinglePassCtx = 256;  // auto plan: one partition up to this context
 constexpr int kTargetItems = 12288;  // auto plan: wavefronts to stay below
 constexpr int kMaxParts = 256;       // auto plan: partitions per sequence to stay below
 // Occupancy floor for the main kernels: every built shape fits 4 waves/SIMD
@@ -67,6 +66,24 @@ constexpr int kMinWaves = 4;
 // Batches up to this size use the flat work list (its per-workgroup scan reads
 // ceil(B / 64) chunks of lengths); larger batches use the grid form.
 constexpr int kFlatMaxBatch = 512;
+// Workgroup form: one workgroup of kSplitWaves waves per (sequence, head).
+// Each wave reads its slice as a serial chain of tiles (~2 us per tile when
+// latency-bound), so the automatic plan takes this form for at most
+// kWgMaxRows (sequence, head) rows when every slice is short (max_ctx <=
+// kWgShortCtx: at most 64 tokens per wave) or when there are enough rows to
+// fill the GPU with workgroups (rows >= kWgMinRows, max_ctx <= kWgMaxCtx).
+// Measured on MI355X (per call, graph replays), workgroup form vs the
+// partition plan: 1 x 96 tokens 3.9 vs 6.8 us, 1 x 512 5.4 vs 7.0, 21 x 1000
+// 13.6 vs 16.3, 16 x 4096 33.5 vs 35.3, 64 x 2048 68.7 vs 73.3, 64 x 4096
+// 124.5 vs 130.7, 16 x 8192 62.3 vs 72.3, config 4 (64 x U[512, 8192])
+// 127.4 vs 130.9; but 1 x 2048 10.6 vs 7.3, 4 x 4096 25 vs 14 and 128 x 512
+// (1536 rows, one workgroup per CU at a time) 45.7 vs 42.3.  Below kWgMinRows
+// rows a long context would leave CUs idle.
+constexpr int kSplitWaves = 16;
+constexpr int kWgShortCtx = 1024;
+constexpr int kWgMinRows = 128;
+constexpr int kWgMaxRows = 1024;
+constexpr int kWgMaxCtx = 8192;
 
 constexpr int next_pow2(int x) {
   int p = 1;
@@ -178,21 +195,23 @@ __device__ __forceinline__ void store_out(char* base, int64_t elem_off, const fl
   }
 }
 
-// One work item: sequence b (ctx tokens, ctx > 0), head h, partition `part`,
-// computed by one full wavefront.
+// Online softmax of sequence b, head h over tokens [t_begin, t_end) (t_begin
+// a multiple of the tile; for FAST the range spans at most kWindow blocks),
+// computed by one full wavefront.  Returns the range's state merged over the
+// wave: m (running max, log2 units) and l are uniform across lanes; acc holds
+// the head_dim slice jl = lane % LPT; bad is wave-uniform and set when a block
+// id outside the pool was met.
 template <int DT, int D, bool FAST>
-__device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, int part, int ctx, int lane) {
+__device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, int t_begin, int t_end, int lane,
+                                             float& m, float& l, float* acc, bool& bad) {
   using G = Geometry<DT, D>;
   constexpr int ELT = G::ELT, VEC = G::VEC, NW = G::NW, LPT = G::LPT, TPL = G::TPL;
   constexpr int ROWS = G::ROWS, TILE = G::TILE;
   constexpr int64_t ROW_BYTES = static_cast<int64_t>(D) * ELT;
 
-  const int nparts = (ctx + (1 << a.part_shift) - 1) >> a.part_shift;
   const int g = lane / LPT;   // token group within a wave load
   const int jl = lane % LPT;  // slice of the head_dim row
   const bool jv = jl < G::NV;
-  const int t_begin = part << a.part_shift;
-  const int t_end = min(ctx, t_begin + (1 << a.part_shift));
 
   // Query slice for this lane: bf16 stays packed for v_dot2; f32 is pre-scaled.
   Words<NW> qw;
@@ -211,7 +230,7 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
   const char* vbase = a.v + lane_off;
   const int64_t blk_bytes = a.kv_sblk * ELT;
 
-  bool bad = false;
+  bad = false;
   int fb = 0;
   int32_t ids = 0;
   if constexpr (FAST) {  // the partition's block ids, one per lane
@@ -256,8 +275,8 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
     }
   };
 
-  float m = -INFINITY, l = 0.f;
-  float acc[VEC];
+  m = -INFINITY;
+  l = 0.f;
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
 
@@ -337,8 +356,24 @@ __device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, i
     m = mn;
   }
   if constexpr (!FAST) bad = __any(bad);
+}
 
-  if (g != 0 || !jv) return;
+// One work item: sequence b (ctx tokens, ctx > 0), head h, partition `part`,
+// computed by one full wavefront.
+template <int DT, int D, bool FAST>
+__device__ __forceinline__ void decode_item(const DecodeArgs& a, int b, int h, int part, int ctx, int lane) {
+  using G = Geometry<DT, D>;
+  constexpr int VEC = G::VEC;
+  const int nparts = (ctx + (1 << a.part_shift) - 1) >> a.part_shift;
+  const int t_begin = part << a.part_shift;
+  const int t_end = min(ctx, t_begin + (1 << a.part_shift));
+  float m, l, acc[VEC];
+  bool bad;
+  attend_range<DT, D, FAST>(a, b, h, t_begin, t_end, lane, m, l, acc, bad);
+
+  const int g = lane / G::LPT;
+  const int jl = lane % G::LPT;
+  if (g != 0 || jl >= G::NV) return;
   if (nparts == 1) {
     const float inv = bad ? NAN : 1.f / l;
     float val[VEC];
@@ -406,6 +441,7 @@ void paged_decode_flat_kernel(DecodeArgs a, int batch, int head_groups) {
   const int item = blockIdx.x;
   const int shift = a.part_shift;
   int base = 0;  // items of the sequences before this chunk
+  int b = -1, part = 0, hg = 0, seq_ctx_len = 0;
   for (int c0 = 0; c0 < batch; c0 += 64) {
     const int bb = c0 + lane;
     const int ctx = bb < batch ? seq_ctx(a, bb) : 0;
@@ -419,24 +455,92 @@ void paged_decode_flat_kernel(DecodeArgs a, int batch, int head_groups) {
     }
     const int chunk_items = __shfl(incl, 63);
     if (item < base + chunk_items) {
+      // The item's coordinates are wave-uniform; readfirstlane tells the
+      // compiler so, keeping them (and every token index and block address
+      // derived from them) in scalar registers.
       const int owner = __ffsll(static_cast<unsigned long long>(__ballot(incl > item - base))) - 1;
-      const int local = item - base - (__shfl(incl, owner) - __shfl(n, owner));
-      const int seq_parts = __shfl(parts, owner);
-      const int hg = local / seq_parts;
-      const int part = local - hg * seq_parts;
-      const int h = hg * kWaves + wave;
-      if (h >= a.H) return;
-      const int b = c0 + owner;
-      const int seq_ctx_len = __shfl(ctx, owner);
-      if (seq_ctx_len == 0) {
-        zero_item<DT, D>(a, b, h, lane);
-        return;
-      }
-      decode_item<DT, D, FAST>(a, b, h, part, seq_ctx_len, lane);
-      return;
+      const int local =
+          __builtin_amdgcn_readfirstlane(item - base - (__shfl(incl, owner) - __shfl(n, owner)));
+      const int seq_parts = __builtin_amdgcn_readfirstlane(__shfl(parts, owner));
+      hg = local / seq_parts;
+      part = local - hg * seq_parts;
+      b = c0 + owner;
+      seq_ctx_len = __builtin_amdgcn_readfirstlane(__shfl(ctx, owner));
+      break;
     }
     base += chunk_items;
   }
+  // The scan's registers are dead from here on.
+  const int h = hg * kWaves + wave;
+  if (b < 0 || h >= a.H) return;
+  if (seq_ctx_len == 0) {
+    zero_item<DT, D>(a, b, h, lane);
+    return;
+  }
+  decode_item<DT, D, FAST>(a, b, h, part, seq_ctx_len, lane);
+}
+
+// Workgroup form for batches of few (sequence, head) rows: grid = (H, batch),
+// one workgroup of kSplitWaves waves per (sequence, head).  Wave w takes the
+// w-th tile-aligned slice of the context, so a short context is read by 16
+// waves at once instead of one; the waves' (max, sum, acc) states are merged
+// through LDS and the workgroup writes the output: one launch, no workspace.
+template <int DT, int D, bool FAST>
+__global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
+void paged_decode_wg_kernel(DecodeArgs a) {
+  using G = Geometry<DT, D>;
+  constexpr int VEC = G::VEC;
+  __shared__ float s_m[kSplitWaves], s_l[kSplitWaves];
+  __shared__ float s_acc[kSplitWaves][D];
+  __shared__ int s_bad;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int ctx = seq_ctx(a, b);
+  const int per_wave = (ctx + kSplitWaves - 1) / kSplitWaves;
+  const int chunk = (per_wave + G::TILE - 1) / G::TILE * G::TILE;
+  const int t_begin = min(ctx, wave * chunk);
+  const int t_end = min(ctx, t_begin + chunk);
+  if (threadIdx.x == 0) s_bad = 0;
+  float m = -INFINITY, l = 0.f, acc[VEC];
+#pragma unroll
+  for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
+  bool bad = false;
+  if (t_begin < t_end) attend_range<DT, D, FAST>(a, b, h, t_begin, t_end, lane, m, l, acc, bad);
+  __syncthreads();  // s_bad is cleared
+  const int jl = lane % G::LPT;
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+    if (bad) s_bad = 1;
+  }
+  if (lane / G::LPT == 0 && jl < G::NV) {
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) s_acc[wave][jl * VEC + i] = acc[i];
+  }
+  __syncthreads();
+  // Threads 0 .. D/4-1 merge four output elements each.
+  const int col = threadIdx.x * 4;
+  if (col >= D) return;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; ++w) mx = fmaxf(mx, s_m[w]);
+  const float mr = mx == -INFINITY ? 0.f : mx;
+  float lt = 0.f;
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int w = 0; w < kSplitWaves; ++w) {
+    const float wt = mie::fast_exp2(s_m[w] - mr);
+    lt += s_l[w] * wt;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] += s_acc[w][col + i] * wt;
+  }
+  // No keys: zeros, as scaled_dot_product_attention returns for an empty set.
+  const float inv = ctx == 0 ? 0.f : (s_bad ? NAN : 1.f / lt);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] *= inv;
+  store_out<DT, 4>(a.out, b * a.o_sb + h * a.o_sh + col, o, a.out_f32);
 }
 
 // Merge the partition partials of one (sequence, head) in one pass:
@@ -550,6 +654,7 @@ struct Plan {
   int32_t max_parts;
   int64_t ws_bytes;
   bool fast;
+  bool wg;  // workgroup form (one workgroup per (sequence, head), no merge launch)
 };
 
 int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size, int32_t max_ctx,
@@ -564,6 +669,29 @@ int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_s
                      num_heads, block_size, max_ctx);
   const bool fast_blocks = is_pow2(block_size) && block_size % ks.tpl == 0;
   const int64_t fast_cap = static_cast<int64_t>(kWindow) * block_size;  // FAST: <= kWindow blocks
+  const int64_t rows = static_cast<int64_t>(batch) * num_heads;
+  const bool wg = requested == -1 ||
+                  (requested == 0 && rows <= kWgMaxRows &&
+                   (max_ctx <= kWgShortCtx || (rows >= kWgMinRows && max_ctx <= kWgMaxCtx)));
+  if (requested < -1)
+    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: partition_tokens %d (0 = automatic, -1 = workgroup form)",
+                     requested);
+  if (wg) {
+    // One partition per sequence, split among the workgroup's waves in
+    // tile-aligned slices.
+    int64_t part = ks.tile;
+    while (part < max_ctx && part < (int64_t{1} << 30)) part <<= 1;
+    const int64_t per_wave = (static_cast<int64_t>(max_ctx) + kSplitWaves - 1) / kSplitWaves;
+    const int64_t slice = (per_wave + ks.tile - 1) / ks.tile * ks.tile;
+    out->part = static_cast<int32_t>(part);
+    out->max_parts = 1;
+    out->ws_bytes = 0;
+    // A slice starts on a tile boundary, not necessarily a block boundary, so it
+    // touches at most (slice + block_size - 2) / block_size + 1 blocks.
+    out->fast = fast_blocks && slice + block_size <= fast_cap;
+    out->wg = true;
+    return MIE_OK;
+  }
   int64_t part;
   if (requested > 0) {
     if (!is_pow2(requested) || requested % ks.tile != 0)
@@ -572,12 +700,8 @@ int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_s
                        "of the %d-token tile",
                        requested, ks.tile);
     part = requested;
-  } else if (max_ctx <= kSinglePassCtx) {
-    part = ks.tile;
-    while (part < max_ctx) part <<= 1;
   } else {
     part = ks.tile;
-    const int64_t rows = static_cast<int64_t>(batch) * num_heads;
     while (part < max_ctx && (rows * ((max_ctx + part - 1) / part) > kTargetItems ||
                               (max_ctx + part - 1) / part > kMaxParts))
       part <<= 1;
@@ -590,13 +714,24 @@ int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_s
   out->max_parts = static_cast<int32_t>(max_parts);
   out->ws_bytes = max_parts > 1 ? static_cast<int64_t>(batch) * num_heads * max_parts * (head_dim + 2) * 4 : 0;
   out->fast = fast_blocks && part <= fast_cap;
+  out->wg = false;
   return MIE_OK;
 }
 
-// flat_items > 0: the flat work list with that many workgroups; 0: the grid form.
+// wg: the workgroup form; else flat_items > 0: the flat work list with that
+// many workgroups; 0: the grid form.
 template <int DT, int D>
-int32_t launch(DecodeArgs& a, int batch, bool fast, int64_t flat_items, hipStream_t st) {
+int32_t launch(DecodeArgs& a, int batch, bool fast, bool wg, int64_t flat_items, hipStream_t st) {
   const int head_groups = (a.H + kWaves - 1) / kWaves;
+  if (wg) {
+    const dim3 grid(a.H, batch);
+    if (fast) {
+      paged_decode_wg_kernel<DT, D, true><<<grid, 64 * kSplitWaves, 0, st>>>(a);
+    } else {
+      paged_decode_wg_kernel<DT, D, false><<<grid, 64 * kSplitWaves, 0, st>>>(a);
+    }
+    return mie::check_launch("paged_decode_wg_kernel");
+  }
   if (flat_items > 0) {
     const dim3 grid(static_cast<uint32_t>(flat_items));
     if (fast) {
@@ -618,12 +753,12 @@ int32_t launch(DecodeArgs& a, int batch, bool fast, int64_t flat_items, hipStrea
   return mie::check_launch("paged_decode_reduce_kernel");
 }
 
-int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, int64_t flat_items,
+int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, bool wg, int64_t flat_items,
                  hipStream_t st) {
-#define MIE_LAUNCH_CASE(DD)                                                                     \
-  case DD:                                                                                      \
-    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, flat_items, st)   \
-                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, flat_items, st);
+#define MIE_LAUNCH_CASE(DD)                                                                         \
+  case DD:                                                                                          \
+    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, wg, flat_items, st)   \
+                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, wg, flat_items, st);
   switch (head_dim) {
     MIE_FOR_EACH_HEAD_DIM(MIE_LAUNCH_CASE)
     default: return mie::fail(MIE_ERR_UNSUPPORTED, "mie_paged_decode: head_dim %d not built", head_dim);
@@ -671,7 +806,7 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
   if (!ctx_lens && (ctx_len < 0 || ctx_len > max_ctx_len))
     return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: ctx_len %d outside [0, max_ctx_len=%d]", ctx_len,
                      max_ctx_len);
-  if (batch > 65535 || num_heads > 65535 * kWaves)
+  if (batch > 65535 || num_heads > 65535 * kWaves || (p.wg && num_heads > 65535))
     return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: batch or heads too large");
   if (out_dtype != MIE_DTYPE_F32 && out_dtype != dtype)
     return mie::fail(MIE_ERR_UNSUPPORTED, "mie_paged_decode: out_dtype %d must be f32 or the input dtype",
@@ -749,5 +884,5 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
     }
     if (flat_items > 0x7fffffff) flat_items = 0;  // beyond a 1-D grid: use the grid form
   }
-  return dispatch(dtype, head_dim, a, batch, p.fast, flat_items, static_cast<hipStream_t>(stream));
+  return dispatch(dtype, head_dim, a, batch, p.fast, p.wg, flat_items, static_cast<hipStream_t>(stream));
 }

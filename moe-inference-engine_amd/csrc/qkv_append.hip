@@ -126,30 +126,51 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
     }
   }
 
-  // 2. x (normalised when ln_w is given) into LDS as float, rounded as the
-  //    reference's norm output is.
-  float s = 0.f;
-  for (int i = threadIdx.x; i < dim; i += 256) {
-    const float v = E::load(a.x, i);
-    y[i] = v;
-    s += v;
+  // 2. Every other global read is issued now too, so the launch waits on one
+  //    round trip: x and the norm parameters (thread t holds elements t,
+  //    t + 256, ...; XPT of them cover dim) and the bias of the row this lane
+  //    will store.
+  constexpr int XPT = NCH * EPV / 4;
+  float xv[XPT], gw[XPT], gb[XPT];
+#pragma unroll
+  for (int k = 0; k < XPT; ++k) {
+    const int i = threadIdx.x + k * 256;
+    xv[k] = i < dim ? E::load(a.x, i) : 0.f;
+    gw[k] = a.ln_w && i < dim ? E::load(a.ln_w, i) : 0.f;
+    gb[k] = a.ln_b && i < dim ? E::load(a.ln_b, i) : 0.f;
   }
+  const int r_store = r0 + ((lane >> 5) & 1);
+  const float bias = a.b_in && (lane & 31) == 0 && r_store < rows ? E::load(a.b_in, r_store) : 0.f;
+
+  // 3. x, normalised when ln_w is given and rounded as the reference's norm
+  //    output is, into LDS as float.
   if (a.ln_w) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) s += xv[k];  // zero past dim
     const float mean = block_sum(s, red) / dim;
     float q = 0.f;
-    for (int i = threadIdx.x; i < dim; i += 256) {
-      const float d = y[i] - mean;
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const float d = threadIdx.x + k * 256 < dim ? xv[k] - mean : 0.f;
       q = fmaf(d, d, q);
     }
     const float rstd = rsqrtf(block_sum(q, red) / dim + a.ln_eps);
-    for (int i = threadIdx.x; i < dim; i += 256) {
-      const float b = a.ln_b ? E::load(a.ln_b, i) : 0.f;
-      y[i] = E::round((y[i] - mean) * rstd * E::load(a.ln_w, i) + b);
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int i = threadIdx.x + k * 256;
+      if (i < dim) y[i] = E::round((xv[k] - mean) * rstd * gw[k] + gb[k]);
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < XPT; ++k) {
+      const int i = threadIdx.x + k * 256;
+      if (i < dim) y[i] = xv[k];
     }
   }
   __syncthreads();
 
-  // 3. Two dot products per wave.
+  // 4. Two dot products per wave.
   float sa = 0.f, sb = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -171,11 +192,11 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   float t = (hi ? sb : sa) + __shfl_xor(hi ? sa : sb, 32);
   t = mie::group_sum<32>(t);
   if ((lane & 31) != 0) return;
-  const int r = r0 + (hi ? 1 : 0);
+  const int r = r_store;
   if (r >= rows) return;
 
-  // 4. Store: q, or the K / V row of the token's pool slot.
-  const float out = t + (a.b_in ? E::load(a.b_in, r) : 0.f);
+  // 5. Store: q, or the K / V row of the token's pool slot.
+  const float out = t + bias;
   if (r < dim) {
     E::store(a.q_out, r, out);
     return;

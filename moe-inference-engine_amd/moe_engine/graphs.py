@@ -12,7 +12,8 @@ in (the previous step's argmax, written to a fixed buffer), the position of the
 new token and the context length (incremented by the graph).  The paged cache
 is put in graph mode (PagedKVCache.graph_pos / graph_ctx), so the append and
 the decode read those device values and the decode launch is sized for the
-pool's capacity.  The host keeps only the block bookkeeping: before each
+pool's capacity (partition_tokens 0 lets the library plan it for that bound:
+one workgroup per head for pools of up to 4096 tokens).  The host keeps only the block bookkeeping: before each
 replay it reserves the block the new token needs (one host-to-device copy of
 one block id every block_size tokens) - the replay itself never allocates.
 
@@ -36,7 +37,7 @@ class GraphedDecoder:
     the next replay: clone it if it must outlive the step.
     """
 
-    def __init__(self, model, cache, partition_tokens=128):
+    def __init__(self, model, cache, partition_tokens=0):
         if not isinstance(cache, PagedKVCache) or cache.attention_mode == "gather":
             raise ValueError("graph decode needs a paged cache whose attention mode is 'auto' or 'direct'")
         weight = model.token_embedding.weight
@@ -131,7 +132,7 @@ class GraphedDecoder:
 
 
 @torch.no_grad()
-def generate_graphed(model, token_ids, max_new_tokens, cache, partition_tokens=128):
+def generate_graphed(model, token_ids, max_new_tokens, cache, partition_tokens=0):
     """Greedy generation with the same results and stopping rules as
     Model.generate(..., temperature=0, cache=cache) (model.py:567-621), with
     decode steps replayed from a HIP graph."""

@@ -59,6 +59,18 @@ def test_decode_plan_rejects_bad_partition_and_unbuilt_shapes():
 
     with pytest.raises(RuntimeError, match="partition_tokens"):
         _native.decode_plan(1, 12, 64, 16, 4096, torch.bfloat16, 100)
+    with pytest.raises(RuntimeError, match="partition_tokens"):
+        _native.decode_plan(1, 12, 64, 16, 4096, torch.bfloat16, -2)
+
+
+def test_decode_plan_workgroup_form_needs_no_workspace():
+    import torch
+
+    # -1 forces one workgroup per (sequence, head): one partition, no workspace.
+    part, ws = _native.decode_plan(8, 12, 64, 16, 131072, torch.bfloat16, -1)
+    assert part >= 131072 and ws == 0
+    # Automatic: short contexts take it too.
+    assert _native.decode_plan(1, 12, 64, 16, 1024, torch.bfloat16, 0)[1] == 0
     assert not _native.decode_supported(72, torch.bfloat16)
     assert not _native.decode_supported(64, torch.float64)
     assert _native.decode_supported(96, torch.float32) and _native.decode_supported(4, torch.bfloat16)

@@ -210,7 +210,7 @@ def test_partition_sizes_agree(dtype):
     while p <= 8192:
         sizes.append(p)
         p *= 4
-    for part in sizes + [0]:
+    for part in sizes + [0, -1]:  # -1: one workgroup per (sequence, head)
         print_case("partition", dtype, part)
         check_workload(w, out_f32_atol=atol, partition_tokens=part)
 
@@ -228,14 +228,43 @@ def test_ragged_batch_with_empty_sequence_and_block_size_3():
     np.testing.assert_allclose(got[1:].cpu().numpy(), want, rtol=0, atol=1e-5)
 
 
+@pytest.mark.parametrize("block_size", [3, 16])
+def test_workgroup_form_ragged_batch_with_empty_sequence(block_size):
+    """The workgroup form (one workgroup of 16 waves per (sequence, head),
+    merged in LDS): empty, single-token and ragged contexts, through the fast
+    block-id path (block 16) and the per-row division (block 3)."""
+    lens = [0, 1, 5, 17, 48, 700, 4096]
+    w = make_workload(lens, block_size=block_size, dtype=torch.float32, seed=12, heavy_fraction=0.01)
+    got = paged_attention.decode_batched(
+        w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, partition_tokens=-1
+    )
+    assert torch.equal(got[0], torch.zeros_like(got[0]))
+    np.testing.assert_allclose(got[1:].cpu().numpy(), oracle_outputs(w, range(1, len(lens))), rtol=0, atol=1e-5)
+
+
+def test_automatic_plan_chooses_the_form():
+    """The automatic plan takes the workgroup form (one launch, no workspace)
+    for few (sequence, head) rows with contexts up to 4096 tokens."""
+    for batch, ctx in ((1, 96), (1, 1024), (21, 1000), (12, 4096), (64, 8192)):
+        part, ws = _native.decode_plan(batch, 12, 64, 16, ctx, torch.bfloat16, 0)
+        assert ws == 0 and part >= ctx, (batch, ctx)
+    # Few rows of longer contexts split into partitions across many waves.
+    for batch, ctx in ((1, 2048), (4, 4096), (64, 16384), (128, 8192)):
+        part, ws = _native.decode_plan(batch, 12, 64, 16, ctx, torch.bfloat16, 0)
+        assert ws > 0 and part < ctx, (batch, ctx)
+
+
 def test_out_of_range_block_id_yields_nan_without_touching_memory():
     """The kernel bounds-checks table entries: an id past the pool is never
     dereferenced and the affected sequence reports NaN; the others are exact."""
     w = make_workload([40, 40], block_size=16, dtype=torch.float32, seed=4)
     w.block_tables[1, 1] = w.k_pool.shape[1] + 5
-    got = paged_attention.decode_batched(w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, 40)
-    assert torch.isnan(got[1]).all()
-    np.testing.assert_allclose(got[0].cpu().numpy(), oracle_outputs(w, [0])[0], rtol=0, atol=1e-5)
+    for part in (0, -1, 16):  # automatic (the workgroup form here), forced, and split partitions
+        got = paged_attention.decode_batched(
+            w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, 40, partition_tokens=part
+        )
+        assert torch.isnan(got[1]).all(), part
+        np.testing.assert_allclose(got[0].cpu().numpy(), oracle_outputs(w, [0])[0], rtol=0, atol=1e-5)
 
 
 def test_decode_is_deterministic_and_leaves_pools_untouched():
