@@ -44,6 +44,8 @@
 // fits one partition is normalised and written by the first kernel.
 #include <math.h>
 
+#include <algorithm>
+
 #include "mie_common.h"
 
 namespace {
@@ -80,6 +82,7 @@ constexpr int kFlatMaxBatch = 512;
 // (1536 rows, one workgroup per CU at a time) 45.7 vs 42.3.  Below kWgMinRows
 // rows a long context would leave CUs idle.
 constexpr int kSplitWaves = 16;
+constexpr int kWgOrderMax = 1024;  // batches the workgroup form can dispatch longest first
 constexpr int kWgShortCtx = 1024;
 constexpr int kWgMinRows = 128;
 constexpr int kWgMaxRows = 1024;
@@ -480,14 +483,27 @@ void paged_decode_flat_kernel(DecodeArgs a, int batch, int head_groups) {
   decode_item<DT, D, FAST>(a, b, h, part, seq_ctx_len, lane);
 }
 
-// Workgroup form for batches of few (sequence, head) rows: grid = (H, batch),
-// one workgroup of kSplitWaves waves per (sequence, head).  Wave w takes the
-// w-th tile-aligned slice of the context, so a short context is read by 16
-// waves at once instead of one; the waves' (max, sum, acc) states are merged
-// through LDS and the workgroup writes the output: one launch, no workspace.
+// Workgroup form: grid = (H, batch), one workgroup of kSplitWaves waves per
+// (sequence, head).  Wave w takes the w-th tile-aligned slice of the context,
+// so a short context is read by 16 waves at once instead of one; the waves'
+// (max, sum, acc) states are merged through LDS and the workgroup writes the
+// output: one launch, no workspace.
+//
+// A workgroup's time grows with its sequence's length and a CU holds one such
+// workgroup at a time, so the order of dispatch sets the tail of a ragged
+// batch.  When the caller gives host lengths, row y of the grid takes
+// order.seq[y]: the sequences longest first (ties by index), which the
+// hardware dispatches first - config 4 runs ~2 % faster, a ragged 48 x
+// U[64, 8192] ~15 %.  Ranking on the device instead delays every workgroup's
+// start by a global load and two barriers, ~5 % on uniform batches.
+struct WgOrder {
+  int32_t n;  // 0: grid order
+  uint16_t seq[kWgOrderMax];
+};
+
 template <int DT, int D, bool FAST>
 __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
-void paged_decode_wg_kernel(DecodeArgs a) {
+void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   using G = Geometry<DT, D>;
   constexpr int VEC = G::VEC;
   __shared__ float s_m[kSplitWaves], s_l[kSplitWaves];
@@ -496,7 +512,7 @@ void paged_decode_wg_kernel(DecodeArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int h = blockIdx.x;
-  const int b = blockIdx.y;
+  const int b = order.n > 0 ? order.seq[blockIdx.y] : blockIdx.y;
   const int ctx = seq_ctx(a, b);
   const int per_wave = (ctx + kSplitWaves - 1) / kSplitWaves;
   const int chunk = (per_wave + G::TILE - 1) / G::TILE * G::TILE;
@@ -721,14 +737,15 @@ int32_t plan(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_s
 // wg: the workgroup form; else flat_items > 0: the flat work list with that
 // many workgroups; 0: the grid form.
 template <int DT, int D>
-int32_t launch(DecodeArgs& a, int batch, bool fast, bool wg, int64_t flat_items, hipStream_t st) {
+int32_t launch(DecodeArgs& a, int batch, bool fast, bool wg, const WgOrder& order, int64_t flat_items,
+               hipStream_t st) {
   const int head_groups = (a.H + kWaves - 1) / kWaves;
   if (wg) {
     const dim3 grid(a.H, batch);
     if (fast) {
-      paged_decode_wg_kernel<DT, D, true><<<grid, 64 * kSplitWaves, 0, st>>>(a);
+      paged_decode_wg_kernel<DT, D, true><<<grid, 64 * kSplitWaves, 0, st>>>(a, order);
     } else {
-      paged_decode_wg_kernel<DT, D, false><<<grid, 64 * kSplitWaves, 0, st>>>(a);
+      paged_decode_wg_kernel<DT, D, false><<<grid, 64 * kSplitWaves, 0, st>>>(a, order);
     }
     return mie::check_launch("paged_decode_wg_kernel");
   }
@@ -753,12 +770,12 @@ int32_t launch(DecodeArgs& a, int batch, bool fast, bool wg, int64_t flat_items,
   return mie::check_launch("paged_decode_reduce_kernel");
 }
 
-int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, bool wg, int64_t flat_items,
-                 hipStream_t st) {
-#define MIE_LAUNCH_CASE(DD)                                                                         \
-  case DD:                                                                                          \
-    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, wg, flat_items, st)   \
-                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, wg, flat_items, st);
+int32_t dispatch(int dtype, int head_dim, DecodeArgs& a, int batch, bool fast, bool wg, const WgOrder& order,
+                 int64_t flat_items, hipStream_t st) {
+#define MIE_LAUNCH_CASE(DD)                                                                                \
+  case DD:                                                                                                 \
+    return dtype == MIE_DTYPE_F32 ? launch<MIE_DTYPE_F32, DD>(a, batch, fast, wg, order, flat_items, st)   \
+                                  : launch<MIE_DTYPE_BF16, DD>(a, batch, fast, wg, order, flat_items, st);
   switch (head_dim) {
     MIE_FOR_EACH_HEAD_DIM(MIE_LAUNCH_CASE)
     default: return mie::fail(MIE_ERR_UNSUPPORTED, "mie_paged_decode: head_dim %d not built", head_dim);
@@ -884,5 +901,16 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
     }
     if (flat_items > 0x7fffffff) flat_items = 0;  // beyond a 1-D grid: use the grid form
   }
-  return dispatch(dtype, head_dim, a, batch, p.fast, p.wg, flat_items, static_cast<hipStream_t>(stream));
+  // Longest first for the workgroup form when host lengths are given.
+  WgOrder order{};
+  if (p.wg && ctx_lens && ctx_lens_host && batch > 1 && batch <= kWgOrderMax) {
+    for (int b = 0; b < batch; ++b) order.seq[b] = static_cast<uint16_t>(b);
+    auto len = [&](int b) {
+      const int c = ctx_lens_host[b];
+      return c < 0 ? 0 : (c > max_ctx_len ? max_ctx_len : c);
+    };
+    std::stable_sort(order.seq, order.seq + batch, [&](uint16_t x, uint16_t y) { return len(x) > len(y); });
+    order.n = batch;
+  }
+  return dispatch(dtype, head_dim, a, batch, p.fast, p.wg, order, flat_items, static_cast<hipStream_t>(stream));
 }
