@@ -11,8 +11,10 @@
  *                        and _paged_decode_kernel src/moe_engine/paged_attention.py:46-110
  *   mie_qkv_append    <- CachedAttention.forward's QKV projection and
  *                        cache.write for one decode token  src/moe_engine/model.py:228-247
+ *   mie_linear_residual <- out_proj + the block's residual add  src/moe_engine/model.py:268, :447
  *   mie_moe_route     <- fused_moe.route         src/moe_engine/fused_moe.py:274-309
  *   mie_moe_decode    <- fused_moe.decode        src/moe_engine/fused_moe.py:312-380
+ *   mie_moe_decode_block <- the block's x + moe(moe_norm(x)) for one token  src/moe_engine/model.py:446-449
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -66,7 +68,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 5
+#define MIE_ABI_VERSION 6
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -188,7 +190,7 @@ int32_t mie_paged_decode_supported(int32_t head_dim, int32_t dtype);
  * the model dtype, the projection accumulates in float32 and rounds once: the
  * reference's rounding points.  dim = num_heads * head_dim; x, the norm
  * parameters, w_in, b_in, q_out and the pools share `dtype` (f32 or bf16);
- * w_in is 16-byte aligned.  mie_qkv_append_supported(dim, dtype) says whether
+ * x, the norm parameters and w_in are 16-byte aligned.  mie_qkv_append_supported(dim, dtype) says whether
  * the shape is built (dim <= 2048 f32 / 4096 bf16, a multiple of 4 / 8).
  */
 int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias,
@@ -202,6 +204,23 @@ int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias
 
 /* 1 if mie_qkv_append is built for (dim, dtype), else 0. */
 int32_t mie_qkv_append_supported(int32_t dim, int32_t dtype);
+
+/*
+ * One-token linear layer with a residual add (the attention's out_proj and the
+ * block's `x + attention(...)`, model.py:268 and :447, in one launch):
+ *
+ *   out[r] = residual[r] + round(weight[r, :] . x + bias[r])     r < rows
+ *
+ * (out = weight . x + bias when residual is NULL; bias may be NULL).  weight is
+ * [rows, cols] row-major; x [cols] and weight 16-byte aligned; bias, residual and out
+ * [rows] share `dtype` (f32 or bf16); out may alias residual, not x.  The
+ * rounding points are the reference's: the projection is rounded to the model
+ * dtype, then the sum.  Built for the widths mie_qkv_append_supported(cols,
+ * dtype) accepts.
+ */
+int32_t mie_linear_residual(const void* x, const void* weight, const void* bias,
+                            const void* residual, void* out, int32_t rows, int32_t cols,
+                            int32_t dtype, void* stream);
 
 /*
  * Router and top-k of the fused MoE decode for ONE token, float32
@@ -234,14 +253,32 @@ int32_t mie_moe_route(const void* x, const void* router_weight, int32_t num_expe
  * canonical contiguous storages w1 [E, hidden, dim], b1 [E, hidden], w2 [E,
  * dim, hidden], b2 [E, dim]; hidden_act is [top_k, hidden], out [dim].  x, the
  * router weight, w1, w2 and hidden_act are 16-byte aligned; dim and hidden are
- * multiples of 4.  The routing outputs are those of mie_moe_route.  Three
- * launches on `stream`; nothing needs clearing beforehand.
+ * multiples of 4.  The routing outputs are those of mie_moe_route.  Two
+ * launches on `stream` (the W1 launch routes in every workgroup); nothing
+ * needs clearing beforehand.  dim <= 2048.
  */
 int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1,
                        const void* b1, const void* w2, const void* b2, int32_t num_experts,
                        int32_t top_k, int32_t dim, int32_t hidden, void* router_logits,
                        void* expert_ids, void* route_weights, void* hidden_act, void* out,
                        int32_t dtype, void* stream);
+
+/*
+ * The MoE half of a decoder block for ONE token (model.py:446-449):
+ *
+ *   out = x + MoE(LayerNorm(x; ln_weight, ln_bias, ln_eps))
+ *
+ * with MoE as in mie_moe_decode (routing outputs and hidden_act filled the
+ * same way) and the norm skipped when ln_weight is NULL.  The norm uses the
+ * biased variance in float32 (nn.LayerNorm); the residual add rounds once.
+ * Same arguments and limits as mie_moe_decode; out may alias x.  Two launches.
+ */
+int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* ln_bias,
+                             float ln_eps, const void* router_weight, const void* w1,
+                             const void* b1, const void* w2, const void* b2,
+                             int32_t num_experts, int32_t top_k, int32_t dim, int32_t hidden,
+                             void* router_logits, void* expert_ids, void* route_weights,
+                             void* hidden_act, void* out, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

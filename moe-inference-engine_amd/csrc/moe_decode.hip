@@ -20,10 +20,18 @@
 // dim], b1 [E, hidden], W2 [E, dim, hidden], b2 [E, dim] - so a selected
 // expert is a device-side offset; the route never leaves the GPU.
 //
-// Three launches.  The GEMVs are HBM-bound (2 * top_k * dim * hidden * 4
-// bytes per token, ~12.6 MB at d 768 / FFN 2048 / top-2): each wave issues all
-// of its weight loads (non-temporal: a token's experts are streamed once)
-// before it reduces, so a launch keeps the whole working set in flight.
+// Two launches.  Every W1 workgroup computes the routing itself (x into LDS,
+// the E router dot products, top-k) - the router is 24 KiB at E = 8, d = 768
+// and stays in L2 - so no launch waits on a separate route kernel; workgroup
+// (0, 0) writes the routing outputs, which the W2 launch reads.  The block
+// form also folds in the block's norm (out = x + MoE(LayerNorm(x)),
+// model.py:446-449): the norm goes into W1's LDS staging and the residual add
+// into W2's store.
+//
+// The GEMVs are HBM-bound (2 * top_k * dim * hidden * 4 bytes per token,
+// ~12.6 MB at d 768 / FFN 2048 / top-2): each wave issues all of its weight
+// loads (non-temporal: a token's experts are streamed once) before it
+// reduces, so a launch keeps the whole working set in flight.
 #include <math.h>
 
 #include "mie_common.h"
@@ -32,6 +40,7 @@ namespace {
 
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
+constexpr int kMaxDim = 2048;  // the W1 kernel holds x in 8 16-byte loads per lane
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -43,6 +52,10 @@ struct MoeArgs {
   const float* w2;      // [E, dim, hidden]
   const float* b2;      // [E, dim]
   int32_t E, top_k, dim, hidden;
+  const float* ln_w;      // block form: norm weight [dim] (NULL: no norm)
+  const float* ln_b;      // block form: norm bias [dim] or NULL
+  float ln_eps;
+  const float* residual;  // block form: x, added to the output
   float* logits;   // [E]
   int32_t* ids;    // [top_k], largest logit first
   float* weights;  // [top_k], same order
@@ -68,7 +81,47 @@ __device__ __forceinline__ float wave_dot(const float* __restrict__ row, const f
   return mie::wave_sum(s);
 }
 
-// One workgroup: E router dot products, then top-k and softmax on one lane.
+// Top-k over a wave: lane e holds expert e's logit (-inf for lanes >= E).
+// Round kk takes the largest logit not yet taken, the lower expert id on ties,
+// with a (value, id) butterfly; ids and weights (the softmax of the selected
+// logits) come out uniform across the wave.  Fixed-size loops keep both arrays
+// in registers.
+__device__ __forceinline__ void wave_topk(float logit, int top_k, int lane, int* ids, float* weights) {
+  bool taken = false;
+  float vals[kMaxTopK];
+#pragma unroll
+  for (int kk = 0; kk < kMaxTopK; ++kk) {
+    ids[kk] = 0;
+    vals[kk] = 0.f;
+    if (kk < top_k) {
+      float v = taken ? -INFINITY : logit;
+      int idx = lane;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(v, off);
+        const int oi = __shfl_xor(idx, off);
+        if (ov > v || (ov == v && oi < idx)) {
+          v = ov;
+          idx = oi;
+        }
+      }
+      ids[kk] = idx;
+      vals[kk] = v;
+      taken = taken || lane == idx;
+    }
+  }
+  // softmax over the selected logits; vals[0] is their maximum
+  float sum = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < kMaxTopK; ++kk) {
+    weights[kk] = kk < top_k ? expf(vals[kk] - vals[0]) : 0.f;
+    sum += weights[kk];
+  }
+#pragma unroll
+  for (int kk = 0; kk < kMaxTopK; ++kk) weights[kk] /= sum;
+}
+
+// One workgroup: E router dot products, then top-k and softmax on wave 0.
 __global__ __launch_bounds__(256) void moe_route_kernel(MoeArgs a) {
   __shared__ float logits[kMaxExperts];
   const int wave = threadIdx.x >> 6;
@@ -81,30 +134,16 @@ __global__ __launch_bounds__(256) void moe_route_kernel(MoeArgs a) {
     }
   }
   __syncthreads();
-  if (threadIdx.x != 0) return;
+  if (wave != 0) return;
   int ids[kMaxTopK];
-  float vals[kMaxTopK];
-  uint64_t taken = 0;
-  for (int k = 0; k < a.top_k; ++k) {
-    int best = -1;
-    for (int e = 0; e < a.E; ++e) {
-      if ((taken >> e) & 1) continue;
-      if (best < 0 || logits[e] > logits[best]) best = e;
-    }
-    taken |= uint64_t{1} << best;
-    ids[k] = best;
-    vals[k] = logits[best];
-  }
-  // softmax over the selected logits; vals[0] is their maximum
   float p[kMaxTopK];
-  float sum = 0.f;
-  for (int k = 0; k < a.top_k; ++k) {
-    p[k] = expf(vals[k] - vals[0]);
-    sum += p[k];
-  }
-  for (int k = 0; k < a.top_k; ++k) {
-    a.ids[k] = ids[k];
-    a.weights[k] = p[k] / sum;
+  wave_topk(lane < a.E ? logits[lane] : -INFINITY, a.top_k, lane, ids, p);
+#pragma unroll
+  for (int kk = 0; kk < kMaxTopK; ++kk) {
+    if (kk < a.top_k && lane == kk) {
+      a.ids[kk] = ids[kk];
+      a.weights[kk] = p[kk];
+    }
   }
 }
 
@@ -121,54 +160,148 @@ __device__ __forceinline__ float wave_sum4(float r0, float r1, float r2, float r
   return mie::group_sum<16>(b);
 }
 
-// grid = (ceil(hidden / 16), top_k); each wave computes 4 rows of slot
-// blockIdx.y's expert.  hidden % 4 == 0, so a wave's rows are all valid or
-// all past the end.
+// grid = (ceil(hidden / 16), top_k), 256 threads; NCH = ceil(dim / 256)
+// 16-byte loads per lane.  Each wave loads x (and the norm parameters) in the
+// lane layout of its dot products and normalises with wave reductions, and
+// loads the router rows of experts wave and wave + 4; the logits meet in LDS
+// behind the kernel's one barrier, every wave takes the top-k itself, then
+// computes 4 rows of slot blockIdx.y's expert.  hidden % 4 == 0, so a wave's
+// rows are all valid or all past the end.
+template <int NCH, bool NORM>
 __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
+  __shared__ float s_logits[kMaxExperts];
   const int k = blockIdx.y;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const int dim = a.dim;
+  const int e0 = wave, e1 = wave + 4;
+
+  // 1. All global reads that do not depend on the routing.
+  f32x4_t y[NCH], gw[NCH], gb[NCH], q0[NCH], q1[NCH];
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int i = c * 256 + lane * 4;
+    const bool valid = i < dim;
+    y[c] = valid ? load4(a.x + i) : zero;
+    gw[c] = NORM && valid ? load4(a.ln_w + i) : zero;
+    gb[c] = NORM && valid && a.ln_b ? load4(a.ln_b + i) : zero;
+    q0[c] = valid && e0 < a.E ? load4(a.router + static_cast<int64_t>(e0) * dim + i) : zero;
+    q1[c] = valid && e1 < a.E ? load4(a.router + static_cast<int64_t>(e1) * dim + i) : zero;
+  }
+
+  // 2. The block's LayerNorm (float32, biased variance), per wave.
+  if constexpr (NORM) {
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) s += y[c].x + y[c].y + y[c].z + y[c].w;
+    const float mean = mie::wave_sum(s) / dim;
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (c * 256 + lane * 4 < dim) {
+        const f32x4_t d = y[c] - mean;
+        q = dot4(d, d, q);
+      }
+    }
+    const float rstd = rsqrtf(mie::wave_sum(q) / dim + a.ln_eps);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) y[c] = (y[c] - mean) * rstd * gw[c] + gb[c];
+  }
+
+  // 3. Router logits: experts wave and wave + 4 from registers, any others
+  //    (E > 8) loaded now.
+  {
+    float l0 = 0.f, l1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      l0 = dot4(q0[c], y[c], l0);
+      l1 = dot4(q1[c], y[c], l1);
+    }
+    l0 = mie::wave_sum(l0);
+    l1 = mie::wave_sum(l1);
+    if (lane == 0) {
+      if (e0 < a.E) s_logits[e0] = l0;
+      if (e1 < a.E) s_logits[e1] = l1;
+    }
+    for (int e = wave + 8; e < a.E; e += 4) {
+      float l = 0.f;
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int i = c * 256 + lane * 4;
+        if (i < dim) l = dot4(load4(a.router + static_cast<int64_t>(e) * dim + i), y[c], l);
+      }
+      l = mie::wave_sum(l);
+      if (lane == 0) s_logits[e] = l;
+    }
+  }
+  __syncthreads();
+
+  // 4. Top-k in every wave; workgroup (0, 0) publishes the routing.
+  int ids[kMaxTopK];
+  float p[kMaxTopK];
+  const float logit = lane < a.E ? s_logits[lane] : -INFINITY;
+  wave_topk(logit, a.top_k, lane, ids, p);
+  if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+    if (lane < a.E) a.logits[lane] = logit;
+#pragma unroll
+    for (int kk = 0; kk < kMaxTopK; ++kk) {
+      if (kk < a.top_k && lane == kk) {
+        a.ids[kk] = ids[kk];
+        a.weights[kk] = p[kk];
+      }
+    }
+  }
+  int e = ids[0];
+#pragma unroll
+  for (int kk = 1; kk < kMaxTopK; ++kk) e = kk == k ? ids[kk] : e;
+
+  // 5. Four rows of the selected expert's W1, GELU, into h[k].
   const int r0 = (blockIdx.x * 4 + wave) * 4;
   if (r0 >= a.hidden) return;
-  const int e = a.ids[k];
-  const int64_t dim = a.dim;
   const float* __restrict__ w = a.w1 + (static_cast<int64_t>(e) * a.hidden + r0) * dim;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-#pragma unroll 4
-  for (int i = lane * 4; i < a.dim; i += 256) {
-    const f32x4_t q0 = stream4(w + i);
-    const f32x4_t q1 = stream4(w + dim + i);
-    const f32x4_t q2 = stream4(w + 2 * dim + i);
-    const f32x4_t q3 = stream4(w + 3 * dim + i);
-    const f32x4_t xv = load4(a.x + i);
-    s0 = dot4(q0, xv, s0);
-    s1 = dot4(q1, xv, s1);
-    s2 = dot4(q2, xv, s2);
-    s3 = dot4(q3, xv, s3);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int i = c * 256 + lane * 4;
+    if (i < dim) {
+      s0 = dot4(stream4(w + i), y[c], s0);
+      s1 = dot4(stream4(w + dim + i), y[c], s1);
+      s2 = dot4(stream4(w + 2 * dim + i), y[c], s2);
+      s3 = dot4(stream4(w + 3 * dim + i), y[c], s3);
+    }
   }
-  const float s = wave_sum4(s0, s1, s2, s3, lane);
+  const float t = wave_sum4(s0, s1, s2, s3, lane);
   if ((lane & 15) == 0) {
     const int r = r0 + (lane >> 4);
-    const float pre = s + a.b1[static_cast<int64_t>(e) * a.hidden + r];
+    const float pre = t + a.b1[static_cast<int64_t>(e) * a.hidden + r];
     a.h[static_cast<int64_t>(k) * a.hidden + r] = 0.5f * pre * (1.f + erff(pre * 0.70710678118654752440f));
   }
 }
 
 // grid = ceil(dim / 4); each wave owns one output element and reads that row
 // of every selected expert's W2 at once.
-template <int K>
+template <int K, bool RESID>
 __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int j = blockIdx.x * 4 + wave;
   if (j >= a.dim) return;
   int e[K];
+  float wt[K], bias[K];
   const float* __restrict__ row[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) {
     e[s] = a.ids[s];
     row[s] = a.w2 + (static_cast<int64_t>(e[s]) * a.dim + j) * a.hidden;
   }
+  // The epilogue's reads go out with the row loads, not after the reduction.
+#pragma unroll
+  for (int s = 0; s < K; ++s) {
+    wt[s] = a.weights[s];
+    bias[s] = a.b2[static_cast<int64_t>(e[s]) * a.dim + j];
+  }
+  const float res = RESID ? a.residual[j] : 0.f;
   float acc[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) acc[s] = 0.f;
@@ -197,12 +330,12 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
 #pragma unroll
     for (int s = 0; s < K; ++s) {
       if (rank[s] == r) {
-        const float y = acc[s] + a.b2[static_cast<int64_t>(e[s]) * a.dim + j];
-        out = __fadd_rn(out, __fmul_rn(a.weights[s], y));
+        const float y = acc[s] + bias[s];
+        out = __fadd_rn(out, __fmul_rn(wt[s], y));
       }
     }
   }
-  a.out[j] = out;
+  a.out[j] = RESID ? __fadd_rn(res, out) : out;
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -238,7 +371,11 @@ MoeArgs make_args(const void* x, const void* router_weight, int32_t num_experts,
 
 template <int K>
 void launch_w2(const MoeArgs& a, hipStream_t st) {
-  moe_w2_reduce_kernel<K><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
+  if (a.residual) {
+    moe_w2_reduce_kernel<K, true><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
+  } else {
+    moe_w2_reduce_kernel<K, false><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
+  }
 }
 
 }  // namespace
@@ -254,33 +391,43 @@ extern "C" int32_t mie_moe_route(const void* x, const void* router_weight, int32
   return mie::check_launch("moe_route_kernel");
 }
 
-extern "C" int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1, const void* b1,
-                                  const void* w2, const void* b2, int32_t num_experts, int32_t top_k, int32_t dim,
-                                  int32_t hidden, void* router_logits, void* expert_ids, void* route_weights,
-                                  void* hidden_act, void* out, int32_t dtype, void* stream) {
-  int32_t rc = check_route_args("mie_moe_decode", x, router_weight, num_experts, top_k, dim, router_logits,
-                                expert_ids, route_weights, dtype);
-  if (rc != MIE_OK) return rc;
+namespace {
+
+int32_t check_expert_args(const char* who, int32_t hidden, int32_t dim, const void* w1, const void* b1,
+                          const void* w2, const void* b2, const void* hidden_act, const void* out) {
   if (hidden <= 0 || hidden % 4 != 0)
-    return mie::fail(MIE_ERR_INVALID, "mie_moe_decode: hidden=%d must be a positive multiple of 4", hidden);
-  if (!w1 || !b1 || !w2 || !b2 || !hidden_act || !out) return mie::fail(MIE_ERR_INVALID, "mie_moe_decode: null pointer");
+    return mie::fail(MIE_ERR_INVALID, "%s: hidden=%d must be a positive multiple of 4", who, hidden);
+  if (dim > kMaxDim) return mie::fail(MIE_ERR_UNSUPPORTED, "%s: dim %d above %d", who, dim, kMaxDim);
+  if (!w1 || !b1 || !w2 || !b2 || !hidden_act || !out) return mie::fail(MIE_ERR_INVALID, "%s: null pointer", who);
   if (!aligned16(w1) || !aligned16(w2) || !aligned16(hidden_act))
-    return mie::fail(MIE_ERR_INVALID, "mie_moe_decode: W1, W2 and the hidden buffer must be 16-byte aligned");
-  MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids, route_weights);
-  a.w1 = static_cast<const float*>(w1);
-  a.b1 = static_cast<const float*>(b1);
-  a.w2 = static_cast<const float*>(w2);
-  a.b2 = static_cast<const float*>(b2);
-  a.h = static_cast<float*>(hidden_act);
-  a.out = static_cast<float*>(out);
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  moe_route_kernel<<<1, 256, 0, st>>>(a);
-  rc = mie::check_launch("moe_route_kernel");
+    return mie::fail(MIE_ERR_INVALID, "%s: W1, W2 and the hidden buffer must be 16-byte aligned", who);
+  return MIE_OK;
+}
+
+template <int NCH>
+void launch_w1(const MoeArgs& a, hipStream_t st) {
+  const dim3 grid((a.hidden + 15) / 16, a.top_k);
+  if (a.ln_w) {
+    moe_w1_gelu_kernel<NCH, true><<<grid, 256, 0, st>>>(a);
+  } else {
+    moe_w1_gelu_kernel<NCH, false><<<grid, 256, 0, st>>>(a);
+  }
+}
+
+int32_t launch_experts(MoeArgs& a, hipStream_t st) {
+  switch ((a.dim + 255) / 256) {
+    case 1: launch_w1<1>(a, st); break;
+    case 2: launch_w1<2>(a, st); break;
+    case 3: launch_w1<3>(a, st); break;
+    case 4: launch_w1<4>(a, st); break;
+    case 5: launch_w1<5>(a, st); break;
+    case 6: launch_w1<6>(a, st); break;
+    case 7: launch_w1<7>(a, st); break;
+    default: launch_w1<8>(a, st); break;
+  }
+  int32_t rc = mie::check_launch("moe_w1_gelu_kernel");
   if (rc != MIE_OK) return rc;
-  moe_w1_gelu_kernel<<<dim3((hidden + 15) / 16, top_k), 256, 0, st>>>(a);
-  rc = mie::check_launch("moe_w1_gelu_kernel");
-  if (rc != MIE_OK) return rc;
-  switch (top_k) {
+  switch (a.top_k) {
     case 1: launch_w2<1>(a, st); break;
     case 2: launch_w2<2>(a, st); break;
     case 3: launch_w2<3>(a, st); break;
@@ -291,4 +438,50 @@ extern "C" int32_t mie_moe_decode(const void* x, const void* router_weight, cons
     default: launch_w2<8>(a, st); break;
   }
   return mie::check_launch("moe_w2_reduce_kernel");
+}
+
+}  // namespace
+
+extern "C" int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1, const void* b1,
+                                  const void* w2, const void* b2, int32_t num_experts, int32_t top_k, int32_t dim,
+                                  int32_t hidden, void* router_logits, void* expert_ids, void* route_weights,
+                                  void* hidden_act, void* out, int32_t dtype, void* stream) {
+  int32_t rc = check_route_args("mie_moe_decode", x, router_weight, num_experts, top_k, dim, router_logits,
+                                expert_ids, route_weights, dtype);
+  if (rc != MIE_OK) return rc;
+  rc = check_expert_args("mie_moe_decode", hidden, dim, w1, b1, w2, b2, hidden_act, out);
+  if (rc != MIE_OK) return rc;
+  MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids, route_weights);
+  a.w1 = static_cast<const float*>(w1);
+  a.b1 = static_cast<const float*>(b1);
+  a.w2 = static_cast<const float*>(w2);
+  a.b2 = static_cast<const float*>(b2);
+  a.h = static_cast<float*>(hidden_act);
+  a.out = static_cast<float*>(out);
+  return launch_experts(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+                                        const void* router_weight, const void* w1, const void* b1, const void* w2,
+                                        const void* b2, int32_t num_experts, int32_t top_k, int32_t dim,
+                                        int32_t hidden, void* router_logits, void* expert_ids, void* route_weights,
+                                        void* hidden_act, void* out, int32_t dtype, void* stream) {
+  int32_t rc = check_route_args("mie_moe_decode_block", x, router_weight, num_experts, top_k, dim, router_logits,
+                                expert_ids, route_weights, dtype);
+  if (rc != MIE_OK) return rc;
+  rc = check_expert_args("mie_moe_decode_block", hidden, dim, w1, b1, w2, b2, hidden_act, out);
+  if (rc != MIE_OK) return rc;
+  if (!ln_weight && ln_bias) return mie::fail(MIE_ERR_INVALID, "mie_moe_decode_block: a norm bias needs a weight");
+  MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids, route_weights);
+  a.ln_w = static_cast<const float*>(ln_weight);
+  a.ln_b = static_cast<const float*>(ln_bias);
+  a.ln_eps = ln_eps;
+  a.residual = static_cast<const float*>(x);
+  a.w1 = static_cast<const float*>(w1);
+  a.b1 = static_cast<const float*>(b1);
+  a.w2 = static_cast<const float*>(w2);
+  a.b2 = static_cast<const float*>(b2);
+  a.h = static_cast<float*>(hidden_act);
+  a.out = static_cast<float*>(out);
+  return launch_experts(a, static_cast<hipStream_t>(stream));
 }

@@ -8,17 +8,22 @@
 //   cache.write: pool[bt[p // BS], h, p % BS, :] = k[h, :]  (and v)
 //
 // as three launches (norm, GEMM, append) plus the GEMM's argument upload.  Here
-// one launch does all of it: every workgroup normalises x into LDS (x is 3 KiB
-// at dim 768, so recomputing it per workgroup is cheaper than another launch),
-// then each wave computes two rows of the projection and stores them where they
-// belong - q into q_out, K and V into their pool slots.
+// one launch does all of it: every wave normalises x itself (x is 3 KiB at dim
+// 768, so recomputing it per wave is cheaper than another launch or a
+// barrier), then computes two rows of the projection and stores them where
+// they belong - q into q_out, K and V into their pool slots.
 //
 // Rounding points follow the reference for each dtype: the norm is computed in
 // float32 and rounded to the model dtype before the projection (bf16 models
 // feed bf16 activations to the GEMM); the projection accumulates in float32,
 // adds the bias, and rounds once to the model dtype.
 //
-// The projection reads 3*dim*dim*elt bytes of weights once: HBM-bound
+// The same body, with a residual epilogue instead of the pool stores, is the
+// attention's output projection plus the block's residual add
+// (model.py:268 and the block's `x + attention(...)`): out = residual +
+// round(W @ x + b) - one launch in place of a GEMM and an add.
+//
+// A projection reads rows*cols*elt bytes of weights once: HBM-bound
 // (0.5 flop/B in float32).  Weight loads are issued before the norm so their
 // latency overlaps it; they carry the non-temporal hint (each layer's weights
 // are streamed once per token).
@@ -28,11 +33,13 @@ namespace {
 
 constexpr int kRowsPerWave = 2;
 constexpr int kRowsPerGroup = 4 * kRowsPerWave;
-constexpr int kMaxDim = 4096;  // the largest dim built: 8 loads x 64 lanes x 8 bf16
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 struct QkvArgs {
+  int32_t rows;  // 3*dim for the QKV projection
+  const void* residual;  // linear form: NULL or [rows]
+  void* out;             // linear form: [rows]
   const void* x;
   const void* ln_w;  // NULL: no norm
   const void* ln_b;
@@ -87,104 +94,98 @@ template <> struct Elt<uint16_t> {  // bfloat16
   }
 };
 
-// Sum of one float over the 256-thread workgroup; every thread gets the total.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = mie::wave_sum(v);
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();  // `red` may still be read from a previous call
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  return red[0] + red[1] + red[2] + red[3];
-}
-
-// grid = ceil(3*dim / 8), 256 threads.  NCH = 16-byte loads per lane per row
-// (ceil(dim / (64 * elements per load))).
-template <typename DT, int NCH>
-__global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
+// grid = ceil(rows / 8), 256 threads, 2 rows per wave.  NCH = 16-byte loads
+// per lane per row (ceil(dim / (64 * elements per load))).  QKV: rows = 3*dim
+// stored as q and the K/V pool rows; else rows outputs stored to out
+// (+ residual).
+//
+// Every wave loads x and the norm parameters itself, in the lane layout of its
+// weight loads (lane l holds elements (c * 64 + l) * EPV ... + EPV - 1 of chunk
+// c), and normalises with wave reductions: no LDS and no barrier, so all of a
+// wave's global reads - weights, x, norm, bias, residual - are issued together
+// and the launch waits on one memory round trip.
+template <typename DT, int NCH, bool QKV>
+__device__ __forceinline__ void projection_body(const QkvArgs& a) {
   using E = Elt<DT>;
   constexpr int EPV = E::kPerVec;
-  __shared__ float y[kMaxDim];
-  __shared__ float red[4];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int dim = a.dim;
-  const int rows = 3 * dim;
+  const int rows = a.rows;
   const int r0 = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave;
   // Rows past the end repeat row r0 (or the last row) and are not stored.
   const int ra = min(r0, rows - 1);
   const int rb = min(r0 + 1, rows - 1);
 
-  // 1. Weight loads first: they do not depend on the norm.
-  u32x4_t wa[NCH], wb[NCH];
+  // 1. All global reads.
+  u32x4_t wa[NCH], wb[NCH], xw[NCH], gw[NCH], gb[NCH];
   const DT* w = static_cast<const DT*>(a.w_in);
+  const bool norm = a.ln_w != nullptr;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = (c * 64 + lane) * EPV;
+    wa[c] = xw[c] = gw[c] = gb[c] = u32x4_t{0u, 0u, 0u, 0u};
+    wb[c] = wa[c];
     if (i < dim) {
       wa[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(ra) * dim + i));
       wb[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(rb) * dim + i));
+      xw[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.x) + i);
+      if (norm) {
+        gw[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.ln_w) + i);
+        if (a.ln_b) gb[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.ln_b) + i);
+      }
     }
-  }
-
-  // 2. Every other global read is issued now too, so the launch waits on one
-  //    round trip: x and the norm parameters (thread t holds elements t,
-  //    t + 256, ...; XPT of them cover dim) and the bias of the row this lane
-  //    will store.
-  constexpr int XPT = NCH * EPV / 4;
-  float xv[XPT], gw[XPT], gb[XPT];
-#pragma unroll
-  for (int k = 0; k < XPT; ++k) {
-    const int i = threadIdx.x + k * 256;
-    xv[k] = i < dim ? E::load(a.x, i) : 0.f;
-    gw[k] = a.ln_w && i < dim ? E::load(a.ln_w, i) : 0.f;
-    gb[k] = a.ln_b && i < dim ? E::load(a.ln_b, i) : 0.f;
   }
   const int r_store = r0 + ((lane >> 5) & 1);
-  const float bias = a.b_in && (lane & 31) == 0 && r_store < rows ? E::load(a.b_in, r_store) : 0.f;
+  const bool storing = (lane & 31) == 0 && r_store < rows;
+  const float bias = a.b_in && storing ? E::load(a.b_in, r_store) : 0.f;
+  const float res = !QKV && a.residual && storing ? E::load(a.residual, r_store) : 0.f;
 
-  // 3. x, normalised when ln_w is given and rounded as the reference's norm
-  //    output is, into LDS as float.
-  if (a.ln_w) {
+  // 2. x, normalised when ln_w is given (float32 mean and biased variance, then
+  //    rounded to the model dtype as the reference's norm output is), in
+  //    registers; elements past dim are zero.
+  float y[NCH][EPV];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) E::widen(xw[c], y[c]);
+  if (norm) {
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < XPT; ++k) s += xv[k];  // zero past dim
-    const float mean = block_sum(s, red) / dim;
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) s += y[c][e];
+    const float mean = mie::wave_sum(s) / dim;
     float q = 0.f;
 #pragma unroll
-    for (int k = 0; k < XPT; ++k) {
-      const float d = threadIdx.x + k * 256 < dim ? xv[k] - mean : 0.f;
-      q = fmaf(d, d, q);
-    }
-    const float rstd = rsqrtf(block_sum(q, red) / dim + a.ln_eps);
+    for (int c = 0; c < NCH; ++c) {
+      const bool valid = (c * 64 + lane) * EPV < dim;
 #pragma unroll
-    for (int k = 0; k < XPT; ++k) {
-      const int i = threadIdx.x + k * 256;
-      if (i < dim) y[i] = E::round((xv[k] - mean) * rstd * gw[k] + gb[k]);
+      for (int e = 0; e < EPV; ++e) {
+        const float d = valid ? y[c][e] - mean : 0.f;
+        q = fmaf(d, d, q);
+      }
     }
-  } else {
+    const float rstd = rsqrtf(mie::wave_sum(q) / dim + a.ln_eps);
 #pragma unroll
-    for (int k = 0; k < XPT; ++k) {
-      const int i = threadIdx.x + k * 256;
-      if (i < dim) y[i] = xv[k];
+    for (int c = 0; c < NCH; ++c) {
+      float fw[EPV], fb[EPV];
+      E::widen(gw[c], fw);
+      E::widen(gb[c], fb);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) y[c][e] = E::round((y[c][e] - mean) * rstd * fw[e] + fb[e]);
     }
   }
-  __syncthreads();
 
-  // 4. Two dot products per wave.
+  // 3. Two dot products per wave (zero weights past dim).
   float sa = 0.f, sb = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int i = (c * 64 + lane) * EPV;
-    if (i < dim) {
-      float fa[EPV], fb[EPV];
-      E::widen(wa[c], fa);
-      E::widen(wb[c], fb);
+    float fa[EPV], fb[EPV];
+    E::widen(wa[c], fa);
+    E::widen(wb[c], fb);
 #pragma unroll
-      for (int e = 0; e < EPV; ++e) {
-        const float yv = y[i + e];
-        sa = fmaf(fa[e], yv, sa);
-        sb = fmaf(fb[e], yv, sb);
-      }
+    for (int e = 0; e < EPV; ++e) {
+      sa = fmaf(fa[e], y[c][e], sa);
+      sb = fmaf(fb[e], y[c][e], sb);
     }
   }
   // Lanes 0-31 finish row a, lanes 32-63 row b.
@@ -195,7 +196,12 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   const int r = r_store;
   if (r >= rows) return;
 
-  // 5. Store: q, or the K / V row of the token's pool slot.
+  // 5. Store: the linear form's output, q, or the K / V row of the token's
+  //    pool slot.
+  if constexpr (!QKV) {
+    E::store(a.out, r, a.residual ? res + E::round(t + bias) : t + bias);
+    return;
+  }
   const float out = t + bias;
   if (r < dim) {
     E::store(a.q_out, r, out);
@@ -215,22 +221,35 @@ __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
   E::store(is_v ? a.v_pool : a.k_pool, phys * a.sblk + h * a.shead + static_cast<int64_t>(slot) * a.head_dim + d, out);
 }
 
-template <typename DT>
+template <typename DT, int NCH>
+__global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
+  projection_body<DT, NCH, true>(a);
+}
+
+template <typename DT, int NCH>
+__global__ __launch_bounds__(256) void linear_residual_kernel(QkvArgs a) {
+  projection_body<DT, NCH, false>(a);
+}
+
+template <typename DT, bool QKV>
 int32_t launch(const QkvArgs& a, hipStream_t st) {
   const int nch = (a.dim + 64 * Elt<DT>::kPerVec - 1) / (64 * Elt<DT>::kPerVec);
-  const int groups = (3 * a.dim + kRowsPerGroup - 1) / kRowsPerGroup;
+  const int groups = (a.rows + kRowsPerGroup - 1) / kRowsPerGroup;
+#define MIE_PROJ_CASE(N)                                             \
+  case N:                                                            \
+    if (QKV) {                                                       \
+      qkv_append_kernel<DT, N><<<groups, 256, 0, st>>>(a);           \
+    } else {                                                         \
+      linear_residual_kernel<DT, N><<<groups, 256, 0, st>>>(a);      \
+    }                                                                \
+    break;
   switch (nch) {
-    case 1: qkv_append_kernel<DT, 1><<<groups, 256, 0, st>>>(a); break;
-    case 2: qkv_append_kernel<DT, 2><<<groups, 256, 0, st>>>(a); break;
-    case 3: qkv_append_kernel<DT, 3><<<groups, 256, 0, st>>>(a); break;
-    case 4: qkv_append_kernel<DT, 4><<<groups, 256, 0, st>>>(a); break;
-    case 5: qkv_append_kernel<DT, 5><<<groups, 256, 0, st>>>(a); break;
-    case 6: qkv_append_kernel<DT, 6><<<groups, 256, 0, st>>>(a); break;
-    case 7: qkv_append_kernel<DT, 7><<<groups, 256, 0, st>>>(a); break;
-    case 8: qkv_append_kernel<DT, 8><<<groups, 256, 0, st>>>(a); break;
-    default: return mie::fail(MIE_ERR_UNSUPPORTED, "mie_qkv_append: dim %d is too large", a.dim);
+    MIE_PROJ_CASE(1) MIE_PROJ_CASE(2) MIE_PROJ_CASE(3) MIE_PROJ_CASE(4)
+    MIE_PROJ_CASE(5) MIE_PROJ_CASE(6) MIE_PROJ_CASE(7) MIE_PROJ_CASE(8)
+    default: return mie::fail(MIE_ERR_UNSUPPORTED, "projection: width %d is too large", a.dim);
   }
-  return mie::check_launch("qkv_append_kernel");
+#undef MIE_PROJ_CASE
+  return mie::check_launch(QKV ? "qkv_append_kernel" : "linear_residual_kernel");
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -261,14 +280,16 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
     return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: null pointer");
   if ((ln_weight == nullptr) != (ln_bias == nullptr) && ln_bias != nullptr)
     return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: a norm bias needs a norm weight");
-  if (!aligned16(w_in))
-    return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: the projection weight must be 16-byte aligned");
+  if (!aligned16(w_in) || !aligned16(x) || !aligned16(ln_weight) || !aligned16(ln_bias))
+    return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: x, the norm parameters and the projection weight must be "
+                                      "16-byte aligned");
   if (pool_stride_head < static_cast<int64_t>(block_size) * head_dim ||
       pool_stride_block < static_cast<int64_t>(num_heads) * pool_stride_head)
     return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: pool strides (%lld, %lld) overlap",
                      static_cast<long long>(pool_stride_block), static_cast<long long>(pool_stride_head));
   if (!position_dev && position < 0) return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: position %d", position);
-  QkvArgs a;
+  QkvArgs a{};
+  a.rows = 3 * dim;
   a.x = x;
   a.ln_w = ln_weight;
   a.ln_b = ln_bias;
@@ -289,6 +310,27 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
   a.head_dim = head_dim;
   a.bs = mie::FastDiv::make(static_cast<uint32_t>(block_size));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == MIE_DTYPE_F32) return launch<float>(a, st);
-  return launch<uint16_t>(a, st);
+  if (dtype == MIE_DTYPE_F32) return launch<float, true>(a, st);
+  return launch<uint16_t, true>(a, st);
+}
+
+extern "C" int32_t mie_linear_residual(const void* x, const void* weight, const void* bias, const void* residual,
+                                       void* out, int32_t rows, int32_t cols, int32_t dtype, void* stream) {
+  if (!mie_qkv_append_supported(cols, dtype))
+    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_linear_residual: width %d with dtype %d is not built", cols, dtype);
+  if (rows <= 0) return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: rows %d", rows);
+  if (!x || !weight || !out) return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: null pointer");
+  if (!aligned16(weight) || !aligned16(x))
+    return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: x and the weight must be 16-byte aligned");
+  QkvArgs a{};
+  a.rows = rows;
+  a.residual = residual;
+  a.out = out;
+  a.x = x;
+  a.w_in = weight;
+  a.b_in = bias;
+  a.dim = cols;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == MIE_DTYPE_F32) return launch<float, false>(a, st);
+  return launch<uint16_t, false>(a, st);
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -78,6 +78,11 @@ _SIGNATURES = {
          _c_void_p, _i32, _i32, _i32, _i32, _c_void_p],  # q_out, heads, head_dim, block_size, dtype, stream
     ),
     "mie_qkv_append_supported": (_i32, [_i32, _i32]),
+    "mie_linear_residual": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, weight, bias, residual, out
+         _i32, _i32, _i32, _c_void_p],  # rows, cols, dtype, stream
+    ),
     "mie_moe_route": (
         _i32,
         [_c_void_p, _c_void_p, _i32, _i32, _i32,  # x, router weight, experts, top_k, dim
@@ -87,6 +92,14 @@ _SIGNATURES = {
         _i32,
         [_c_void_p, _c_void_p,  # x, router weight
          _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # canonical w1, b1, w2, b2 storages
+         _i32, _i32, _i32, _i32,  # experts, top_k, dim, hidden
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # logits, ids, weights, hidden, out
+         _i32, _c_void_p],  # dtype, stream
+    ),
+    "mie_moe_decode_block": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _f32,  # x, norm weight, norm bias, eps
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # router, canonical w1, b1, w2, b2
          _i32, _i32, _i32, _i32,  # experts, top_k, dim, hidden
          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # logits, ids, weights, hidden, out
          _i32, _c_void_p],  # dtype, stream

@@ -4,12 +4,15 @@ Drop-in for the reference's src/moe_engine/fused_moe.py: the same functions
 (`is_configuration_supported`, `is_supported`, `has_canonical_layout`, `route`,
 `decode`) with the same arguments, workspaces and errors, plus an availability
 flag.  Instead of three Triton programs it calls mie_moe_route / mie_moe_decode
-(include/mie_paged_kv.h).
+(include/mie_paged_kv.h); the decode is two launches, the first routing in
+every workgroup.
 
 The reference fixes one shape (hidden 768, 8 experts, top-2, expert hidden
 3072; fused_moe.py:27-53).  These kernels take the shape as arguments: up to
-64 experts, top-k up to 8, hidden and expert-hidden sizes multiples of 4 -
-which includes the reference's shape and the miniMoE FFN-2048 variant.
+64 experts, top-k up to 8, hidden size up to 2048, hidden and expert-hidden
+sizes multiples of 4 - which includes the reference's shape and the miniMoE
+FFN-2048 variant.  `decode_block` is the block's x + MoE(moe_norm(x)) in the
+same two launches.
 
 Semantics (fused_moe.py:119-262, model.py:443-461):
   router_logits = router_weight @ x
@@ -30,6 +33,7 @@ from moe_engine import _native
 HAS_HIP = _native.HAS_HIP
 MAX_EXPERTS = 64
 MAX_TOP_K = 8
+MAX_HIDDEN_DIM = 2048  # the W1 kernel holds x in 8 16-byte loads per lane
 
 
 def is_configuration_supported(
@@ -56,6 +60,7 @@ def is_configuration_supported(
         and hidden_dim % 4 == 0
         and expert_hidden_dim > 0
         and expert_hidden_dim % 4 == 0
+        and hidden_dim <= MAX_HIDDEN_DIM
     )
 
 
@@ -169,4 +174,35 @@ def decode(x, router_weight, w1_base, b1_base, w2_base, b2_base, *, router_logit
     )
     if rc:
         _native.check(rc, "mie_moe_decode")
+    return out.view(1, 1, dim)
+
+
+def decode_block(x, norm_weight, norm_bias, norm_eps, router_weight, w1_base, b1_base, w2_base, b2_base, *,
+                 router_logits, expert_ids, route_weights, hidden, out) -> torch.Tensor:
+    """The MoE half of a decoder block for one token, out = x + MoE(LayerNorm(x))
+    (reference model.py:446-449), in two launches; the routing workspaces are
+    filled as decode() fills them.  norm_weight None skips the norm.  Returns
+    `out` viewed as [1, 1, hidden]."""
+    params = [t for t in (norm_weight, norm_bias) if t is not None]
+    _require_rocm_float32(x, router_weight, w1_base, b1_base, w2_base, b2_base, router_logits, route_weights,
+                          hidden, out, *params)
+    if not has_canonical_layout(router_weight, w1_base, b1_base, w2_base, b2_base, router_logits, expert_ids,
+                                route_weights, hidden, out):
+        raise ValueError("direct MoE weights and workspaces must use canonical layouts")
+    num_experts, dim = router_weight.shape
+    if x.numel() != dim or not x.is_contiguous():
+        raise ValueError(f"direct MoE needs a contiguous x of {dim} values")
+    if norm_bias is not None and norm_weight is None:
+        raise ValueError("a norm bias needs a norm weight")
+    if any(t.shape != (dim,) or not t.is_contiguous() for t in params):
+        raise ValueError(f"norm parameters must be contiguous [{dim}] vectors")
+    rc = _native.lib().mie_moe_decode_block(
+        x.data_ptr(), _native.ptr(norm_weight), _native.ptr(norm_bias), float(norm_eps),
+        router_weight.data_ptr(), w1_base.data_ptr(), b1_base.data_ptr(), w2_base.data_ptr(), b2_base.data_ptr(),
+        num_experts, expert_ids.numel(), dim, w1_base.shape[1],
+        router_logits.data_ptr(), expert_ids.data_ptr(), route_weights.data_ptr(), hidden.data_ptr(),
+        out.data_ptr(), _native.dtype_code(x.dtype), _native.stream_of(x),
+    )
+    if rc:
+        _native.check(rc, "mie_moe_decode_block")
     return out.view(1, 1, dim)

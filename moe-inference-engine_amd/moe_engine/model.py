@@ -28,7 +28,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from moe_engine import _native, fused_moe, kv_ops, paged_attention
+from moe_engine import _native, fused_moe, kv_ops, paged_attention, projection
 
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
@@ -310,9 +310,12 @@ class CachedAttention(nn.Module):
         nn.init.zeros_(self.in_proj_bias)
 
     def fused_decode(self, x, norm, cache, layer_idx, position: int):
-        """attention(norm(x)) for one decode token with the QKV projection
-        stored straight into the paged pools (mie_qkv_append), or None when
-        that path does not apply (then the caller runs forward(norm(x), ...)).
+        """x + attention(norm(x)) for one decode token - the attention half of
+        the block (reference model.py:447) - in three launches: the QKV
+        projection stored straight into the paged pools (mie_qkv_append), the
+        paged decode, and out_proj with the residual add (mie_linear_residual).
+        Returns None when that path does not apply; the caller then runs
+        x + forward(norm(x), ...).
 
         Applies to a paged cache on a ROCm device whose decode runs the direct
         kernel, a float32 / bfloat16 model of a built width, and a plain
@@ -333,12 +336,22 @@ class CachedAttention(nn.Module):
             or norm.weight.dtype != x.dtype
             or (norm.bias is not None and norm.bias.dtype != x.dtype)
             or tuple(norm.normalized_shape) != (x.shape[-1],)
+            or self.out_proj.weight.dtype != x.dtype
+            or not self.out_proj.weight.is_contiguous()
             or not paged_attention.is_supported(x, self.head_dim)
         ):
             return None
         q = cache.write_projected(layer_idx, position, x, self.in_proj_weight, self.in_proj_bias, norm)
-        out = paged_attention.decode(q, cache, layer_idx, context_len=position + 1)
-        return self.out_proj(out.transpose(1, 2).reshape(1, 1, x.shape[-1]))
+        attn = paged_attention.decode(q, cache, layer_idx, context_len=position + 1)  # [1, H, 1, D]: heads in order
+        w, b = self.out_proj.weight, self.out_proj.bias
+        out = torch.empty_like(x)
+        rc = _native.lib().mie_linear_residual(
+            attn.data_ptr(), w.data_ptr(), _native.ptr(b), x.data_ptr(), out.data_ptr(),
+            w.shape[0], w.shape[1], alloc._launch[3], _native.stream_of(x),
+        )
+        if rc:
+            _native.check(rc, "mie_linear_residual")
+        return out
 
     def forward(self, x, cache, layer_idx, position: int):
         batch, seq_len, dim = x.shape
@@ -539,6 +552,29 @@ class MoEFeedForward(nn.Module):
             return self._forward_direct(x)
         return self._forward_reference(x)
 
+    def fused_block_decode(self, x, norm):
+        """x + self(norm(x), decode=True) for one token in two launches
+        (mie_moe_decode_block: the norm and routing in the W1 launch, the
+        residual add in the W2 launch), or None when the fused kernels do not
+        apply - mode 'reference', an unsupported configuration, or a norm that
+        is not a float32 LayerNorm over the hidden size."""
+        if (
+            self.mode == "reference"
+            or not isinstance(norm, nn.LayerNorm)
+            or norm.weight is None
+            or norm.weight.dtype != torch.float32
+            or (norm.bias is not None and norm.bias.dtype != torch.float32)
+            or tuple(norm.normalized_shape) != (self.dim,)
+            or not self._direct_supported(x)
+        ):
+            return None
+        s = self._expert_storage
+        return fused_moe.decode_block(
+            x, norm.weight, norm.bias, norm.eps, self.router.weight, s["w1"], s["b1"], s["w2"], s["b2"],
+            router_logits=self._router_logits, expert_ids=self._expert_ids, route_weights=self._route_weights,
+            hidden=self._expert_hidden, out=self._direct_out,
+        )
+
 
 class TransformerMoEBlock(nn.Module):
     def __init__(self, config: ModelConfig):
@@ -549,12 +585,17 @@ class TransformerMoEBlock(nn.Module):
         self.moe_norm = nn.LayerNorm(config.hidden_dim)
 
     def forward(self, x, cache, layer_idx, position):
-        attn = self.attention.fused_decode(x, self.attn_norm, cache, layer_idx, position)
-        if attn is None:
-            attn = self.attention(self.attn_norm(x), cache, layer_idx, position)
-        x = x + attn
-        normed = self.moe_norm(x)
-        return x + self.moe(normed, decode=position > 0 and normed.shape[1] == 1)
+        # One-token decode takes the fused halves where they apply (same
+        # results to float32 rounding); everything else is the reference's
+        # block (model.py:446-449).
+        h = self.attention.fused_decode(x, self.attn_norm, cache, layer_idx, position)
+        if h is None:
+            h = x + self.attention(self.attn_norm(x), cache, layer_idx, position)
+        decode = position > 0 and h.shape[1] == 1
+        out = self.moe.fused_block_decode(h, self.moe_norm) if decode else None
+        if out is None:
+            out = h + self.moe(self.moe_norm(h), decode=decode)
+        return out
 
 
 class Model(nn.Module):

@@ -1,7 +1,9 @@
 """Fused MoE decode (moe_engine.fused_moe -> mie_moe_route / mie_moe_decode)
 against the reference's PyTorch MoE path.
 
-Mirrors the reference's tests/test_fused_moe.py:52-236.  The PyTorch path
+Mirrors the reference's tests/test_fused_moe.py:52-236, and checks the
+block form (x + MoE(LayerNorm(x)), mie_moe_decode_block) against the
+reference block's own sequence.  The PyTorch path
 (model.py:443-461) is the oracle: same module, same input, mode 'reference'
 vs 'direct'.  Expert ids must match torch.topk exactly; route weights match
 softmax to 2e-6 (reference :66-69); outputs agree to float32 GEMV-vs-GEMM
@@ -211,3 +213,66 @@ def test_auto_uses_fused_kernel_for_decode_and_pytorch_for_prefill():
     assert not layer.uses_direct(x1.double(), decode=True)
     layer.set_mode("reference")
     assert not layer.uses_direct(x1, decode=True)
+
+
+@pytest.mark.parametrize("dim,hidden,experts,top_k", [(768, 2048, 8, 2), (64, 256, 16, 4), (128, 64, 3, 1)])
+@pytest.mark.parametrize("norm", [True, False])
+def test_block_decode_matches_norm_then_pytorch_path(dim, hidden, experts, top_k, norm):
+    """decode_block: out = x + MoE(LayerNorm(x)) against the reference block's
+    own sequence (model.py:446-449) with the PyTorch MoE path; routing outputs
+    against torch.topk / softmax of the normalised token's router logits."""
+    print_case("moe block", dim, hidden, experts, top_k, norm)
+    layer = moe(dim, hidden, experts, top_k)
+    ln = torch.nn.LayerNorm(dim).to("cuda")
+    with torch.no_grad():
+        ln.weight.copy_(1 + 0.1 * torch.randn(dim, device="cuda"))
+        ln.bias.copy_(0.1 * torch.randn(dim, device="cuda"))
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    for _ in range(4):
+        x = torch.randn(1, 1, dim, generator=gen, device="cuda") * 3 + 0.5
+        with torch.no_grad():
+            normed = ln(x) if norm else x
+            want = x + layer._forward_reference(normed)
+            s = layer._expert_storage
+            got = fused_moe.decode_block(
+                x, ln.weight if norm else None, ln.bias if norm else None, ln.eps, layer.router.weight,
+                s["w1"], s["b1"], s["w2"], s["b2"], router_logits=layer._router_logits,
+                expert_ids=layer._expert_ids, route_weights=layer._route_weights, hidden=layer._expert_hidden,
+                out=layer._direct_out,
+            ).clone()
+            logits = F.linear(normed.reshape(1, -1), layer.router.weight)[0]
+        assert_output_close(got, want)
+        top = torch.topk(logits, top_k)
+        assert torch.equal(layer._expert_ids.long(), top.indices)
+        torch.testing.assert_close(layer._route_weights, F.softmax(top.values, dim=0), atol=2e-6, rtol=1e-6)
+        torch.testing.assert_close(layer._router_logits, logits, atol=2e-5, rtol=1e-5)
+
+
+def test_block_decode_output_may_alias_input():
+    layer = moe(64, 128, 4, 2)
+    x = torch.randn(1, 1, 64, device="cuda")
+    s = layer._expert_storage
+    with torch.no_grad():
+        want = x + layer._forward_reference(x)
+        fused_moe.decode_block(x, None, None, 1e-5, layer.router.weight, s["w1"], s["b1"], s["w2"], s["b2"],
+                               router_logits=layer._router_logits, expert_ids=layer._expert_ids,
+                               route_weights=layer._route_weights, hidden=layer._expert_hidden, out=x.view(64))
+    assert_output_close(x, want)
+
+
+def test_model_block_fusion_matches_reference_block():
+    """The model's decode steps with the fused MoE half (mode auto) against
+    mode 'reference' (the PyTorch path after the block's norm), float32."""
+    torch.manual_seed(0)
+    model = Model(ModelConfig(max_seq_length=128, vocab_size=512, num_layers=2, hidden_dim=128, num_heads=4,
+                              num_experts=8, top_k=2)).to("cuda").eval()
+    ids = torch.randint(0, 512, (1, 24), device="cuda")
+    logits = {}
+    for mode in ("reference", "auto"):
+        model.set_moe_mode(mode)
+        cache = model.new_block_allocator(num_blocks=16, block_size=16, attention_mode="direct").new_cache()
+        with torch.no_grad():
+            steps = [model(ids[:, :16], cache)[:, -1]]
+            steps += [model(ids[:, t : t + 1], cache)[:, -1] for t in range(16, 24)]
+        logits[mode] = torch.stack(steps, 1)
+    torch.testing.assert_close(logits["auto"], logits["reference"], atol=1e-4, rtol=1e-4)

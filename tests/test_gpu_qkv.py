@@ -191,3 +191,48 @@ def test_model_decode_with_and_without_fused_projection(dtype):
     else:
         rel = ((logits[True] - logits[False]).norm() / logits[False].norm()).item()
         assert rel < 1e-2, rel
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols,residual,bias", [(768, 768, True, True), (96, 2048, False, True),
+                                                       (50, 64, True, False), (3, 8, False, False)])
+def test_linear_residual_matches_float64(dtype, rows, cols, residual, bias):
+    """out = residual + round(W x + b) (the attention's out_proj plus the
+    block's residual add) against float64 on the same inputs, with the
+    projection's output rounding to the model dtype."""
+    from moe_engine import projection
+
+    if not projection.supported(cols, dtype):
+        pytest.skip(f"width {cols} not built for {dtype}")
+    print_case("linear_residual", dtype, rows, cols, residual, bias)
+    g = torch.Generator().manual_seed(rows + cols)
+    x = torch.randn(cols, generator=g).to(dtype)
+    w = (torch.randn(rows, cols, generator=g) / math.sqrt(cols)).to(dtype)
+    b = (torch.randn(rows, generator=g) * 0.1).to(dtype) if bias else None
+    r = torch.randn(rows, generator=g).to(dtype) if residual else None
+    got = projection.linear_residual(x.cuda(), w.cuda(), None if b is None else b.cuda(),
+                                     None if r is None else r.cuda())
+    proj = ref.to_f64(w) @ ref.to_f64(x) + (ref.to_f64(b) if b is not None else 0.0)
+    scale = np.abs(ref.to_f64(w)) @ np.abs(ref.to_f64(x)) + (np.abs(ref.to_f64(b)) if b is not None else 0.0)
+    if residual:
+        proj_rounded = round_to(dtype)(proj)
+        want = ref.to_f64(r) + proj_rounded
+        got_f = ref.to_f64(got.cpu())
+        # the projection's error, then one more rounding of the sum
+        bound = (1e-5 * scale + 1e-6) if dtype == torch.float32 else (2.0**-7 * (np.abs(want) + np.abs(proj)) + 1e-4 * scale)
+        assert (np.abs(got_f - want) <= bound).all()
+    else:
+        assert_close(got.cpu(), proj, scale, dtype, "linear")
+
+
+def test_linear_residual_may_write_over_its_residual():
+    from moe_engine import projection
+
+    x = torch.randn(64, device="cuda")
+    w = torch.randn(32, 64, device="cuda") / 8
+    r = torch.randn(32, device="cuda")
+    want = r + w @ x
+    projection.linear_residual(x, w, None, r, out=r)
+    torch.testing.assert_close(r, want, atol=1e-5, rtol=1e-5)
+    with pytest.raises(ValueError, match="alias"):
+        projection.linear_residual(x[:32].contiguous(), torch.eye(32, device="cuda"), out=x[:32])
