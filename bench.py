@@ -264,40 +264,56 @@ def secondary_config2(torch):
 
 
 def secondary_config3(torch):
-    """12 layers, bf16, context 8192 over a 65536-block pool: per-layer append
-    (one token) and per-layer gather of the full context."""
+    """12 layers, bf16, 12 x 64, block 16, random tables
+    over a 65536-block pool, contexts 128, 1024 and 8192.  Per context: the
+    per-layer append of one token and the per-layer gather of the whole
+    context, as device time per layer (the 12 layers' calls replayed from one
+    HIP graph) and host-launched time per layer through the validating
+    wrapper; at 8192 also the prefill scatter of the whole context."""
     from moe_engine import kv_ops, workloads
 
-    L, NB, H, BS, D, C = 12, 65536, 12, 16, 64, 8192
+    L, NB, H, BS, D = 12, 65536, 12, 16, 64
     k_pool = torch.zeros(L, NB, H, BS, D, dtype=torch.bfloat16, device="cuda")
     v_pool = torch.zeros_like(k_pool)
-    table = torch.zeros(NB, dtype=torch.int32, device="cuda")
-    nblk = -(-C // BS)
-    table[:nblk] = torch.randperm(NB, generator=torch.Generator().manual_seed(3))[:nblk].to(torch.int32).cuda()
     new = torch.randn(1, H, 1, D, device="cuda").to(torch.bfloat16)
-    outk = torch.empty(1, H, C, D, dtype=torch.bfloat16, device="cuda")
-    outv = torch.empty_like(outk)
-    append_us = timed_us(torch, lambda: [kv_ops.append(k_pool, v_pool, l, new, new, table, position=C - 1) for l in range(L)]) / L
-    gather_us = timed_us(torch, lambda: [kv_ops.gather(k_pool, v_pool, l, table, C, outk, outv) for l in range(L)], iters=20) / L
+    perm = torch.randperm(NB, generator=torch.Generator().manual_seed(3)).to(torch.int32).cuda()
+    res = {}
+    for C in (128, 1024, 8192):
+        nblk = -(-C // BS)
+        table = torch.zeros(NB, dtype=torch.int32, device="cuda")
+        table[:nblk] = perm[:nblk]
+        outk = torch.empty(1, H, C, D, dtype=torch.bfloat16, device="cuda")
+        outv = torch.empty_like(outk)
+        appends = [lambda l=l: kv_ops.append(k_pool, v_pool, l, new, new, table, position=C - 1) for l in range(L)]
+        gathers = [lambda l=l: kv_ops.gather(k_pool, v_pool, l, table, C, outk, outv) for l in range(L)]
+        append_dev = graph_replay_us(torch, appends)
+        gather_dev = graph_replay_us(torch, gathers)
+        append_host = timed_us(torch, lambda: [f() for f in appends]) / L
+        gb = workloads.gather_bytes(C, H, D, 2)
+        ab = workloads.append_bytes(1, H, D, 2)
+        res[f"c{C}"] = {
+            "append_device_us_per_layer": round(append_dev, 2),
+            "append_host_launched_us_per_layer": round(append_host, 2),
+            "append_bytes_per_layer": ab,
+            "gather_device_us_per_layer": round(gather_dev, 2),
+            "gather_gbs": round(gb / gather_dev / 1e3, 1),
+            "gather_bytes_per_layer": gb,
+        }
     # Prefill scatter (SURVEY f1): the whole context written through the table in one launch per layer.
+    C = 8192
+    table = torch.zeros(NB, dtype=torch.int32, device="cuda")
+    table[: C // BS] = perm[: C // BS]
     prefill = torch.randn(1, H, C, D, device="cuda").to(torch.bfloat16)
-    prefill_us = timed_us(
-        torch, lambda: [kv_ops.append(k_pool, v_pool, l, prefill, prefill, table, position=0) for l in range(L)], iters=20
-    ) / L
-    gb = workloads.gather_bytes(C, H, D, 2)
+    prefill_dev = graph_replay_us(
+        torch, [lambda l=l: kv_ops.append(k_pool, v_pool, l, prefill, prefill, table, position=0) for l in range(L)]
+    )
     pb = workloads.append_bytes(C, H, D, 2)  # C tokens, K and V read and written
+    res["prefill_scatter_c8192"] = {"device_us_per_layer": round(prefill_dev, 2), "gbs": round(pb / prefill_dev / 1e3, 1)}
+    res["note"] = ("device: the 12 layers' calls replayed from one HIP graph, time per layer; "
+                   "host_launched: back-to-back calls through the Python wrapper")
     del k_pool, v_pool
     torch.cuda.empty_cache()
-    return {
-        "append_us_per_layer": round(append_us, 2),
-        "append_note": "one token per layer through the full-validation wrapper: host-bound (kernel ~4 us in the rocprof trace)",
-        "gather_us_per_layer": round(gather_us, 2),
-        "gather_gbs": round(gb / gather_us / 1e3, 1),
-        "gather_bytes_per_layer": gb,
-        "prefill_scatter_us_per_layer": round(prefill_us, 2),
-        "prefill_scatter_gbs": round(pb / prefill_us / 1e3, 1),
-        "context": C,
-    }
+    return res
 
 
 def secondary_moe(torch):
@@ -328,24 +344,26 @@ def secondary_moe(torch):
 
 
 def secondary_config5(torch):
-    """Long-context split decode, bf16, block 32: batch 1 and 8 at 131072."""
+    """BASELINE config 5, the long-context split decode: batch 1 and 8,
+    contexts 32768 and 131072, block 16 and 32, bf16 and fp32, 1 % of keys
+    x20.  Device time per call from 10 graph-replayed calls, GB/s of the
+    algorithmic bytes."""
     from moe_engine import paged_attention, workloads
 
     res = {}
-    for batch in (1, 8):
-        w = workloads.make_workload([131072] * batch, block_size=32, dtype=torch.bfloat16, seed=5, heavy_fraction=0.01)
-        nbytes = workloads.attention_bytes(w.lens, 12, 64, 32, 2)
-        us = timed_us(
-            torch,
-            lambda: paged_attention.decode_batched(
-                w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, context_lens_host=w.lens
-            ),
-            iters=20,
-        )
-        res[f"b{batch}_c131072_us"] = round(us, 2)
-        res[f"b{batch}_c131072_gbs"] = round(nbytes / us / 1e3, 1)
-        del w
-        torch.cuda.empty_cache()
+    for dtype, tag in ((torch.bfloat16, "bf16"), (torch.float32, "f32")):
+        for batch in (1, 8):
+            for ctx in (32768, 131072):
+                for bs in (16, 32):
+                    w = workloads.make_workload([ctx] * batch, block_size=bs, dtype=dtype, seed=5, heavy_fraction=0.01)
+                    nbytes = workloads.attention_bytes(w.lens, 12, 64, bs, w.k_pool.element_size())
+                    call = lambda: paged_attention.decode_batched(
+                        w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, context_lens_host=w.lens
+                    )
+                    us = graph_replay_us(torch, [call] * 10)
+                    res[f"{tag}_b{batch}_c{ctx}_bs{bs}"] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1)}
+                    del w
+                    torch.cuda.empty_cache()
     return res
 
 
