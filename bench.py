@@ -461,9 +461,23 @@ def main():
         },
         "roofline": main_res["roofline"],
         "cpu_baseline": cpu,
+        "per_token_decode_ms": per_token_decode_ms(secondary.get("config1_e2e_decode")),
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
+
+
+def per_token_decode_ms(e2e):
+    """The metric's second half: BASELINE config 1's median greedy decode
+    latency per token for each system, from the config1_e2e_decode secondary
+    (None when it did not run)."""
+    if not e2e or "summary" not in e2e:
+        return None
+    out = {system: s["decode_median_ms"] for system, s in e2e["summary"].items()}
+    out["tokens_identical"] = e2e.get("tokens_identical")
+    out["workload"] = ("BASELINE config 1: 12 layers, d 768, 12 x 64 heads, top-2 of 8, FFN 2048, vocab 50257, "
+                       "fp32, random init seed 0, 32-token prompt, 64 greedy tokens, block 16")
+    return out
 
 
 if __name__ == "__main__":

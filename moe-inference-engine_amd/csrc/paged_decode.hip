@@ -909,7 +909,10 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
       const int c = ctx_lens_host[b];
       return c < 0 ? 0 : (c > max_ctx_len ? max_ctx_len : c);
     };
-    std::stable_sort(order.seq, order.seq + batch, [&](uint16_t x, uint16_t y) { return len(x) > len(y); });
+    // A total order (length descending, then index), so the in-place sort gives
+    // the stable order without a temporary buffer.
+    std::sort(order.seq, order.seq + batch,
+              [&](uint16_t x, uint16_t y) { return len(x) > len(y) || (len(x) == len(y) && x < y); });
     order.n = batch;
   }
   return dispatch(dtype, head_dim, a, batch, p.fast, p.wg, order, flat_items, static_cast<hipStream_t>(stream));

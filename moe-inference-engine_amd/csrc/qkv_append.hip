@@ -94,7 +94,28 @@ template <> struct Elt<uint16_t> {  // bfloat16
   }
 };
 
-// grid = ceil(rows / 8), 256 threads, 2 rows per wave.  NCH = 16-byte loads
+// Sums R per-lane partials (one per row) over the wave with a transposed
+// butterfly: exchange k (lane bit 5 - k) keeps the upper or lower half of the
+// rows, so after log2(R) exchanges lanes [q * 64 / R, (q + 1) * 64 / R) hold
+// partials of row q only, which one group sum finishes.  Returns row
+// lane / (64 / R)'s total in every lane.
+template <int R>
+__device__ __forceinline__ float reduce_rows(const float (&v)[R], int lane) {
+  float cur[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) cur[i] = v[i];
+#pragma unroll
+  for (int step = 0; (1 << step) < R; ++step) {
+    const int off = 32 >> step;
+    const int half = R >> (step + 1);
+    const bool up = lane & off;
+#pragma unroll
+    for (int i = 0; i < half; ++i) cur[i] = (up ? cur[i + half] : cur[i]) + __shfl_xor(up ? cur[i] : cur[i + half], off);
+  }
+  return mie::group_sum<64 / R>(cur[0]);
+}
+
+// grid = ceil(rows / (4 * kRowsPerWave)), 256 threads.  NCH = 16-byte loads
 // per lane per row (ceil(dim / (64 * elements per load))).  QKV: rows = 3*dim
 // stored as q and the K/V pool rows; else rows outputs stored to out
 // (+ residual).
@@ -112,23 +133,25 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   const int lane = threadIdx.x & 63;
   const int dim = a.dim;
   const int rows = a.rows;
-  const int r0 = blockIdx.x * kRowsPerGroup + wave * kRowsPerWave;
-  // Rows past the end repeat row r0 (or the last row) and are not stored.
-  const int ra = min(r0, rows - 1);
-  const int rb = min(r0 + 1, rows - 1);
+  constexpr int R = kRowsPerWave;
+  const int r0 = blockIdx.x * kRowsPerGroup + wave * R;
 
-  // 1. All global reads.
-  u32x4_t wa[NCH], wb[NCH], xw[NCH], gw[NCH], gb[NCH];
+  // 1. All global reads.  Rows past the end repeat the last row and are not
+  //    stored.
+  u32x4_t wr[R][NCH], xw[NCH], gw[NCH], gb[NCH];
   const DT* w = static_cast<const DT*>(a.w_in);
   const bool norm = a.ln_w != nullptr;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = (c * 64 + lane) * EPV;
-    wa[c] = xw[c] = gw[c] = gb[c] = u32x4_t{0u, 0u, 0u, 0u};
-    wb[c] = wa[c];
+    xw[c] = gw[c] = gb[c] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int r = 0; r < R; ++r) wr[r][c] = xw[c];
     if (i < dim) {
-      wa[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(ra) * dim + i));
-      wb[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(rb) * dim + i));
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        wr[r][c] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(min(r0 + r, rows - 1)) * dim + i));
       xw[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.x) + i);
       if (norm) {
         gw[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.ln_w) + i);
@@ -136,8 +159,9 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
       }
     }
   }
-  const int r_store = r0 + ((lane >> 5) & 1);
-  const bool storing = (lane & 31) == 0 && r_store < rows;
+  constexpr int kGroup = 64 / R;  // lanes that finish one row
+  const int r_store = r0 + lane / kGroup;
+  const bool storing = lane % kGroup == 0 && r_store < rows;
   const float bias = a.b_in && storing ? E::load(a.b_in, r_store) : 0.f;
   const float res = !QKV && a.residual && storing ? E::load(a.residual, r_store) : 0.f;
 
@@ -175,26 +199,22 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
     }
   }
 
-  // 3. Two dot products per wave (zero weights past dim).
-  float sa = 0.f, sb = 0.f;
+  // 3. R dot products per wave (zero weights past dim).
+  float acc[R];
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    float fa[EPV], fb[EPV];
-    E::widen(wa[c], fa);
-    E::widen(wb[c], fb);
+  for (int r = 0; r < R; ++r) {
+    acc[r] = 0.f;
 #pragma unroll
-    for (int e = 0; e < EPV; ++e) {
-      sa = fmaf(fa[e], y[c][e], sa);
-      sb = fmaf(fb[e], y[c][e], sb);
+    for (int c = 0; c < NCH; ++c) {
+      float f[EPV];
+      E::widen(wr[r][c], f);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) acc[r] = fmaf(f[e], y[c][e], acc[r]);
     }
   }
-  // Lanes 0-31 finish row a, lanes 32-63 row b.
-  const bool hi = lane & 32;
-  float t = (hi ? sb : sa) + __shfl_xor(hi ? sa : sb, 32);
-  t = mie::group_sum<32>(t);
-  if ((lane & 31) != 0) return;
+  const float t = reduce_rows<R>(acc, lane);
+  if (!storing) return;
   const int r = r_store;
-  if (r >= rows) return;
 
   // 5. Store: the linear form's output, q, or the K / V row of the token's
   //    pool slot.
@@ -278,8 +298,7 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
                      num_blocks, block_table_len);
   if (!x || !w_in || !k_pool || !v_pool || !block_table || !q_out)
     return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: null pointer");
-  if ((ln_weight == nullptr) != (ln_bias == nullptr) && ln_bias != nullptr)
-    return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: a norm bias needs a norm weight");
+  if (ln_bias && !ln_weight) return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: a norm bias needs a norm weight");
   if (!aligned16(w_in) || !aligned16(x) || !aligned16(ln_weight) || !aligned16(ln_bias))
     return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: x, the norm parameters and the projection weight must be "
                                       "16-byte aligned");

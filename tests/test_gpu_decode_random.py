@@ -1,0 +1,67 @@
+"""Randomized parity sweep of mie_paged_decode against the float64 oracle.
+
+48 seeded cases draw the batch (1-40), ragged context lengths (zero
+included), block size (power of two or not), head count and head_dim, dtype,
+output dtype, plan (automatic, workgroup form, fixed partitions) and whether
+host lengths size the launch.  Each case checks every sequence against
+oracle.paged_ref.attention_fp64 on the same pool contents: float32 inputs
+within 1e-5, bfloat16 inputs within 2e-3 with float32 output or
+2e-3 + 2^-8 |ref| with bf16 output (the tolerances of the north star and of
+tests/test_gpu_decode.py).  The cases print before they run, so a failure
+names its draw.
+"""
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import print_case
+from moe_engine import _native, paged_attention
+from paged_cases import bf16_close, make_workload, oracle_outputs
+
+pytestmark = pytest.mark.gpu
+
+HEAD_DIMS = (16, 32, 64, 96, 128)
+
+
+def draw(seed):
+    rng = random.Random(seed)
+    dtype = rng.choice((torch.float32, torch.bfloat16))
+    head_dim = rng.choice(HEAD_DIMS)
+    heads = rng.choice((1, 3, 4, 12))
+    block_size = rng.choice((1, 3, 5, 8, 16, 32))
+    batch = rng.randint(1, 40)
+    reach = rng.choice((16, 300, 3000))
+    lens = [rng.randint(0, reach) if rng.random() < 0.9 else 0 for _ in range(batch)]
+    if max(lens) == 0:
+        lens[0] = 1
+    tile, _ = _native.decode_plan(batch, heads, head_dim, block_size, 1, dtype, 0)
+    partition = rng.choice((0, -1, tile, 2 * tile, 8 * tile))
+    return dict(dtype=dtype, head_dim=head_dim, heads=heads, block_size=block_size, lens=lens,
+                partition=partition, host_lens=rng.random() < 0.5, out_f32=rng.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(48))
+def test_random_decode_matches_oracle(seed):
+    c = draw(seed)
+    print_case("random decode", seed, {k: (v if k != "lens" else f"{len(v)} seqs, max {max(v)}") for k, v in c.items()})
+    w = make_workload(c["lens"], num_heads=c["heads"], head_dim=c["head_dim"], block_size=c["block_size"],
+                      dtype=c["dtype"], seed=seed, heavy_fraction=0.01)
+    got = paged_attention.decode_batched(
+        w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
+        partition_tokens=c["partition"], context_lens_host=w.lens if c["host_lens"] else None,
+        out_dtype=torch.float32 if c["out_f32"] else None,
+    )
+    want = oracle_outputs(w)
+    zero = [b for b, n in enumerate(c["lens"]) if n == 0]
+    for b in zero:  # no keys: zeros, as scaled_dot_product_attention returns
+        assert torch.equal(got[b], torch.zeros_like(got[b]))
+    got = got.float().cpu().numpy()
+    if c["dtype"] == torch.float32:
+        np.testing.assert_allclose(got, want, rtol=0, atol=1e-5)
+    elif c["out_f32"]:
+        np.testing.assert_allclose(got, want, rtol=0, atol=2e-3)
+    else:
+        assert bf16_close(got, want)
