@@ -7,14 +7,17 @@ Workload (the configuration the north-star HBM target is
 quoted on): 64 sequences with contexts U[512, 8192] (seed 2), 12 heads x 64,
 block size 16, bf16 K/V, each block table a random shuffle over a shared
 40000-block pool.  One step is one decode step of the paged path for one
-layer over the whole batch: the batched HIP append of each sequence's new
-token (into its last slot) followed by the batched direct paged decode
-attention over the full contexts.  Inputs are resident in HBM before timing.
+layer over the whole batch: the batched append of each sequence's new token
+(into its last slot) and the batched direct paged decode attention over the
+full contexts - one mie_paged_decode_append launch (`--unfused`: the append
+launch, then the decode launch).  Inputs are resident in HBM before timing.
 
 Printed: ONE JSON line.  `value` is algorithmic bytes (attention + append) per
-step over the measured step time, in GB/s.  `roofline` is the attention alone:
-its algorithmic bytes over its average duration from HIP events recorded on
-the launch stream around every attention call of the timed region.
+step over the measured step time, in GB/s.  `roofline` is the dominant
+launch: its algorithmic bytes (attention + append fused; attention alone with
+`--unfused`) over its average duration from HIP events recorded on the launch
+stream: one event pair around the timed loop of back-to-back fused launches
+(region / steps), or events around every attention call with `--unfused`.
 `cpu_baseline` times the oracle's gather + scaled_dot_product_attention path
 (the reference's CPU path) on a bounded sample of the same workload.
 `secondary` carries the per-token end-to-end decode latency (config 1) and the
@@ -45,6 +48,8 @@ def parse_args():
     p.add_argument("--partition-tokens", type=int, default=0, help="0 = the library's automatic choice")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--unfused", action="store_true",
+                   help="run the step's append and decode as two launches instead of mie_paged_decode_append")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     p.add_argument(
         "--copy-calibration-mib",
@@ -100,6 +105,8 @@ def run_config4(torch, args):
         len(w.lens), heads, dim, 16, w.max_len, torch.bfloat16, args.partition_tokens
     )
 
+    k_rows, v_rows = k_new[:, :, 0], v_new[:, :, 0]
+
     def append():
         kv_ops.append(w.k_pool, w.v_pool, 0, k_new, v_new, w.block_tables, positions=positions)
 
@@ -109,24 +116,51 @@ def run_config4(torch, args):
             out=out, partition_tokens=args.partition_tokens, context_lens_host=w.lens,
         )
 
+    def step_fused():
+        # The new token is each sequence's last context token: one launch
+        # stores it and attends (mie_paged_decode_append).
+        paged_attention.decode_batched(
+            w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
+            out=out, partition_tokens=args.partition_tokens, context_lens_host=w.lens, k_new=k_rows, v_new=v_rows,
+        )
+
+    # Timed region: the whole step.  Fused, the step is one launch, so one
+    # pair of HIP events around the timed loop gives its average duration
+    # (region / steps: inter-launch gaps included, no per-call event packets,
+    # which cost ~1-2 us of stream time each).  Unfused, events bracket every
+    # attention call to separate it from the append launch.
+    before, timed = (append, attend) if args.unfused else (None, step_fused)
+    timed_bytes = attn_bytes if args.unfused else attn_bytes + app_bytes
     for _ in range(args.warmup):
-        append()
-        attend()
+        if before:
+            before()
+        timed()
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    per_call = args.unfused
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps if per_call else 1)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps if per_call else 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    if not per_call:
+        starts[0].record()
     for i in range(args.steps):
-        append()
-        starts[i].record()
-        attend()
-        ends[i].record()
+        if before:
+            before()
+        if per_call:
+            starts[i].record()
+        timed()
+        if per_call:
+            ends[i].record()
+    if not per_call:
+        ends[0].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    attn_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    if per_call:
+        attn_ms = [s_.elapsed_time(e_) for s_, e_ in zip(starts, ends)]
+    else:
+        attn_ms = [starts[0].elapsed_time(ends[0]) / args.steps]
     attn_avg_s = sum(attn_ms) / len(attn_ms) / 1e3
-    achieved = attn_bytes / attn_avg_s / 1e9
+    achieved = timed_bytes / attn_avg_s / 1e9
     traffic = None
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
@@ -140,18 +174,21 @@ def run_config4(torch, args):
         "workspace_bytes": ws_bytes,
         "roofline": {
             "bound": "hbm",
-            "kernel": "mie_paged_decode ("
+            "kernel": ("mie_paged_decode (" if args.unfused else "mie_paged_decode_append (")
             + ("paged_decode_wg_kernel, one workgroup per (sequence, head)" if ws_bytes == 0
                else "paged_decode_flat_kernel + paged_decode_reduce_kernel")
+            + ("" if args.unfused or ws_bytes else ", the step's append fused in")
             + ")",
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "algorithmic_bytes_per_launch": attn_bytes,
+            "algorithmic_bytes_per_launch": timed_bytes,
             "avg_duration_us": round(attn_avg_s * 1e6, 2),
-            "median_duration_us": round(statistics.median(attn_ms) * 1e3, 2),
+            "median_duration_us": round(statistics.median(attn_ms) * 1e3, 2) if per_call else None,
+            "duration_source": "HIP events around every attention call" if per_call
+            else "one HIP event pair around the timed loop of back-to-back launches (region / steps)",
         },
     }
 

@@ -9,6 +9,8 @@
  *   mie_kv_gather     <- PagedKVCache.read      src/moe_engine/model.py:186-201
  *   mie_paged_decode  <- paged_attention.decode src/moe_engine/paged_attention.py:113-154
  *                        and _paged_decode_kernel src/moe_engine/paged_attention.py:46-110
+ *   mie_paged_decode_append <- cache.write then paged_attention.decode for a
+ *                        decode token (model.py:247 then :263), in one launch
  *   mie_qkv_append    <- CachedAttention.forward's QKV projection and
  *                        cache.write for one decode token  src/moe_engine/model.py:228-247
  *   mie_linear_residual <- out_proj + the block's residual add  src/moe_engine/model.py:268, :447
@@ -68,7 +70,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 6
+#define MIE_ABI_VERSION 7
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -156,6 +158,34 @@ int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          int64_t out_stride_h, int32_t out_dtype, void* workspace,
                          int64_t workspace_bytes, int32_t partition_tokens,
                          int32_t dtype, void* stream);
+
+/*
+ * A decode step's append and attention together (model.py:247 then :263 for
+ * B sequences): each sequence's new token is its LAST context token, so
+ * k_new[b] / v_new[b] ([B, H, D] rows, element strides new_stride_b /
+ * new_stride_h, inner axis contiguous, `dtype`) are stored at position
+ * ctx_b - 1 through the block table, exactly as mie_kv_append stores them,
+ * and the output is mie_paged_decode's over tokens [0, ctx_b) with that token
+ * included.  The pools are written.  When the plan takes the workgroup form
+ * this is ONE launch: the decode kernel stores the rows and takes the new
+ * token's score and value from the rows it loaded, without reading them back;
+ * otherwise the append runs as its own launch before the decode, on the same
+ * stream.  A sequence with ctx_b = 0 gets no append and a zero output; a new
+ * token whose block id is outside the pool is not stored and its output is
+ * NaN.  Other arguments and limits as mie_paged_decode.
+ */
+int32_t mie_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                void* k_pool, void* v_pool, int64_t pool_stride_block,
+                                int64_t pool_stride_head, int32_t num_blocks,
+                                const int32_t* block_tables, int64_t block_table_stride,
+                                const int32_t* ctx_lens, const int32_t* ctx_lens_host,
+                                int32_t ctx_len, int32_t max_ctx_len, int32_t batch,
+                                int32_t num_heads, int32_t head_dim, int32_t block_size,
+                                float scale, void* out, int64_t out_stride_b,
+                                int64_t out_stride_h, int32_t out_dtype, void* workspace,
+                                int64_t workspace_bytes, int32_t partition_tokens,
+                                const void* k_new, const void* v_new, int64_t new_stride_b,
+                                int64_t new_stride_h, int32_t dtype, void* stream);
 
 /*
  * Host-only planning query for mie_paged_decode (no device work).  Given the

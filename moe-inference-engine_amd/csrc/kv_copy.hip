@@ -29,6 +29,7 @@ struct AppendArgs {
   uint32_t bt_cap;    // entries readable per table row
   const int32_t* positions;
   int32_t position;
+  int32_t pos_bias;  // added to the position: -1 appends at a length's last slot
   int32_t seq_len;
   int32_t num_heads;
   int32_t row_bytes;
@@ -51,7 +52,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int h = r / a.vecs_per_row;
   const int vec = r - h * a.vecs_per_row;
 
-  const int pos = (a.positions ? a.positions[b] : a.position) + s;
+  const int pos = (a.positions ? a.positions[b] : a.position) + a.pos_bias + s;
   if (pos < 0) return;
   const uint32_t blk = a.bs.div(static_cast<uint32_t>(pos));
   const uint32_t slot = static_cast<uint32_t>(pos) - blk * a.bs.d;
@@ -119,14 +120,12 @@ int pick_vec_bytes(int row_bytes, std::initializer_list<int64_t> byte_strides,
 
 }  // namespace
 
-extern "C" int32_t mie_kv_append(void* k_pool, void* v_pool, int64_t pool_stride_block,
-                                 int64_t pool_stride_head, int32_t num_blocks, const void* k_new,
-                                 const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
-                                 int64_t new_stride_s, const int32_t* block_tables,
-                                 int64_t block_table_stride, const int32_t* positions,
-                                 int32_t position, int32_t batch, int32_t seq_len,
-                                 int32_t num_heads, int32_t head_dim, int32_t block_size,
-                                 int32_t dtype, void* stream) {
+int32_t mie::kv_append_impl(void* k_pool, void* v_pool, int64_t pool_stride_block, int64_t pool_stride_head,
+                            int32_t num_blocks, const void* k_new, const void* v_new, int64_t new_stride_b,
+                            int64_t new_stride_h, int64_t new_stride_s, const int32_t* block_tables,
+                            int64_t block_table_stride, const int32_t* positions, int32_t position,
+                            int32_t pos_bias, int32_t batch, int32_t seq_len, int32_t num_heads,
+                            int32_t head_dim, int32_t block_size, int32_t dtype, void* stream) {
   const int elt = mie::elt_size(dtype);
   if (elt == 0) return mie::fail(MIE_ERR_UNSUPPORTED, "mie_kv_append: unknown dtype %d", dtype);
   if (batch < 0 || seq_len < 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 ||
@@ -138,15 +137,15 @@ extern "C" int32_t mie_kv_append(void* k_pool, void* v_pool, int64_t pool_stride
   if (batch == 0 || seq_len == 0) return MIE_OK;
   if (!k_pool || !v_pool || !k_new || !v_new || !block_tables)
     return mie::fail(MIE_ERR_INVALID, "mie_kv_append: null pointer");
-  if (!positions && position < 0)
-    return mie::fail(MIE_ERR_INVALID, "mie_kv_append: negative position %d", position);
+  if (!positions && position + pos_bias < 0)
+    return mie::fail(MIE_ERR_INVALID, "mie_kv_append: negative position %d", position + pos_bias);
   if (seq_len > 65535 || batch > 65535)
     return mie::fail(MIE_ERR_INVALID, "mie_kv_append: batch/seq_len above 65535");
   if (pool_stride_head < static_cast<int64_t>(block_size) * head_dim ||
       pool_stride_block < static_cast<int64_t>(num_heads) * pool_stride_head)
     return mie::fail(MIE_ERR_INVALID, "mie_kv_append: pool strides overlap");
 
-  AppendArgs a;
+  AppendArgs a{};
   a.k_pool = static_cast<char*>(k_pool);
   a.v_pool = static_cast<char*>(v_pool);
   a.pool_sblk = pool_stride_block * elt;
@@ -162,6 +161,7 @@ extern "C" int32_t mie_kv_append(void* k_pool, void* v_pool, int64_t pool_stride
   a.bt_cap = static_cast<uint32_t>(block_table_stride > 0 ? block_table_stride : num_blocks);
   a.positions = positions;
   a.position = position;
+  a.pos_bias = pos_bias;
   a.seq_len = seq_len;
   a.num_heads = num_heads;
   a.row_bytes = head_dim * elt;
@@ -183,6 +183,19 @@ extern "C" int32_t mie_kv_append(void* k_pool, void* v_pool, int64_t pool_stride
     default: kv_append_kernel<2><<<grid, threads, 0, st>>>(a); break;
   }
   return mie::check_launch("mie_kv_append");
+}
+
+extern "C" int32_t mie_kv_append(void* k_pool, void* v_pool, int64_t pool_stride_block,
+                                 int64_t pool_stride_head, int32_t num_blocks, const void* k_new,
+                                 const void* v_new, int64_t new_stride_b, int64_t new_stride_h,
+                                 int64_t new_stride_s, const int32_t* block_tables,
+                                 int64_t block_table_stride, const int32_t* positions,
+                                 int32_t position, int32_t batch, int32_t seq_len,
+                                 int32_t num_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t dtype, void* stream) {
+  return mie::kv_append_impl(k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, k_new, v_new,
+                             new_stride_b, new_stride_h, new_stride_s, block_tables, block_table_stride, positions,
+                             position, 0, batch, seq_len, num_heads, head_dim, block_size, dtype, stream);
 }
 
 extern "C" int32_t mie_kv_gather(const void* k_pool, const void* v_pool, int64_t pool_stride_block,

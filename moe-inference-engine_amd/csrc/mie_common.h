@@ -27,6 +27,15 @@ inline int elt_size(int32_t dtype) {
 // Maps a launch failure to MIE_ERR_LAUNCH with the runtime's message.
 int32_t check_launch(const char* what);
 
+// mie_kv_append with `pos_bias` added to every position: pos_bias = -1 with
+// positions = the sequences' lengths appends each sequence's last token.
+int32_t kv_append_impl(void* k_pool, void* v_pool, int64_t pool_stride_block, int64_t pool_stride_head,
+                       int32_t num_blocks, const void* k_new, const void* v_new, int64_t new_stride_b,
+                       int64_t new_stride_h, int64_t new_stride_s, const int32_t* block_tables,
+                       int64_t block_table_stride, const int32_t* positions, int32_t position, int32_t pos_bias,
+                       int32_t batch, int32_t seq_len, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                       int32_t dtype, void* stream);
+
 // Unsigned division by a runtime divisor d >= 1 for numerators n < 2^31:
 //   q = (umulhi(n, magic) + n) >> shift,  shift = ceil(log2 d),
 //   magic = floor(2^32 * (2^shift - d) / d) + 1

@@ -172,6 +172,11 @@ struct DecodeArgs {
   float* ws_acc;  // [B, H, max_parts, D]
   int32_t max_parts;
   int32_t part_shift;  // partition = 1 << part_shift tokens
+  // Fused append (workgroup form): the new token's K/V rows [B, H, D]; NULL
+  // for a plain decode.  The token is the sequence's last (position ctx - 1).
+  const char* k_new;
+  const char* v_new;
+  int64_t new_sb, new_sh;  // elements
 };
 
 __device__ __forceinline__ int seq_ctx(const DecodeArgs& a, int b) {
@@ -505,19 +510,26 @@ template <int DT, int D, bool FAST>
 __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
 void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   using G = Geometry<DT, D>;
-  constexpr int VEC = G::VEC;
-  __shared__ float s_m[kSplitWaves], s_l[kSplitWaves];
-  __shared__ float s_acc[kSplitWaves][D];
+  constexpr int VEC = G::VEC, NW = G::NW, LPT = G::LPT, ELT = G::ELT;
+  constexpr int kStates = kSplitWaves + 1;  // the waves' slices, then a fused append's new token
+  __shared__ float s_m[kStates], s_l[kStates];
+  __shared__ float s_acc[kStates][D];
   __shared__ int s_bad;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int h = blockIdx.x;
   const int b = order.n > 0 ? order.seq[blockIdx.y] : blockIdx.y;
   const int ctx = seq_ctx(a, b);
-  const int per_wave = (ctx + kSplitWaves - 1) / kSplitWaves;
+  // With a fused append the new token (the last, ctx - 1) comes from the
+  // caller's rows, not the pool: the waves read tokens [0, ctx - 1), the last
+  // wave - whose slice is the shortest - stores the rows into the pool and
+  // supplies the token's (max, sum, acc) state from registers.
+  const bool append = a.k_new != nullptr && ctx > 0;
+  const int pool_ctx = append ? ctx - 1 : ctx;
+  const int per_wave = (pool_ctx + kSplitWaves - 1) / kSplitWaves;
   const int chunk = (per_wave + G::TILE - 1) / G::TILE * G::TILE;
-  const int t_begin = min(ctx, wave * chunk);
-  const int t_end = min(ctx, t_begin + chunk);
+  const int t_begin = min(pool_ctx, wave * chunk);
+  const int t_end = min(pool_ctx, t_begin + chunk);
   if (threadIdx.x == 0) s_bad = 0;
   float m = -INFINITY, l = 0.f, acc[VEC];
 #pragma unroll
@@ -525,28 +537,84 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   bool bad = false;
   if (t_begin < t_end) attend_range<DT, D, FAST>(a, b, h, t_begin, t_end, lane, m, l, acc, bad);
   __syncthreads();  // s_bad is cleared
-  const int jl = lane % G::LPT;
+  const int g = lane / LPT;
+  const int jl = lane % LPT;
+  const bool jv = jl < G::NV;
   if (lane == 0) {
     s_m[wave] = m;
     s_l[wave] = l;
     if (bad) s_bad = 1;
   }
-  if (lane / G::LPT == 0 && jl < G::NV) {
+  if (g == 0 && jv) {
 #pragma unroll
     for (int i = 0; i < VEC; ++i) s_acc[wave][jl * VEC + i] = acc[i];
+  }
+  if (append && wave == kSplitWaves - 1) {
+    const int64_t row = (b * a.new_sb + h * a.new_sh + jl * VEC) * ELT;
+    Words<NW> kw, vw, qw;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) kw.w[w] = vw.w[w] = qw.w[w] = 0u;
+    if (jv) {
+      kw = load_words<NW>(a.k_new + row);
+      vw = load_words<NW>(a.v_new + row);
+      qw = load_words<NW>(a.q + (b * a.q_sb + h * a.q_sh + jl * VEC) * ELT);
+    }
+    // Store the rows at position ctx - 1 (bounds-checked like the append kernel).
+    const uint32_t p = static_cast<uint32_t>(ctx - 1);
+    const uint32_t lb = a.bs.div(p);
+    const int32_t phys = lb < a.bt_cap ? a.bt[b * a.bt_stride + lb] : -1;
+    const bool ok = phys >= 0 && phys < a.num_blocks;
+    if (ok && g == 0 && jv) {
+      const int64_t off = (phys * a.kv_sblk + h * a.kv_sh + static_cast<int64_t>(p - lb * a.bs.d) * D + jl * VEC) * ELT;
+      if constexpr (NW == 4) {
+        *reinterpret_cast<u32x4_t*>(const_cast<char*>(a.k) + off) = u32x4_t{kw.w[0], kw.w[1], kw.w[2], kw.w[3]};
+        *reinterpret_cast<u32x4_t*>(const_cast<char*>(a.v) + off) = u32x4_t{vw.w[0], vw.w[1], vw.w[2], vw.w[3]};
+      } else {
+        *reinterpret_cast<u32x2_t*>(const_cast<char*>(a.k) + off) = u32x2_t{kw.w[0], kw.w[1]};
+        *reinterpret_cast<u32x2_t*>(const_cast<char*>(a.v) + off) = u32x2_t{vw.w[0], vw.w[1]};
+      }
+    }
+    // The token's score, computed as the pool path computes one (consume()).
+    float dot = 0.f;
+    if constexpr (DT == MIE_DTYPE_BF16) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        dot = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, kw.w[w]), __builtin_bit_cast(bf16x2_t, qw.w[w]),
+                                              dot, false);
+      dot = mie::group_sum<LPT>(dot) * a.qk_scale;
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) dot = fmaf(__uint_as_float(kw.w[i]), __uint_as_float(qw.w[i]) * a.qk_scale, dot);
+      dot = mie::group_sum<LPT>(dot);
+    }
+    if (lane == 0) {
+      s_m[kSplitWaves] = dot;
+      s_l[kSplitWaves] = 1.f;
+      if (!ok) s_bad = 1;
+    }
+    if (g == 0 && jv) {
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        if constexpr (DT == MIE_DTYPE_BF16) {
+          s_acc[kSplitWaves][jl * VEC + 2 * w] = mie::bf16_lo(vw.w[w]);
+          s_acc[kSplitWaves][jl * VEC + 2 * w + 1] = mie::bf16_hi(vw.w[w]);
+        } else {
+          s_acc[kSplitWaves][jl * VEC + w] = __uint_as_float(vw.w[w]);
+        }
+      }
+    }
   }
   __syncthreads();
   // Threads 0 .. D/4-1 merge four output elements each.
   const int col = threadIdx.x * 4;
   if (col >= D) return;
+  const int states = append ? kStates : kSplitWaves;
   float mx = -INFINITY;
-#pragma unroll
-  for (int w = 0; w < kSplitWaves; ++w) mx = fmaxf(mx, s_m[w]);
+  for (int w = 0; w < states; ++w) mx = fmaxf(mx, s_m[w]);
   const float mr = mx == -INFINITY ? 0.f : mx;
   float lt = 0.f;
   float o[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int w = 0; w < kSplitWaves; ++w) {
+  for (int w = 0; w < states; ++w) {
     const float wt = mie::fast_exp2(s_m[w] - mr);
     lt += s_l[w] * wt;
 #pragma unroll
@@ -803,17 +871,17 @@ extern "C" int32_t mie_paged_decode_plan(int32_t batch, int32_t num_heads, int32
   return MIE_OK;
 }
 
-extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
-                                    const void* k_pool, const void* v_pool, int64_t pool_stride_block,
-                                    int64_t pool_stride_head, int32_t num_blocks,
-                                    const int32_t* block_tables, int64_t block_table_stride,
-                                    const int32_t* ctx_lens, const int32_t* ctx_lens_host,
-                                    int32_t ctx_len, int32_t max_ctx_len,
-                                    int32_t batch, int32_t num_heads, int32_t head_dim,
-                                    int32_t block_size, float scale, void* out, int64_t out_stride_b,
-                                    int64_t out_stride_h, int32_t out_dtype, void* workspace,
-                                    int64_t workspace_bytes, int32_t partition_tokens, int32_t dtype,
-                                    void* stream) {
+namespace {
+
+// mie_paged_decode, and with k_new / v_new (rows [B, H, D]) mie_paged_decode_append.
+int32_t decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_pool, const void* v_pool,
+                    int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                    const int32_t* block_tables, int64_t block_table_stride, const int32_t* ctx_lens,
+                    const int32_t* ctx_lens_host, int32_t ctx_len, int32_t max_ctx_len, int32_t batch,
+                    int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, void* out,
+                    int64_t out_stride_b, int64_t out_stride_h, int32_t out_dtype, void* workspace,
+                    int64_t workspace_bytes, int32_t partition_tokens, const void* k_new, const void* v_new,
+                    int64_t new_stride_b, int64_t new_stride_h, int32_t dtype, void* stream) {
   Plan p;
   int32_t rc = plan(batch, num_heads, head_dim, block_size, max_ctx_len, dtype, partition_tokens, &p);
   if (rc != MIE_OK) return rc;
@@ -850,8 +918,15 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
                         aligned(out, vec * oelt) && (out_stride_b * oelt) % (vec * oelt) == 0 &&
                         (out_stride_h * oelt) % (vec * oelt) == 0 && (vec * oelt) % ob == 0;
   if (!ok_align) return mie::fail(MIE_ERR_INVALID, "mie_paged_decode: misaligned q / pool / out");
+  if ((k_new == nullptr) != (v_new == nullptr))
+    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_append: pass both k_new and v_new");
+  if (k_new && !(aligned(k_new, vb) && aligned(v_new, vb) && (new_stride_b * elt) % vb == 0 &&
+                 (new_stride_h * elt) % vb == 0))
+    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_append: misaligned new rows");
+  if (k_new && !ctx_lens && ctx_len < 1)
+    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_append: ctx_len %d leaves no slot for the new token", ctx_len);
 
-  DecodeArgs a;
+  DecodeArgs a{};
   a.q = static_cast<const char*>(q);
   a.q_sb = q_stride_b;
   a.q_sh = q_stride_h;
@@ -915,5 +990,57 @@ extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q
               [&](uint16_t x, uint16_t y) { return len(x) > len(y) || (len(x) == len(y) && x < y); });
     order.n = batch;
   }
+  if (k_new) {
+    if (p.wg) {
+      // The decode kernel stores the rows and attends to the new token itself.
+      a.k_new = static_cast<const char*>(k_new);
+      a.v_new = static_cast<const char*>(v_new);
+      a.new_sb = new_stride_b;
+      a.new_sh = new_stride_h;
+    } else {
+      // Partition form: append each sequence's last token first (same stream).
+      const int32_t rc = mie::kv_append_impl(const_cast<void*>(k_pool), const_cast<void*>(v_pool), pool_stride_block,
+                                             pool_stride_head, num_blocks, k_new, v_new, new_stride_b, new_stride_h, 0,
+                                             block_tables, block_table_stride, ctx_lens, ctx_len, -1, batch, 1,
+                                             num_heads, head_dim, block_size, dtype, stream);
+      if (rc != MIE_OK) return rc;
+    }
+  }
   return dispatch(dtype, head_dim, a, batch, p.fast, p.wg, order, flat_items, static_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                    const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                                    int64_t pool_stride_head, int32_t num_blocks,
+                                    const int32_t* block_tables, int64_t block_table_stride,
+                                    const int32_t* ctx_lens, const int32_t* ctx_lens_host,
+                                    int32_t ctx_len, int32_t max_ctx_len,
+                                    int32_t batch, int32_t num_heads, int32_t head_dim,
+                                    int32_t block_size, float scale, void* out, int64_t out_stride_b,
+                                    int64_t out_stride_h, int32_t out_dtype, void* workspace,
+                                    int64_t workspace_bytes, int32_t partition_tokens, int32_t dtype,
+                                    void* stream) {
+  return decode_impl(q, q_stride_b, q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks,
+                     block_tables, block_table_stride, ctx_lens, ctx_lens_host, ctx_len, max_ctx_len, batch,
+                     num_heads, head_dim, block_size, scale, out, out_stride_b, out_stride_h, out_dtype, workspace,
+                     workspace_bytes, partition_tokens, nullptr, nullptr, 0, 0, dtype, stream);
+}
+
+extern "C" int32_t mie_paged_decode_append(const void* q, int64_t q_stride_b, int64_t q_stride_h, void* k_pool,
+                                           void* v_pool, int64_t pool_stride_block, int64_t pool_stride_head,
+                                           int32_t num_blocks, const int32_t* block_tables,
+                                           int64_t block_table_stride, const int32_t* ctx_lens,
+                                           const int32_t* ctx_lens_host, int32_t ctx_len, int32_t max_ctx_len,
+                                           int32_t batch, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                                           float scale, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                           int32_t out_dtype, void* workspace, int64_t workspace_bytes,
+                                           int32_t partition_tokens, const void* k_new, const void* v_new,
+                                           int64_t new_stride_b, int64_t new_stride_h, int32_t dtype, void* stream) {
+  if (!k_new || !v_new) return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_append: null new rows");
+  return decode_impl(q, q_stride_b, q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks,
+                     block_tables, block_table_stride, ctx_lens, ctx_lens_host, ctx_len, max_ctx_len, batch,
+                     num_heads, head_dim, block_size, scale, out, out_stride_b, out_stride_h, out_dtype, workspace,
+                     workspace_bytes, partition_tokens, k_new, v_new, new_stride_b, new_stride_h, dtype, stream);
 }

@@ -61,6 +61,8 @@ def decode_layer(
     out_dtype: torch.dtype = None,
     partition_tokens: int = 0,
     context_lens_host=None,
+    k_new: torch.Tensor = None,
+    v_new: torch.Tensor = None,
 ) -> torch.Tensor:
     """Decode attention for q [B, H, D] over one layer's pools [NB, H, BS, D].
 
@@ -70,6 +72,11 @@ def decode_layer(
     the launch hold exactly the batch's work items (no idle workgroups on
     ragged batches).  block_tables is int32 [B, max_blocks], or 1-D when B == 1.
     Returns out [B, H, D] in `out_dtype` (q's dtype or float32).
+
+    With k_new / v_new ([B, H, D], the pools' dtype) the step's append is
+    fused in: each sequence's new token is its last context token, stored at
+    position ctx_b - 1 through the table and attended to (mie_paged_decode_append;
+    one launch when the plan takes the workgroup form).
     """
     lib = _native.lib()
     if q.dim() != 3:
@@ -130,6 +137,30 @@ def decode_layer(
         batch, heads, head_dim, block_size, int(max_context_len), q.dtype, int(partition_tokens)
     )
     ws = _workspace(ws_bytes, q.device)
+    if k_new is not None or v_new is not None:
+        if k_new is None or v_new is None:
+            raise ValueError("pass both k_new and v_new")
+        for t in (k_new, v_new):
+            if t.shape != (batch, heads, head_dim) or t.dtype != k_layer.dtype or t.device != q.device:
+                raise ValueError(f"new rows must be [{batch}, {heads}, {head_dim}] {k_layer.dtype} on q's device")
+        if k_new.stride() != v_new.stride() or k_new.stride(2) != 1:
+            k_new, v_new = k_new.contiguous(), v_new.contiguous()
+        _native.check(
+            lib.mie_paged_decode_append(
+                q.data_ptr(), q.stride(0), q.stride(1),
+                k_layer.data_ptr(), v_layer.data_ptr(), k_layer.stride(0), k_layer.stride(1), nb,
+                block_tables.data_ptr(), bt_stride,
+                ctx_ptr, host_lens, int(context_len), int(max_context_len),
+                batch, heads, head_dim, block_size,
+                float(scale),
+                out.data_ptr(), out.stride(0), out.stride(1), _native.dtype_code(out.dtype),
+                _native.ptr(ws), ws_bytes, int(partition_tokens),
+                k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+                _native.dtype_code(q.dtype), _native.stream_of(q),
+            ),
+            "mie_paged_decode_append",
+        )
+        return out
     _native.check(
         lib.mie_paged_decode(
             q.data_ptr(), q.stride(0), q.stride(1),

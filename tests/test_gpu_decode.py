@@ -287,3 +287,64 @@ def test_explicit_scale():
     want = ref.attention_fp64(ref.to_f64(w.q[0]), ref.to_f64(k), ref.to_f64(v), scale=0.05)
     np.testing.assert_allclose(got[0].cpu().numpy(), want, rtol=0, atol=1e-5)
     assert math.isfinite(float(got.abs().max()))
+
+
+def take_last_tokens(w):
+    """The new rows of a fused append: each sequence's last token's K/V, read
+    from the pool and then zeroed there, so only the fused store can restore it."""
+    heads, dim = w.k_pool.shape[2], w.k_pool.shape[4]
+    bs = w.k_pool.shape[3]
+    k_new = torch.zeros(len(w.lens), heads, dim, dtype=w.k_pool.dtype, device=w.k_pool.device)
+    v_new = torch.zeros_like(k_new)
+    for b, ctx in enumerate(w.lens):
+        if ctx == 0:
+            continue
+        blk, slot = w.tables[b][(ctx - 1) // bs], (ctx - 1) % bs
+        k_new[b] = w.k_pool[w.layer, blk, :, slot]
+        v_new[b] = w.v_pool[w.layer, blk, :, slot]
+        w.k_pool[w.layer, blk, :, slot] = 0
+        w.v_pool[w.layer, blk, :, slot] = 0
+    return k_new, v_new
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("partition", [0, -1, 64])
+@pytest.mark.parametrize("host_lens", [False, True])
+def test_fused_append_decode_matches_append_then_decode(dtype, partition, host_lens):
+    """mie_paged_decode_append: the pools end bit-identical to appending the
+    new tokens (mie_kv_append's closed form), and the output is the oracle's
+    attention over the full contexts - in the workgroup form (one launch) and
+    in the partition form (append launch, then decode)."""
+    print_case("fused append", dtype, partition, host_lens)
+    lens = [0, 1, 2, 17, 300, 1000, 3000]
+    w = make_workload(lens, block_size=16, dtype=dtype, seed=21, heavy_fraction=0.01)
+    want = oracle_outputs(w)
+    k_before, v_before = w.k_pool.clone(), w.v_pool.clone()
+    k_new, v_new = take_last_tokens(w)
+    got = paged_attention.decode_batched(
+        w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, out_dtype=torch.float32,
+        partition_tokens=partition, context_lens_host=w.lens if host_lens else None, k_new=k_new, v_new=v_new,
+    )
+    assert np.array_equal(ref.raw_bits(w.k_pool.cpu()), ref.raw_bits(k_before.cpu()))
+    assert np.array_equal(ref.raw_bits(w.v_pool.cpu()), ref.raw_bits(v_before.cpu()))
+    assert torch.equal(got[0], torch.zeros_like(got[0]))
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=0, atol=1e-5 if dtype == torch.float32 else 2e-3)
+
+
+def test_fused_append_to_an_unmapped_block_is_skipped_and_reported():
+    """A new token whose block id lies outside the pool is not stored and its
+    (sequence, head) outputs are NaN; the other sequences are exact."""
+    w = make_workload([33, 40], block_size=16, dtype=torch.float32, seed=22)
+    want = oracle_outputs(w, [0])
+    k_new, v_new = take_last_tokens(w)
+    w.block_tables[1, (40 - 1) // 16] = w.k_pool.shape[1] + 3
+    k_before = w.k_pool.clone()
+    got = paged_attention.decode_batched(
+        w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, partition_tokens=-1,
+        k_new=k_new[:, :, :].contiguous(), v_new=v_new,
+    )
+    assert torch.isnan(got[1]).all()
+    np.testing.assert_allclose(got[0].cpu().numpy(), want[0], rtol=0, atol=1e-5)
+    # Only sequence 0's new token was stored.
+    diff = (w.k_pool != k_before).nonzero()
+    assert diff.numel() > 0 and all(int(i) == w.tables[0][(33 - 1) // 16] for i in diff[:, 1])
