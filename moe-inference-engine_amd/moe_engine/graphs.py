@@ -163,3 +163,51 @@ def generate_graphed(model, token_ids, max_new_tokens, cache, partition_tokens=0
             decoder.prime(next_token)
         next_token = decoder.step()
     return torch.cat(out, dim=1)
+
+
+class GraphedGenerator:
+    """generate_graphed for a sequence of requests on one cache object: the
+    step graph is captured on the first request and replayed by every later
+    one (the cache is freed after each request; its device block table, which
+    the graph reads, stays).  Requests must not overlap."""
+
+    def __init__(self, model, cache, partition_tokens=0):
+        if not isinstance(cache, PagedKVCache):
+            raise ValueError("graph decode needs a paged cache")
+        self.model = model
+        self.cache = cache
+        self.partition_tokens = partition_tokens
+        self.decoder = None
+
+    @torch.no_grad()
+    def generate(self, token_ids, max_new_tokens):
+        """Greedy tokens as Model.generate(..., temperature=0) returns them."""
+        model, cache = self.model, self.cache
+        if max_new_tokens < 1:
+            raise ValueError("max_new_tokens must be at least 1")
+        if token_ids.dim() == 1:
+            token_ids = token_ids.unsqueeze(0)
+        token_ids = token_ids.to(model.token_embedding.weight.device).long()
+        if token_ids.shape[0] != 1 or token_ids.shape[1] == 0:
+            raise ValueError("generate() handles one non-empty sequence")
+        if token_ids.shape[1] > model.max_seq_length:
+            raise ValueError(f"prompt is {token_ids.shape[1]} tokens; max_seq_length is {model.max_seq_length}")
+        cache.free()
+        try:
+            out = [token_ids]
+            logits = model(token_ids, cache)[:, -1, :]
+            next_token = torch.argmax(logits, dim=-1, keepdim=True)
+            for step in range(max_new_tokens):
+                if next_token.item() == EOS_TOKEN_ID:
+                    break
+                out.append(next_token.clone())
+                if step == max_new_tokens - 1 or cache.position >= model.max_seq_length:
+                    break
+                if step == 0:
+                    if self.decoder is None:
+                        self.decoder = GraphedDecoder(model, cache, self.partition_tokens)
+                    self.decoder.prime(next_token)
+                next_token = self.decoder.step()
+            return torch.cat(out, dim=1)
+        finally:
+            cache.free()

@@ -9,6 +9,11 @@ paged pool sized for one maximum-length request (ceil(max_seq_length / 16)
 blocks, scripts/serve.py:147-155), blocks returned in `finally`
 (scripts/serve.py:103-115), and the same response fields.
 
+One addition: `--decode-graph` (paged cache on a ROCm device) serves greedy
+requests (temperature 0) by replaying one captured HIP graph per decode step
+(moe_engine.graphs); the graph is captured on the first such request and
+reused by every later one.  Other requests take Model.generate.
+
 Differences forced by this environment:
   * --checkpoint loads the reference's checkpoint format
     ({"model", "model_config", "step", ...}, read with weights_only=True,
@@ -80,6 +85,7 @@ enc = make_tokenizer()
 model = None  # set by main() or by tests
 cache_mode = "contiguous"
 allocator = None  # shared paged pool, paged mode only
+graph_generator = None  # --decode-graph: greedy requests replay a captured decode step
 device = "cpu"
 # The pool holds one max-length sequence, so requests run one at a time.
 generate_lock = threading.Lock()
@@ -111,6 +117,8 @@ def build_parser() -> argparse.ArgumentParser:
                         help="paged cache only: direct HIP kernel, gather oracle, or automatic fallback")
     parser.add_argument("--moe", choices=["auto", "direct", "reference"], default="auto",
                         help="MoE decode mode")
+    parser.add_argument("--decode-graph", action="store_true",
+                        help="paged cache on a GPU: replay greedy decode steps from a captured HIP graph")
     return parser
 
 
@@ -145,13 +153,16 @@ def generate(req: GenerateRequest):
     prompt_ids = torch.tensor(ids, device=device)
 
     with generate_lock:
-        cache = new_request_cache()
         start = time.perf_counter()
-        try:
-            out = model.generate(prompt_ids, max_new_tokens=req.max_new_tokens, temperature=req.temperature,
-                                 top_k=50, cache=cache)
-        finally:
-            release_request_cache(cache)
+        if graph_generator is not None and req.temperature == 0:
+            out = graph_generator.generate(prompt_ids, req.max_new_tokens)
+        else:
+            cache = new_request_cache()
+            try:
+                out = model.generate(prompt_ids, max_new_tokens=req.max_new_tokens, temperature=req.temperature,
+                                     top_k=50, cache=cache)
+            finally:
+                release_request_cache(cache)
         elapsed = time.perf_counter() - start
 
     new_ids = out[0, len(ids):].tolist()
@@ -170,8 +181,21 @@ def generate(req: GenerateRequest):
     }
 
 
+def enable_decode_graph() -> None:
+    """Serve greedy requests through a GraphedGenerator on its own paged cache
+    (a second pool of the same size, so ordinary requests keep theirs)."""
+    global graph_generator
+    from moe_engine.graphs import GraphedGenerator
+
+    if cache_mode != "paged" or allocator is None or not allocator.on_device:
+        raise SystemExit("--decode-graph needs --cache paged on a GPU")
+    pool = model.new_block_allocator(num_blocks=allocator.num_blocks, block_size=allocator.block_size,
+                                     attention_mode=allocator.attention_mode)
+    graph_generator = GraphedGenerator(model, pool.new_cache())
+
+
 def main(argv=None) -> None:
-    global model, cache_mode, allocator, device
+    global model, cache_mode, allocator, device, graph_generator
     args = build_parser().parse_args(argv)
     device = ("cuda" if torch.cuda.is_available() else "cpu") if args.device == "auto" else args.device
     if device == "cuda" and not torch.cuda.is_available():
@@ -184,6 +208,9 @@ def main(argv=None) -> None:
         num_blocks = -(-model.max_seq_length // BLOCK_SIZE)
         allocator = model.new_block_allocator(num_blocks=num_blocks, block_size=BLOCK_SIZE,
                                               attention_mode=args.paged_attention)
+    graph_generator = None
+    if args.decode_graph:
+        enable_decode_graph()
     print(f"Serving {meta['source']} on {device} with {cache_mode} KV cache "
           f"({args.paged_attention} attention), {args.moe} MoE, tokenizer {enc.name}")
     import uvicorn
