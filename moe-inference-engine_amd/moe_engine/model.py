@@ -400,12 +400,15 @@ class Expert(nn.Module):
 class MoEFeedForward(nn.Module):
     """Top-k mixture of experts (model.py:285-481).
 
-    Prefill, and decode in mode 'reference', run the reference's PyTorch path
-    (model.py:443-461).  One-token decode in mode 'auto' or 'direct' runs the
-    fused HIP kernels (moe_engine.fused_moe) where they apply: a ROCm device,
-    the HIP library, float32, one token.  'auto' falls back to the PyTorch path
-    elsewhere; a forced 'direct' that cannot run raises before any cache
-    mutation, through the model's decode preflight (model.py:408-441).
+    Mode 'reference' runs the reference's PyTorch path (model.py:443-461)
+    everywhere.  In mode 'auto' or 'direct', one-token decode runs the fused
+    HIP kernels (moe_engine.fused_moe) where they apply - a ROCm device, the
+    HIP library, float32, one token - and a float32 prefill of up to 512
+    tokens on a ROCm device runs dense-masked (_forward_dense: the reference's
+    result without its per-expert synchronisations).  'auto' falls back to the
+    PyTorch path elsewhere; a forced 'direct' decode that cannot run raises
+    before any cache mutation, through the model's decode preflight
+    (model.py:408-441).
 
     The experts' parameters are views into four canonical contiguous storages
     (`_expert_storage`: w1 [E, hidden, dim], b1 [E, hidden], w2 [E, dim,
@@ -547,9 +550,51 @@ class MoEFeedForward(nn.Module):
             hidden=self._expert_hidden, out=self._direct_out,
         )
 
+    # Prefill of at most this many tokens runs dense-masked on the GPU.
+    DENSE_PREFILL_MAX_TOKENS = 512
+
+    def uses_dense_prefill(self, x: torch.Tensor, *, decode: bool) -> bool:
+        """Multi-token (or mode 'auto'/'direct' prefill) float32 input on a
+        ROCm device with the canonical layout takes _forward_dense; everything
+        else keeps the reference path."""
+        tokens = x.shape[0] * x.shape[1]
+        return (
+            self.mode != "reference"
+            and not (decode and tokens == 1)
+            and 1 <= tokens <= self.DENSE_PREFILL_MAX_TOKENS
+            and _native.is_rocm_device(x)
+            and x.dtype == torch.float32
+            and self.router.weight.dtype == torch.float32
+            and self._expert_storage["w1"].dtype == torch.float32
+        )
+
+    def _forward_dense(self, x: torch.Tensor) -> torch.Tensor:
+        """The reference path's result (model.py:443-461) without its
+        per-expert torch.where synchronisations: every expert runs on every
+        token as one batched GEMM over the canonical storages, and the
+        experts' weighted outputs are summed in increasing expert id, each
+        product rounded before its add.  For a token's selected experts that is
+        index_add_'s order and rounding; the unselected experts add exact zeros
+        (routing weight 0).  Routing is the reference's: float32 logits,
+        torch.topk, softmax over the top-k."""
+        batch, seq_len, dim = x.shape
+        flat = x.reshape(-1, dim)
+        logits = F.linear(flat, self.router.weight)
+        top_logits, top_ids = torch.topk(logits, k=self.top_k, dim=-1)
+        dense_w = torch.zeros_like(logits).scatter_(1, top_ids, F.softmax(top_logits, dim=-1))
+        s = self._expert_storage
+        h = F.gelu(torch.matmul(flat, s["w1"].transpose(1, 2)) + s["b1"].unsqueeze(1))  # [E, T, hidden]
+        y = torch.matmul(h, s["w2"].transpose(1, 2)) + s["b2"].unsqueeze(1)  # [E, T, dim]
+        out = torch.zeros_like(flat)
+        for e in range(self.num_experts):
+            out = out + dense_w[:, e : e + 1] * y[e]
+        return out.reshape(batch, seq_len, dim)
+
     def forward(self, x, *, decode=False):
         if self.uses_direct(x, decode=decode):
             return self._forward_direct(x)
+        if self.uses_dense_prefill(x, decode=decode):
+            return self._forward_dense(x)
         return self._forward_reference(x)
 
     def fused_block_decode(self, x, norm):

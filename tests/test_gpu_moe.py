@@ -276,3 +276,45 @@ def test_model_block_fusion_matches_reference_block():
             steps += [model(ids[:, t : t + 1], cache)[:, -1] for t in range(16, 24)]
         logits[mode] = torch.stack(steps, 1)
     torch.testing.assert_close(logits["auto"], logits["reference"], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dim,hidden,experts,top_k,tokens", [(768, 2048, 8, 2, 32), (768, 3072, 8, 2, 7),
+                                                             (64, 256, 16, 4, 512), (128, 64, 3, 1, 1)])
+def test_dense_prefill_matches_pytorch_path(dim, hidden, experts, top_k, tokens):
+    """_forward_dense (every expert on every token, summed in id order with the
+    unselected weights zero) against the reference path on the same layer:
+    the same routing, outputs equal to float32 GEMM rounding."""
+    print_case("dense prefill", dim, hidden, experts, top_k, tokens)
+    layer = moe(dim, hidden, experts, top_k, mode="auto")
+    x = torch.randn(1, tokens, dim, device="cuda")
+    with torch.no_grad():
+        assert layer.uses_dense_prefill(x, decode=False)
+        got = layer(x)
+        want = layer._forward_reference(x)
+    assert_output_close(got, want)
+
+
+def test_dense_prefill_applies_only_where_it_should():
+    layer = moe(64, 128, 4, 2, mode="auto")
+    x = torch.randn(1, 8, 64, device="cuda")
+    assert layer.uses_dense_prefill(x, decode=False)
+    assert not layer.uses_dense_prefill(x.double(), decode=False)
+    assert not layer.uses_dense_prefill(torch.randn(1, 513, 64, device="cuda"), decode=False)
+    assert not layer.uses_dense_prefill(x.cpu(), decode=False)
+    layer.set_mode("reference")
+    assert not layer.uses_dense_prefill(x, decode=False)
+
+
+def test_model_prefill_with_dense_moe_matches_reference_mode():
+    """A 40-token prefill through the whole model (float32), mode auto (dense
+    MoE prefill) vs mode reference: logits within 1e-4."""
+    torch.manual_seed(0)
+    model = Model(ModelConfig(max_seq_length=128, vocab_size=512, num_layers=2, hidden_dim=128, num_heads=4,
+                              num_experts=8, top_k=2)).to("cuda").eval()
+    ids = torch.randint(0, 512, (1, 40), device="cuda")
+    logits = {}
+    for mode in ("reference", "auto"):
+        model.set_moe_mode(mode)
+        with torch.no_grad():
+            logits[mode] = model(ids, model.new_cache())
+    torch.testing.assert_close(logits["auto"], logits["reference"], atol=1e-4, rtol=1e-4)
