@@ -17,6 +17,7 @@
  *   mie_moe_route     <- fused_moe.route         src/moe_engine/fused_moe.py:274-309
  *   mie_moe_decode    <- fused_moe.decode        src/moe_engine/fused_moe.py:312-380
  *   mie_moe_decode_block <- the block's x + moe(moe_norm(x)) for one token  src/moe_engine/model.py:446-449
+ *   mie_argmax        <- Model.generate's greedy torch.argmax   src/moe_engine/model.py:603
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -70,7 +71,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 7
+#define MIE_ABI_VERSION 8
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -309,6 +310,15 @@ int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* l
                              int32_t num_experts, int32_t top_k, int32_t dim, int32_t hidden,
                              void* router_logits, void* expert_ids, void* route_weights,
                              void* hidden_act, void* out, int32_t dtype, void* stream);
+
+/*
+ * Greedy pick (Model.generate at temperature 0, model.py:603): the index
+ * of the largest of x[0..n) (float32), as torch.argmax returns it - the first
+ * index of the maximum, NaN counting as larger than every number - written to
+ * *out as int64.  One launch of one workgroup; nothing to clear beforehand.
+ * 0 < n < 2^31 - 8192.
+ */
+int32_t mie_argmax(const void* x, int64_t n, void* out, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -109,6 +109,7 @@ _SIGNATURES = {
          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # logits, ids, weights, hidden, out
          _i32, _c_void_p],  # dtype, stream
     ),
+    "mie_argmax": (_i32, [_c_void_p, _i64, _c_void_p, _i32, _c_void_p]),  # x, n, out (int64), dtype, stream
     "mie_moe_decode_block": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _f32,  # x, norm weight, norm bias, eps

@@ -4,12 +4,11 @@ A decode step of the engine launches ~15 kernels per layer; on the eager path
 the host spends longer issuing them than the GPU spends running them.  Here
 one step - embeddings, every layer (QKV projection, HIP KV append, HIP paged
 decode, fused HIP MoE), final norm, output projection - is captured once and
-replayed for every later token; the greedy argmax runs eagerly after each
-replay.
+replayed for every later token, the greedy pick included.
 
 Everything that changes from step to step lives on the device: the token fed
-in (the previous step's argmax, written to a fixed buffer), the position of the
-new token and the context length (incremented by the graph).  The paged cache
+in (the previous step's argmax, written by the graph into a fixed buffer), the
+position of the new token and the context length (incremented by the graph).  The paged cache
 is put in graph mode (PagedKVCache.graph_pos / graph_ctx), so the append and
 the decode read those device values and the decode launch is sized for the
 pool's capacity (partition_tokens 0 lets the library plan it for that bound:
@@ -23,7 +22,7 @@ run the direct kernel is captured; everything else uses Model.generate.
 
 import torch
 
-from moe_engine import paged_attention
+from moe_engine import _native, paged_attention
 from moe_engine.model import EOS_TOKEN_ID, PagedKVCache
 
 
@@ -32,9 +31,9 @@ class GraphedDecoder:
 
     The cache must already hold the prompt (cache.position > 0).  prime(token)
     sets the token to decode next; each step() appends it, attends, and leaves
-    the next greedy token in `next_token` (and the logits in `logits`).  From
-    the second step on `logits` is the graph's output buffer, overwritten by
-    the next replay: clone it if it must outlive the step.
+    the next greedy token in `next_token` (and the logits in `logits`).  Both
+    are the decoder's buffers, overwritten by the next step: clone what must
+    outlive it.
     """
 
     def __init__(self, model, cache, partition_tokens=0):
@@ -71,19 +70,19 @@ class GraphedDecoder:
         c.graph_partition_tokens = self.partition_tokens if on else 0
 
     def _forward_body(self):
-        """The captured part: one forward step and the device position update."""
+        """The captured step: the forward pass, the greedy pick written into
+        the token buffer the next step reads, and the position update."""
         logits = self.model(self.token, self.cache)[:, -1, :]
+        # mie_argmax is one workgroup with nothing to clear (torch.argmax over
+        # a row this wide reduces across workgroups behind a memset, which a
+        # graph must not hold).
+        rc = _native.lib().mie_argmax(logits.data_ptr(), logits.shape[-1], self.token.data_ptr(), 0,
+                                      _native.stream_of(logits))
+        if rc:
+            _native.check(rc, "mie_argmax")
         self.pos.add_(1)
         self.ctx.add_(1)
         return logits
-
-    def _select(self, logits):
-        """Greedy pick, run eagerly after every replay: torch's argmax over a
-        wide row reduces across workgroups and clears its semaphores with a
-        memset, which a graph must not hold."""
-        nxt = torch.argmax(logits, dim=-1, keepdim=True)
-        self.token.copy_(nxt)
-        return nxt
 
     @torch.no_grad()
     def prime(self, token):
@@ -125,7 +124,7 @@ class GraphedDecoder:
                 cache.position += 1
                 self.replays += 1
                 self.logits = self._graph_out
-            self.next_token = self._select(self.logits)
+            self.next_token = self.token
         finally:
             self._graph_mode(False)
         return self.next_token

@@ -128,3 +128,29 @@ def test_config1_graphed_tokens_identical_to_eager():
     got = generate_graphed(model, prompt, 64, cache)
     cache.free()
     assert torch.equal(got, want)
+
+
+def test_argmax_kernel_matches_torch_argmax():
+    """mie_argmax (the graph's greedy pick) against torch.argmax: random rows
+    of several widths, ties (the first index wins), -inf, and NaN (counted as
+    the largest, the first NaN wins)."""
+    from moe_engine import _native
+
+    def pick(x):
+        out = torch.empty(1, dtype=torch.int64, device="cuda")
+        _native.check(_native.lib().mie_argmax(x.data_ptr(), x.numel(), out.data_ptr(), 0,
+                                               _native.stream_of(x)), "mie_argmax")
+        return int(out)
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    for n in (1, 5, 64, 1000, 1024, 1025, 50257, 200003):
+        x = torch.randn(n, generator=g, device="cuda")
+        assert pick(x) == int(torch.argmax(x)), n
+    x = torch.zeros(50257, device="cuda")
+    x[[7, 300, 40000]] = 3.0
+    assert pick(x) == 7 == int(torch.argmax(x))
+    x = torch.full((4096,), -float("inf"), device="cuda")
+    assert pick(x) == 0 == int(torch.argmax(x))
+    x = torch.randn(50257, generator=g, device="cuda")
+    x[[123, 9000]] = float("nan")
+    assert pick(x) == 123 == int(torch.argmax(x))
