@@ -18,6 +18,9 @@
  *   mie_moe_decode    <- fused_moe.decode        src/moe_engine/fused_moe.py:312-380
  *   mie_moe_decode_block <- the block's x + moe(moe_norm(x)) for one token  src/moe_engine/model.py:446-449
  *   mie_argmax        <- Model.generate's greedy torch.argmax   src/moe_engine/model.py:603
+ *   mie_lm_head       <- final_norm + output_projection (model.py:564-565) and,
+ *                        optionally, the greedy argmax (:603) for one token
+ *   mie_embed         <- token_embedding(ids) + positional_embedding(pos)  src/moe_engine/model.py:558
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -71,7 +74,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 8
+#define MIE_ABI_VERSION 9
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -316,9 +319,43 @@ int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* l
  * of the largest of x[0..n) (float32), as torch.argmax returns it - the first
  * index of the maximum, NaN counting as larger than every number - written to
  * *out as int64.  One launch of one workgroup; nothing to clear beforehand.
- * 0 < n < 2^31 - 8192.
+ * 0 < n < 2^31 - 65536.
  */
 int32_t mie_argmax(const void* x, int64_t n, void* out, int32_t dtype, void* stream);
+
+/*
+ * The decode step's head for one token (model.py:564-565, then :603):
+ *     logits[v] = round(W[v, :] . round(LayerNorm(x)) + bias[v])   v < vocab
+ * with the norm skipped when ln_weight is NULL and the bias when bias is NULL
+ * (rounding as mie_qkv_append).  x [dim], W [vocab, dim] row-major (the tied
+ * token embedding), logits [vocab], all in `dtype` (float32 or bfloat16);
+ * dim as for mie_qkv_append_supported.  x, W and the norm parameters 16-byte
+ * aligned.
+ *
+ * token_out (int64, or NULL for the logits only): the index of the largest
+ * stored logit in torch.argmax's order (first index of the maximum, NaN
+ * largest), computed by a second one-workgroup launch from per-workgroup
+ * picks kept in `workspace` (mie_lm_head_workspace(vocab) bytes, 8-byte
+ * aligned).  Nothing needs clearing beforehand, so both launches can be
+ * captured in a graph.
+ */
+/*
+ * Token plus positional embedding (model.py:558) of n tokens:
+ *     out[i, :] = round(token_table[token_ids[i], :] + pos_table[pos_i, :])
+ * with pos_i = positions[i] (device int32) or, when positions is NULL,
+ * position + i.  token_ids are int64; tables [vocab, dim] and
+ * [max_positions, dim] and out [n, dim] in `dtype` (float32 or bfloat16),
+ * summed in float32 and rounded once.  An id or position outside its table
+ * writes a row of NaN.  n <= 65535.
+ */
+int32_t mie_embed(const void* token_ids, const int32_t* positions, int32_t position, int32_t n,
+                  const void* token_table, int32_t vocab, const void* pos_table, int32_t max_positions, int32_t dim,
+                  void* out, int32_t dtype, void* stream);
+
+int64_t mie_lm_head_workspace(int32_t vocab);
+int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* weight,
+                    const void* bias, int32_t vocab, int32_t dim, void* logits, void* token_out, void* workspace,
+                    int64_t workspace_bytes, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -112,4 +112,40 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- greedy pick -------------------------------------------------------------
+// torch.argmax's order: the larger value wins, NaN counts as larger than every
+// number, and between equal values (or two NaNs) the lower index wins.  The
+// order is total over (value, index), so pairs may be merged in any order.
+__device__ __forceinline__ void argmax_take(float& va, int& ia, float vb, int ib) {
+  const bool a_nan = va != va, b_nan = vb != vb;
+  const bool b_wins = (a_nan || b_nan) ? b_nan && (!a_nan || ib < ia) : vb > va || (vb == va && ib < ia);
+  if (b_wins) {
+    va = vb;
+    ia = ib;
+  }
+}
+
+// Merges (v, i) over the 64 lanes; every lane ends with the wave's pick.
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(v, off);
+    const int oi = __shfl_xor(i, off);
+    argmax_take(v, i, ov, oi);
+  }
+}
+
+// One workgroup's pick: (-inf, INT32_MAX) when it had no rows.
+struct ArgmaxPair {
+  float v;
+  int32_t i;
+};
+
+}  // namespace mie
+
+namespace mie {
+// Reduces n per-workgroup picks to the final index, written as int64 to *out
+// (0 if no pair holds an index below `limit`).  One workgroup; nothing to
+// clear beforehand.
+int32_t launch_argmax_pairs(const ArgmaxPair* pairs, int32_t n, int32_t limit, int64_t* out, hipStream_t stream);
 }  // namespace mie

@@ -177,6 +177,11 @@ struct DecodeArgs {
   const char* k_new;
   const char* v_new;
   int64_t new_sb, new_sh;  // elements
+  // Workgroup form with FAST block ids: > 0 when every block a sequence can
+  // use (ceil(max_ctx / block_size) <= kWindow) fits one window.  Each wave
+  // then reads table entries [0, win_blocks) at its start, alongside the
+  // context length, instead of after it.
+  int32_t win_blocks;
 };
 
 __device__ __forceinline__ int seq_ctx(const DecodeArgs& a, int b) {
@@ -211,7 +216,7 @@ __device__ __forceinline__ void store_out(char* base, int64_t elem_off, const fl
 // id outside the pool was met.
 template <int DT, int D, bool FAST>
 __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, int t_begin, int t_end, int lane,
-                                             float& m, float& l, float* acc, bool& bad) {
+                                             float& m, float& l, float* acc, bool& bad, int32_t win_ids = -1) {
   using G = Geometry<DT, D>;
   constexpr int ELT = G::ELT, VEC = G::VEC, NW = G::NW, LPT = G::LPT, TPL = G::TPL;
   constexpr int ROWS = G::ROWS, TILE = G::TILE;
@@ -242,12 +247,18 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
   int fb = 0;
   int32_t ids = 0;
   if constexpr (FAST) {  // the partition's block ids, one per lane
-    fb = t_begin >> a.bs.shift;
-    const int nblk = ((t_end - 1) >> a.bs.shift) - fb + 1;  // <= kWindow by the plan
-    const uint32_t idx = static_cast<uint32_t>(fb + lane);
-    const bool mine = lane < nblk;
-    ids = (mine && idx < a.bt_cap) ? bt[idx] : -1;
-    bad = __any(mine && (ids < 0 || ids >= a.num_blocks));
+    const int first = t_begin >> a.bs.shift;
+    const int last = (t_end - 1) >> a.bs.shift;
+    if (a.win_blocks > 0) {  // entries [0, win_blocks), read by the caller
+      ids = win_ids;
+      bad = __any(lane >= first && lane <= last && (ids < 0 || ids >= a.num_blocks));
+    } else {
+      fb = first;
+      const uint32_t idx = static_cast<uint32_t>(fb + lane);
+      const bool mine = lane <= last - fb;  // <= kWindow blocks by the plan
+      ids = (mine && idx < a.bt_cap) ? bt[idx] : -1;
+      bad = __any(mine && (ids < 0 || ids >= a.num_blocks));
+    }
   }
 
   auto issue = [&](int t0, Words<NW>* kr, Words<NW>* vr) {
@@ -519,6 +530,10 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   const int lane = threadIdx.x & 63;
   const int h = blockIdx.x;
   const int b = order.n > 0 ? order.seq[blockIdx.y] : blockIdx.y;
+  int32_t win_ids = -1;
+  if constexpr (FAST) {
+    if (lane < a.win_blocks && static_cast<uint32_t>(lane) < a.bt_cap) win_ids = a.bt[b * a.bt_stride + lane];
+  }
   const int ctx = seq_ctx(a, b);
   // With a fused append the new token (the last, ctx - 1) comes from the
   // caller's rows, not the pool: the waves read tokens [0, ctx - 1), the last
@@ -535,7 +550,7 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
   bool bad = false;
-  if (t_begin < t_end) attend_range<DT, D, FAST>(a, b, h, t_begin, t_end, lane, m, l, acc, bad);
+  if (t_begin < t_end) attend_range<DT, D, FAST>(a, b, h, t_begin, t_end, lane, m, l, acc, bad, win_ids);
   __syncthreads();  // s_bad is cleared
   const int g = lane / LPT;
   const int jl = lane % LPT;
@@ -989,6 +1004,10 @@ int32_t decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
     std::sort(order.seq, order.seq + batch,
               [&](uint16_t x, uint16_t y) { return len(x) > len(y) || (len(x) == len(y) && x < y); });
     order.n = batch;
+  }
+  if (p.wg && p.fast) {
+    const int64_t blocks = (static_cast<int64_t>(max_ctx_len) + block_size - 1) / block_size;
+    if (blocks <= kWindow) a.win_blocks = static_cast<int32_t>(blocks);
   }
   if (k_new) {
     if (p.wg) {

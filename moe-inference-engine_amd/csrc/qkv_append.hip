@@ -23,16 +23,28 @@
 // (model.py:268 and the block's `x + attention(...)`): out = residual +
 // round(W @ x + b) - one launch in place of a GEMM and an add.
 //
+// With the norm and a pick epilogue it is the decode step's head
+// (model.py:564-565 final_norm + output_projection, then generate's greedy
+// torch.argmax, model.py:603): logits = round(W @ LayerNorm(x) + b), and each
+// workgroup leaves the (value, index) of its largest logit, in torch.argmax's
+// order, for a one-workgroup merge - two launches in place of the norm, the
+// GEMM and a multi-workgroup argmax.
+//
 // A projection reads rows*cols*elt bytes of weights once: HBM-bound
 // (0.5 flop/B in float32).  Weight loads are issued before the norm so their
 // latency overlaps it; they carry the non-temporal hint (each layer's weights
 // are streamed once per token).
+#include <limits.h>
+
 #include "mie_common.h"
 
 namespace {
 
-constexpr int kRowsPerWave = 2;
-constexpr int kRowsPerGroup = 4 * kRowsPerWave;
+constexpr int kRowsPerWave = 2;   // QKV and output projections
+constexpr int kHeadRowsPerWave = 4;  // the LM head: fewer waves re-normalising x
+constexpr int kWavesPerGroup = 4;
+
+enum Mode { kQkv, kLinear, kHead };
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -58,6 +70,7 @@ struct QkvArgs {
   void* q_out;  // [dim]
   int32_t head_dim;
   mie::FastDiv bs;
+  mie::ArgmaxPair* picks;  // head form: one per workgroup, or NULL for logits only
 };
 
 template <typename DT> struct Elt;
@@ -115,7 +128,7 @@ __device__ __forceinline__ float reduce_rows(const float (&v)[R], int lane) {
   return mie::group_sum<64 / R>(cur[0]);
 }
 
-// grid = ceil(rows / (4 * kRowsPerWave)), 256 threads.  NCH = 16-byte loads
+// grid = ceil(rows / (4 * R)), 256 threads.  NCH = 16-byte loads
 // per lane per row (ceil(dim / (64 * elements per load))).  QKV: rows = 3*dim
 // stored as q and the K/V pool rows; else rows outputs stored to out
 // (+ residual).
@@ -125,16 +138,21 @@ __device__ __forceinline__ float reduce_rows(const float (&v)[R], int lane) {
 // c), and normalises with wave reductions: no LDS and no barrier, so all of a
 // wave's global reads - weights, x, norm, bias, residual - are issued together
 // and the launch waits on one memory round trip.
-template <typename DT, int NCH, bool QKV>
+template <typename DT, int NCH, int MODE, int R>
 __device__ __forceinline__ void projection_body(const QkvArgs& a) {
+  constexpr bool QKV = MODE == kQkv;
   using E = Elt<DT>;
   constexpr int EPV = E::kPerVec;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int dim = a.dim;
   const int rows = a.rows;
-  constexpr int R = kRowsPerWave;
-  const int r0 = blockIdx.x * kRowsPerGroup + wave * R;
+  const int r0 = (blockIdx.x * kWavesPerGroup + wave) * R;
+
+  // 0. QKV: the token's position, read first; the block-table read that
+  //    depends on it is issued after the weight loads, so both overlap them.
+  int pos = -1;
+  if constexpr (QKV) pos = a.position_dev ? *a.position_dev : a.position;
 
   // 1. All global reads.  Rows past the end repeat the last row and are not
   //    stored.
@@ -164,6 +182,17 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   const bool storing = lane % kGroup == 0 && r_store < rows;
   const float bias = a.b_in && storing ? E::load(a.b_in, r_store) : 0.f;
   const float res = !QKV && a.residual && storing ? E::load(a.residual, r_store) : 0.f;
+  // The pool slot for the wave's K / V rows (wave-uniform); phys < 0 skips
+  // the store, as the append kernel skips an unmapped block.
+  int32_t phys = -1;
+  uint32_t slot = 0;
+  if constexpr (QKV) {
+    if (r0 + R > a.dim && pos >= 0) {
+      const uint32_t lb = a.bs.div(static_cast<uint32_t>(pos));
+      slot = static_cast<uint32_t>(pos) - lb * a.bs.d;
+      phys = lb < static_cast<uint32_t>(a.bt_len) ? a.block_table[lb] : -1;
+    }
+  }
 
   // 2. x, normalised when ln_w is given (float32 mean and biased variance, then
   //    rounded to the model dtype as the reference's norm output is), in
@@ -213,6 +242,27 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
     }
   }
   const float t = reduce_rows<R>(acc, lane);
+  if constexpr (MODE == kHead) {
+    const float logit = E::round(t + bias);
+    if (storing) E::store(a.out, r_store, logit);
+    if (a.picks) {  // kernel argument: every wave takes the same branch
+      __shared__ float s_v[kWavesPerGroup];
+      __shared__ int s_i[kWavesPerGroup];
+      float v = storing ? logit : -INFINITY;
+      int i = storing ? r_store : INT_MAX;
+      mie::wave_argmax(v, i);
+      if (lane == 0) {
+        s_v[wave] = v;
+        s_i[wave] = i;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        for (int w = 1; w < kWavesPerGroup; ++w) mie::argmax_take(v, i, s_v[w], s_i[w]);
+        a.picks[blockIdx.x] = mie::ArgmaxPair{v, i};
+      }
+    }
+    return;
+  }
   if (!storing) return;
   const int r = r_store;
 
@@ -231,36 +281,44 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   const int j = r - (is_v ? 2 * dim : dim);
   const int h = j / a.head_dim;
   const int d = j - h * a.head_dim;
-  const int pos = a.position_dev ? *a.position_dev : a.position;
-  if (pos < 0) return;
-  const uint32_t lb = a.bs.div(static_cast<uint32_t>(pos));
-  const uint32_t slot = static_cast<uint32_t>(pos) - lb * a.bs.d;
-  if (lb >= static_cast<uint32_t>(a.bt_len)) return;
-  const int32_t phys = a.block_table[lb];
   if (phys < 0 || phys >= a.num_blocks) return;
   E::store(is_v ? a.v_pool : a.k_pool, phys * a.sblk + h * a.shead + static_cast<int64_t>(slot) * a.head_dim + d, out);
 }
 
 template <typename DT, int NCH>
 __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
-  projection_body<DT, NCH, true>(a);
+  projection_body<DT, NCH, kQkv, kRowsPerWave>(a);
 }
 
 template <typename DT, int NCH>
 __global__ __launch_bounds__(256) void linear_residual_kernel(QkvArgs a) {
-  projection_body<DT, NCH, false>(a);
+  projection_body<DT, NCH, kLinear, kRowsPerWave>(a);
 }
 
-template <typename DT, bool QKV>
+template <typename DT, int NCH>
+__global__ __launch_bounds__(256) void lm_head_kernel(QkvArgs a) {
+  projection_body<DT, NCH, kHead, kHeadRowsPerWave>(a);
+}
+
+constexpr int rows_per_wave(int mode) { return mode == kHead ? kHeadRowsPerWave : kRowsPerWave; }
+
+int32_t groups_for(int mode, int rows) {
+  const int per_group = kWavesPerGroup * rows_per_wave(mode);
+  return (rows + per_group - 1) / per_group;
+}
+
+template <typename DT, int MODE>
 int32_t launch(const QkvArgs& a, hipStream_t st) {
   const int nch = (a.dim + 64 * Elt<DT>::kPerVec - 1) / (64 * Elt<DT>::kPerVec);
-  const int groups = (a.rows + kRowsPerGroup - 1) / kRowsPerGroup;
+  const int groups = groups_for(MODE, a.rows);
 #define MIE_PROJ_CASE(N)                                             \
   case N:                                                            \
-    if (QKV) {                                                       \
+    if (MODE == kQkv) {                                              \
       qkv_append_kernel<DT, N><<<groups, 256, 0, st>>>(a);           \
-    } else {                                                         \
+    } else if (MODE == kLinear) {                                    \
       linear_residual_kernel<DT, N><<<groups, 256, 0, st>>>(a);      \
+    } else {                                                         \
+      lm_head_kernel<DT, N><<<groups, 256, 0, st>>>(a);              \
     }                                                                \
     break;
   switch (nch) {
@@ -269,7 +327,8 @@ int32_t launch(const QkvArgs& a, hipStream_t st) {
     default: return mie::fail(MIE_ERR_UNSUPPORTED, "projection: width %d is too large", a.dim);
   }
 #undef MIE_PROJ_CASE
-  return mie::check_launch(QKV ? "qkv_append_kernel" : "linear_residual_kernel");
+  return mie::check_launch(MODE == kQkv ? "qkv_append_kernel"
+                                        : (MODE == kLinear ? "linear_residual_kernel" : "lm_head_kernel"));
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -329,8 +388,8 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
   a.head_dim = head_dim;
   a.bs = mie::FastDiv::make(static_cast<uint32_t>(block_size));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == MIE_DTYPE_F32) return launch<float, true>(a, st);
-  return launch<uint16_t, true>(a, st);
+  if (dtype == MIE_DTYPE_F32) return launch<float, kQkv>(a, st);
+  return launch<uint16_t, kQkv>(a, st);
 }
 
 extern "C" int32_t mie_linear_residual(const void* x, const void* weight, const void* bias, const void* residual,
@@ -350,6 +409,45 @@ extern "C" int32_t mie_linear_residual(const void* x, const void* weight, const 
   a.b_in = bias;
   a.dim = cols;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == MIE_DTYPE_F32) return launch<float, false>(a, st);
-  return launch<uint16_t, false>(a, st);
+  if (dtype == MIE_DTYPE_F32) return launch<float, kLinear>(a, st);
+  return launch<uint16_t, kLinear>(a, st);
+}
+
+extern "C" int64_t mie_lm_head_workspace(int32_t vocab) {
+  return vocab > 0 ? static_cast<int64_t>(groups_for(kHead, vocab)) * sizeof(mie::ArgmaxPair) : 0;
+}
+
+extern "C" int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+                               const void* weight, const void* bias, int32_t vocab, int32_t dim, void* logits,
+                               void* token_out, void* workspace, int64_t workspace_bytes, int32_t dtype,
+                               void* stream) {
+  if (!mie_qkv_append_supported(dim, dtype))
+    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_lm_head: width %d with dtype %d is not built", dim, dtype);
+  if (vocab <= 0 || vocab > INT32_MAX - 64) return mie::fail(MIE_ERR_INVALID, "mie_lm_head: vocab %d", vocab);
+  if (!x || !weight || !logits) return mie::fail(MIE_ERR_INVALID, "mie_lm_head: null pointer");
+  if (ln_bias && !ln_weight) return mie::fail(MIE_ERR_INVALID, "mie_lm_head: a norm bias needs a norm weight");
+  if (!aligned16(weight) || !aligned16(x) || !aligned16(ln_weight) || !aligned16(ln_bias))
+    return mie::fail(MIE_ERR_INVALID, "mie_lm_head: x, the norm parameters and the weight must be 16-byte aligned");
+  const int64_t need = mie_lm_head_workspace(vocab);
+  if (token_out && (!workspace || workspace_bytes < need))
+    return mie::fail(MIE_ERR_INVALID, "mie_lm_head: the pick needs a %lld-byte workspace (got %lld)",
+                     static_cast<long long>(need), static_cast<long long>(workspace ? workspace_bytes : 0));
+  if (token_out && (reinterpret_cast<uintptr_t>(workspace) % alignof(mie::ArgmaxPair) ||
+                    reinterpret_cast<uintptr_t>(token_out) % alignof(int64_t)))
+    return mie::fail(MIE_ERR_INVALID, "mie_lm_head: misaligned workspace or token");
+  QkvArgs a{};
+  a.rows = vocab;
+  a.out = logits;
+  a.x = x;
+  a.ln_w = ln_weight;
+  a.ln_b = ln_bias;
+  a.ln_eps = ln_eps;
+  a.w_in = weight;
+  a.b_in = bias;
+  a.dim = dim;
+  a.picks = token_out ? static_cast<mie::ArgmaxPair*>(workspace) : nullptr;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int32_t rc = dtype == MIE_DTYPE_F32 ? launch<float, kHead>(a, st) : launch<uint16_t, kHead>(a, st);
+  if (rc != MIE_OK || !token_out) return rc;
+  return mie::launch_argmax_pairs(a.picks, groups_for(kHead, vocab), vocab, static_cast<int64_t*>(token_out), st);
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -110,6 +110,19 @@ _SIGNATURES = {
          _i32, _c_void_p],  # dtype, stream
     ),
     "mie_argmax": (_i32, [_c_void_p, _i64, _c_void_p, _i32, _c_void_p]),  # x, n, out (int64), dtype, stream
+    "mie_embed": (
+        _i32,
+        [_c_void_p, _c_void_p, _i32, _i32,  # token ids (int64), positions (int32, device), position, n
+         _c_void_p, _i32, _c_void_p, _i32, _i32,  # token table, vocab, position table, max positions, dim
+         _c_void_p, _i32, _c_void_p],  # out, dtype, stream
+    ),
+    "mie_lm_head_workspace": (_i64, [_i32]),
+    "mie_lm_head": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p,  # x, norm weight, norm bias, eps, W, bias
+         _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,  # vocab, dim, logits, token, workspace, its bytes
+         _i32, _c_void_p],  # dtype, stream
+    ),
     "mie_moe_decode_block": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _f32,  # x, norm weight, norm bias, eps

@@ -22,7 +22,7 @@ run the direct kernel is captured; everything else uses Model.generate.
 
 import torch
 
-from moe_engine import _native, paged_attention
+from moe_engine import paged_attention, projection
 from moe_engine.model import EOS_TOKEN_ID, PagedKVCache
 
 
@@ -48,14 +48,22 @@ class GraphedDecoder:
             moe = block.moe
             if moe.mode == "reference" or not moe.direct_configuration_supported(1):
                 raise RuntimeError("graph decode needs the fused MoE decode kernel (mode 'auto' or 'direct', float32)")
+        if not projection.supported(model.config.hidden_dim, weight.dtype):
+            raise RuntimeError("graph decode needs the HIP LM head for this width and dtype")
         if cache.position <= 0:
             raise ValueError("prefill the cache before building a graphed decoder")
         self.model = model
         self.cache = cache
         device = weight.device
         self.token = torch.zeros(1, 1, dtype=torch.long, device=device)
-        self.pos = torch.zeros(1, dtype=torch.int32, device=device)
-        self.ctx = torch.zeros(1, dtype=torch.int32, device=device)
+        # The new token's position and the context length, advanced together
+        # by one add at the end of each step.
+        self.counters = torch.zeros(2, dtype=torch.int32, device=device)
+        self.pos = self.counters[0:1]
+        self.ctx = self.counters[1:2]
+        vocab = model.output_projection.weight.shape[0]
+        self._logits = torch.empty(1, vocab, dtype=weight.dtype, device=device)
+        self._head_ws = torch.empty(projection.head_workspace_bytes(vocab), dtype=torch.uint8, device=device)
         self.partition_tokens = partition_tokens
         self.graph = None
         self._graph_out = None
@@ -70,19 +78,18 @@ class GraphedDecoder:
         c.graph_partition_tokens = self.partition_tokens if on else 0
 
     def _forward_body(self):
-        """The captured step: the forward pass, the greedy pick written into
-        the token buffer the next step reads, and the position update."""
-        logits = self.model(self.token, self.cache)[:, -1, :]
-        # mie_argmax is one workgroup with nothing to clear (torch.argmax over
-        # a row this wide reduces across workgroups behind a memset, which a
-        # graph must not hold).
-        rc = _native.lib().mie_argmax(logits.data_ptr(), logits.shape[-1], self.token.data_ptr(), 0,
-                                      _native.stream_of(logits))
-        if rc:
-            _native.check(rc, "mie_argmax")
-        self.pos.add_(1)
-        self.ctx.add_(1)
-        return logits
+        """The captured step: embeddings and blocks (Model.hidden_states), the
+        final norm, LM head and greedy pick in mie_lm_head - which writes the
+        token the next step reads - and the position update.  The pick's
+        merge is one workgroup with nothing to clear (torch.argmax over a
+        row this wide reduces across workgroups behind a memset, which a
+        graph must not hold)."""
+        model = self.model
+        x = model.hidden_states(self.token, self.cache)
+        projection.lm_head(x[0, -1], model.final_norm, model.output_projection, out=self._logits,
+                           token_out=self.token, workspace=self._head_ws)
+        self.counters.add_(1)
+        return self._logits
 
     @torch.no_grad()
     def prime(self, token):

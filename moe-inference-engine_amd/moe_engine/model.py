@@ -28,7 +28,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from moe_engine import _native, fused_moe, kv_ops, paged_attention, projection
+from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention, projection
 
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
@@ -670,6 +670,12 @@ class Model(nn.Module):
         return BlockAllocator(self.config, num_blocks, block_size, weight.device, weight.dtype, attention_mode)
 
     def forward(self, token_ids, cache):
+        x = self.hidden_states(token_ids, cache)
+        return self.output_projection(self.final_norm(x))
+
+    def hidden_states(self, token_ids, cache):
+        """The forward pass up to the final norm (model.py:543-562): the
+        embeddings and every block, advancing cache.position."""
         batch, seq_len = token_ids.shape
         position = cache.position
         assert position + seq_len <= self.max_seq_length, "KV cache is full"
@@ -680,14 +686,14 @@ class Model(nn.Module):
 
         graph_pos = getattr(cache, "graph_pos", None)
         if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
-            pos = graph_pos.long()
+            x = embedding.embed(token_ids, graph_pos, self.token_embedding, self.positional_embedding)
         else:
             pos = torch.arange(position, position + seq_len, device=token_ids.device)
-        x = self.token_embedding(token_ids) + self.positional_embedding(pos)
+            x = self.token_embedding(token_ids) + self.positional_embedding(pos)
         for i, block in enumerate(self.MoEBlocks):
             x = block(x, cache, i, position)
         cache.position += seq_len
-        return self.output_projection(self.final_norm(x))
+        return x
 
     @torch.no_grad()
     def generate(self, token_ids, max_new_tokens, temperature=1.0, top_k=None, cache=None):

@@ -1,8 +1,13 @@
-"""One-token linear layers through the HIP library (mie_linear_residual).
+"""One-token linear layers through the HIP library.
 
-The attention's output projection and the block's residual add
-(reference src/moe_engine/model.py:268 and :447, `x + out_proj(attn)`) as one
-launch: out = residual + round(weight @ x + bias), float32 or bfloat16.
+- linear_residual (mie_linear_residual): the attention's output projection and
+  the block's residual add (reference src/moe_engine/model.py:268 and :447,
+  `x + out_proj(attn)`) as one launch: out = residual + round(weight @ x + bias).
+- lm_head (mie_lm_head): the decode step's head, final_norm + output_projection
+  (model.py:564-565), optionally with generate's greedy torch.argmax (:603)
+  written to a device token, in two launches.
+
+float32 or bfloat16.
 """
 
 import torch
@@ -50,3 +55,60 @@ def linear_residual(x, weight, bias=None, residual=None, out=None):
         "mie_linear_residual",
     )
     return out
+
+
+def lm_head(x, norm, linear, out=None, token_out=None, workspace=None):
+    """linear(norm(x)) for one token (norm a LayerNorm or None), written to
+    `out` ([vocab], allocated when None); with `token_out` (an int64 device
+    tensor of one element) also the index of the largest logit, as
+    torch.argmax picks it.  `workspace` (uint8, at least
+    head_workspace_bytes(vocab)) holds the per-workgroup picks; it is
+    allocated when None.  Returns out."""
+    weight, bias = linear.weight, linear.bias
+    if weight.dim() != 2 or not weight.is_contiguous():
+        raise ValueError("weight must be a contiguous [vocab, dim] matrix")
+    vocab, dim = weight.shape
+    dtype, device = weight.dtype, weight.device
+    if not _native.is_rocm_device(weight):
+        raise RuntimeError("mie_lm_head needs tensors on a ROCm device")
+    if x.numel() != dim or not x.is_contiguous():
+        raise ValueError(f"x must hold {dim} contiguous values")
+    ln_w = ln_b = None
+    eps = 0.0
+    if norm is not None:
+        ln_w, ln_b, eps = norm.weight, norm.bias, float(norm.eps)
+    params = (x, bias, ln_w, ln_b, out)
+    if any(t is not None and (t.dtype != dtype or t.device != device) for t in params):
+        raise ValueError("x, the norm, the bias and out must match the weight's dtype and device")
+    if any(t is not None and not t.is_contiguous() for t in (bias, ln_w, ln_b)):
+        raise ValueError("the bias and norm parameters must be contiguous")
+    if not supported(dim, dtype):
+        raise RuntimeError(f"mie_lm_head is not built for width {dim} in {dtype}")
+    if out is None:
+        out = torch.empty(vocab, dtype=dtype, device=device)
+    elif out.numel() != vocab or not out.is_contiguous():
+        raise ValueError(f"out must hold {vocab} contiguous values")
+    ws_ptr, ws_bytes = 0, 0
+    if token_out is not None:
+        if token_out.dtype != torch.int64 or token_out.numel() != 1 or token_out.device != device:
+            raise ValueError("token_out must be one int64 value on the weight's device")
+        need = head_workspace_bytes(vocab)
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=device)
+        elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
+            raise ValueError(f"workspace must hold {need} bytes on the weight's device")
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    _native.check(
+        _native.lib().mie_lm_head(
+            x.data_ptr(), _native.ptr(ln_w), _native.ptr(ln_b), eps, weight.data_ptr(), _native.ptr(bias),
+            vocab, dim, out.data_ptr(), _native.ptr(token_out), ws_ptr, ws_bytes,
+            _native.dtype_code(dtype), _native.stream_of(weight),
+        ),
+        "mie_lm_head",
+    )
+    return out
+
+
+def head_workspace_bytes(vocab: int) -> int:
+    """Bytes of the per-workgroup picks mie_lm_head needs for a greedy token."""
+    return int(_native.lib().mie_lm_head_workspace(int(vocab)))
