@@ -338,6 +338,11 @@ int32_t mie_argmax(const void* x, int64_t n, void* out, int32_t dtype, void* str
  * picks kept in `workspace` (mie_lm_head_workspace(vocab) bytes, 8-byte
  * aligned).  Nothing needs clearing beforehand, so both launches can be
  * captured in a graph.
+ *
+ * advance (device int32[n_advance], n_advance <= 64; needs token_out): each
+ * counter is incremented by one after the pick, in the same launch - a
+ * captured decode step advances its device position and context length there.
+ * NULL / 0 for none.
  */
 /*
  * Token plus positional embedding (model.py:558) of n tokens:
@@ -355,7 +360,7 @@ int32_t mie_embed(const void* token_ids, const int32_t* positions, int32_t posit
 int64_t mie_lm_head_workspace(int32_t vocab);
 int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* weight,
                     const void* bias, int32_t vocab, int32_t dim, void* logits, void* token_out, void* workspace,
-                    int64_t workspace_bytes, int32_t dtype, void* stream);
+                    int64_t workspace_bytes, int32_t* advance, int32_t n_advance, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

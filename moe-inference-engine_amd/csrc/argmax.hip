@@ -69,7 +69,8 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
 }
 
 __global__ __launch_bounds__(kThreads) void argmax_pairs_kernel(const mie::ArgmaxPair* __restrict__ p, int n,
-                                                                int limit, int64_t* out) {
+                                                                int limit, int64_t* out, int32_t* advance,
+                                                                int n_advance) {
   float v = -INFINITY;
   int idx = INT_MAX;
   for (int j0 = 0; j0 < n; j0 += kPairsPerThread * kThreads) {
@@ -84,13 +85,15 @@ __global__ __launch_bounds__(kThreads) void argmax_pairs_kernel(const mie::Argma
   }
   block_argmax(v, idx);
   if (threadIdx.x == 0) *out = idx < limit ? idx : 0;
+  if (threadIdx.x < n_advance) advance[threadIdx.x] += 1;
 }
 
 }  // namespace
 
 namespace mie {
-int32_t launch_argmax_pairs(const ArgmaxPair* pairs, int32_t n, int32_t limit, int64_t* out, hipStream_t stream) {
-  argmax_pairs_kernel<<<1, kThreads, 0, stream>>>(pairs, n, limit, out);
+int32_t launch_argmax_pairs(const ArgmaxPair* pairs, int32_t n, int32_t limit, int64_t* out, int32_t* advance,
+                            int32_t n_advance, hipStream_t stream) {
+  argmax_pairs_kernel<<<1, kThreads, 0, stream>>>(pairs, n, limit, out, advance, n_advance);
   return check_launch("argmax_pairs_kernel");
 }
 }  // namespace mie

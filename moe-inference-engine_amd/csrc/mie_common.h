@@ -116,13 +116,15 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // torch.argmax's order: the larger value wins, NaN counts as larger than every
 // number, and between equal values (or two NaNs) the lower index wins.  The
 // order is total over (value, index), so pairs may be merged in any order.
+// Written with bitwise operators on the comparisons so it compiles to
+// compares and selects, not branches.
 __device__ __forceinline__ void argmax_take(float& va, int& ia, float vb, int ib) {
   const bool a_nan = va != va, b_nan = vb != vb;
-  const bool b_wins = (a_nan || b_nan) ? b_nan && (!a_nan || ib < ia) : vb > va || (vb == va && ib < ia);
-  if (b_wins) {
-    va = vb;
-    ia = ib;
-  }
+  const bool lower = ib < ia;
+  // vb > va and vb == va are false when either is NaN.
+  const bool b_wins = (b_nan & (!a_nan | lower)) | (vb > va) | ((vb == va) & lower);
+  va = b_wins ? vb : va;
+  ia = b_wins ? ib : ia;
 }
 
 // Merges (v, i) over the 64 lanes; every lane ends with the wave's pick.
@@ -145,7 +147,9 @@ struct ArgmaxPair {
 
 namespace mie {
 // Reduces n per-workgroup picks to the final index, written as int64 to *out
-// (0 if no pair holds an index below `limit`).  One workgroup; nothing to
-// clear beforehand.
-int32_t launch_argmax_pairs(const ArgmaxPair* pairs, int32_t n, int32_t limit, int64_t* out, hipStream_t stream);
+// (0 if no pair holds an index below `limit`), then adds one to each of the
+// n_advance int32 counters at `advance`.  One workgroup; nothing to clear
+// beforehand.
+int32_t launch_argmax_pairs(const ArgmaxPair* pairs, int32_t n, int32_t limit, int64_t* out, int32_t* advance,
+                            int32_t n_advance, hipStream_t stream);
 }  // namespace mie

@@ -41,7 +41,10 @@
 namespace {
 
 constexpr int kRowsPerWave = 2;   // QKV and output projections
-constexpr int kHeadRowsPerWave = 4;  // the LM head: fewer waves re-normalising x
+#ifndef MIE_HEAD_ROWS_PER_WAVE
+#define MIE_HEAD_ROWS_PER_WAVE 4
+#endif
+constexpr int kHeadRowsPerWave = MIE_HEAD_ROWS_PER_WAVE;  // the LM head: fewer waves re-normalising x
 constexpr int kWavesPerGroup = 4;
 
 enum Mode { kQkv, kLinear, kHead };
@@ -419,8 +422,8 @@ extern "C" int64_t mie_lm_head_workspace(int32_t vocab) {
 
 extern "C" int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
                                const void* weight, const void* bias, int32_t vocab, int32_t dim, void* logits,
-                               void* token_out, void* workspace, int64_t workspace_bytes, int32_t dtype,
-                               void* stream) {
+                               void* token_out, void* workspace, int64_t workspace_bytes, int32_t* advance,
+                               int32_t n_advance, int32_t dtype, void* stream) {
   if (!mie_qkv_append_supported(dim, dtype))
     return mie::fail(MIE_ERR_UNSUPPORTED, "mie_lm_head: width %d with dtype %d is not built", dim, dtype);
   if (vocab <= 0 || vocab > INT32_MAX - 64) return mie::fail(MIE_ERR_INVALID, "mie_lm_head: vocab %d", vocab);
@@ -432,6 +435,8 @@ extern "C" int32_t mie_lm_head(const void* x, const void* ln_weight, const void*
   if (token_out && (!workspace || workspace_bytes < need))
     return mie::fail(MIE_ERR_INVALID, "mie_lm_head: the pick needs a %lld-byte workspace (got %lld)",
                      static_cast<long long>(need), static_cast<long long>(workspace ? workspace_bytes : 0));
+  if (n_advance < 0 || n_advance > 64 || (n_advance > 0 && (!advance || !token_out)))
+    return mie::fail(MIE_ERR_INVALID, "mie_lm_head: %d counters to advance (at most 64, with a token)", n_advance);
   if (token_out && (reinterpret_cast<uintptr_t>(workspace) % alignof(mie::ArgmaxPair) ||
                     reinterpret_cast<uintptr_t>(token_out) % alignof(int64_t)))
     return mie::fail(MIE_ERR_INVALID, "mie_lm_head: misaligned workspace or token");
@@ -449,5 +454,6 @@ extern "C" int32_t mie_lm_head(const void* x, const void* ln_weight, const void*
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int32_t rc = dtype == MIE_DTYPE_F32 ? launch<float, kHead>(a, st) : launch<uint16_t, kHead>(a, st);
   if (rc != MIE_OK || !token_out) return rc;
-  return mie::launch_argmax_pairs(a.picks, groups_for(kHead, vocab), vocab, static_cast<int64_t*>(token_out), st);
+  return mie::launch_argmax_pairs(a.picks, groups_for(kHead, vocab), vocab, static_cast<int64_t*>(token_out), advance,
+                                  n_advance, st);
 }

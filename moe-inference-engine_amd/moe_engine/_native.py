@@ -121,7 +121,7 @@ _SIGNATURES = {
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p,  # x, norm weight, norm bias, eps, W, bias
          _i32, _i32, _c_void_p, _c_void_p, _c_void_p, _i64,  # vocab, dim, logits, token, workspace, its bytes
-         _i32, _c_void_p],  # dtype, stream
+         _c_void_p, _i32, _i32, _c_void_p],  # counters to advance (int32), their count, dtype, stream
     ),
     "mie_moe_decode_block": (
         _i32,

@@ -57,7 +57,7 @@ class GraphedDecoder:
         device = weight.device
         self.token = torch.zeros(1, 1, dtype=torch.long, device=device)
         # The new token's position and the context length, advanced together
-        # by one add at the end of each step.
+        # by the pick's launch at the end of each step.
         self.counters = torch.zeros(2, dtype=torch.int32, device=device)
         self.pos = self.counters[0:1]
         self.ctx = self.counters[1:2]
@@ -78,17 +78,16 @@ class GraphedDecoder:
         c.graph_partition_tokens = self.partition_tokens if on else 0
 
     def _forward_body(self):
-        """The captured step: embeddings and blocks (Model.hidden_states), the
-        final norm, LM head and greedy pick in mie_lm_head - which writes the
-        token the next step reads - and the position update.  The pick's
-        merge is one workgroup with nothing to clear (torch.argmax over a
-        row this wide reduces across workgroups behind a memset, which a
-        graph must not hold)."""
+        """The captured step: embeddings and blocks (Model.hidden_states),
+        then mie_lm_head - final norm, LM head and greedy pick, which writes
+        the token the next step reads and advances the device position and
+        context length.  The pick's merge is one workgroup with nothing to
+        clear (torch.argmax over a row this wide reduces across workgroups
+        behind a memset, which a graph must not hold)."""
         model = self.model
         x = model.hidden_states(self.token, self.cache)
         projection.lm_head(x[0, -1], model.final_norm, model.output_projection, out=self._logits,
-                           token_out=self.token, workspace=self._head_ws)
-        self.counters.add_(1)
+                           token_out=self.token, workspace=self._head_ws, advance=self.counters)
         return self._logits
 
     @torch.no_grad()

@@ -57,13 +57,15 @@ def linear_residual(x, weight, bias=None, residual=None, out=None):
     return out
 
 
-def lm_head(x, norm, linear, out=None, token_out=None, workspace=None):
+def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=None):
     """linear(norm(x)) for one token (norm a LayerNorm or None), written to
     `out` ([vocab], allocated when None); with `token_out` (an int64 device
     tensor of one element) also the index of the largest logit, as
     torch.argmax picks it.  `workspace` (uint8, at least
     head_workspace_bytes(vocab)) holds the per-workgroup picks; it is
-    allocated when None.  Returns out."""
+    allocated when None.  `advance` (a contiguous int32 device tensor, with
+    token_out): every element is incremented by one after the pick, in the
+    same launch.  Returns out."""
     weight, bias = linear.weight, linear.bias
     if weight.dim() != 2 or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous [vocab, dim] matrix")
@@ -98,10 +100,17 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None):
         elif workspace.numel() * workspace.element_size() < need or workspace.device != device:
             raise ValueError(f"workspace must hold {need} bytes on the weight's device")
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+    if advance is not None:
+        if token_out is None:
+            raise ValueError("advance needs token_out")
+        if advance.dtype != torch.int32 or not advance.is_contiguous() or advance.device != device \
+                or not 0 < advance.numel() <= 64:
+            raise ValueError("advance must be 1 to 64 contiguous int32 values on the weight's device")
     _native.check(
         _native.lib().mie_lm_head(
             x.data_ptr(), _native.ptr(ln_w), _native.ptr(ln_b), eps, weight.data_ptr(), _native.ptr(bias),
             vocab, dim, out.data_ptr(), _native.ptr(token_out), ws_ptr, ws_bytes,
+            _native.ptr(advance), 0 if advance is None else advance.numel(),
             _native.dtype_code(dtype), _native.stream_of(weight),
         ),
         "mie_lm_head",

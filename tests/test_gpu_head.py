@@ -117,6 +117,18 @@ def test_lm_head_pick_keeps_argmax_ties_and_nan_rules():
     assert int(token) == 0 == pick(logits)
 
 
+def test_lm_head_advances_counters_after_the_pick():
+    x, ln, linear = make_head(700, 64, torch.float32, True, True, seed=2)
+    token = torch.zeros(1, dtype=torch.int64, device="cuda")
+    counters = torch.tensor([5, 6, -1], dtype=torch.int32, device="cuda")
+    for step in range(3):
+        logits = projection.lm_head(x, ln, linear, token_out=token, advance=counters)
+    assert counters.tolist() == [8, 9, 2]
+    assert int(token) == pick(logits)
+    with pytest.raises(ValueError, match="token_out"):
+        projection.lm_head(x, ln, linear, advance=counters)
+
+
 def test_lm_head_validates_before_launch():
     x, ln, linear = make_head(300, 64, torch.float32, True, True, seed=1)
     token = torch.zeros(1, dtype=torch.int64, device="cuda")
