@@ -55,12 +55,13 @@ constexpr int kWaves = 4;            // heads (wavefronts) per workgroup
 constexpr int kWindow = 64;          // FAST path: block ids held one per lane
 // Automatic partition size: the smallest power of two (>= the tile) that keeps
 // B * H * ceil(max_ctx / P) at or below kTargetItems wavefronts AND every
-// sequence at or below kMaxParts partitions.  The first bound keeps enough
-// short work items for the dispatcher to balance; the second bounds the merge
-// work per (sequence, head).  Fitted on MI355X with the flat work list:
-// config 4 (64 x U[512, 8192]) and 64 x 4352 are fastest at 512 tokens,
-// 8 x 131072 at 1024, 1 x 131072 at 512.
-constexpr int kTargetItems = 12288;  // auto plan: wavefronts to stay below
+// sequence at or below kMaxParts partitions, capped at the FAST window.  The
+// first bound is where a partition sweep on MI355X (P = 64 .. 2048 tokens,
+// 12 heads x 64, bf16 and fp32) was fastest in every long-context shape:
+// about 3072 wavefronts, 12 per CU - 1 x 32768 at P = 128, 1 x 131072 at
+// 512, 8 x 32768 at 1024 (123 us against 133 us at 12288 wavefronts).  The
+// second bounds the merge work per (sequence, head).
+constexpr int kTargetItems = 3072;  // auto plan: wavefronts to stay below
 constexpr int kMaxParts = 256;       // auto plan: partitions per sequence to stay below
 // Occupancy floor for the main kernels: every built shape fits 4 waves/SIMD
 // (<= 128 VGPRs) without spills; at 3 waves/SIMD config 4 runs ~8 % slower.
