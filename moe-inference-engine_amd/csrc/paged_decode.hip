@@ -83,6 +83,12 @@ constexpr int kFlatMaxBatch = 512;
 // (1536 rows, one workgroup per CU at a time) 45.7 vs 42.3.  Below kWgMinRows
 // rows a long context would leave CUs idle.
 constexpr int kSplitWaves = 16;
+// Workgroup form: half the partition kernels' tile (16 tokens for bf16 and
+// f32 at head_dim 64): 69 instead of 103 VGPRs (7 instead of 4 waves per
+// SIMD) for the same bytes in flight per CU.  Config 4 on MI355X: 119.8 us
+// against 121.7-124.7 us with the partition tile, 121.8 us at a quarter of it
+// (graph-replayed decode launches).
+constexpr int kWgTileWords = 8;
 constexpr int kWgOrderMax = 1024;  // batches the workgroup form can dispatch longest first
 constexpr int kWgShortCtx = 1024;
 constexpr int kWgMinRows = 128;
@@ -99,7 +105,10 @@ template <int DT> struct Elt;
 template <> struct Elt<MIE_DTYPE_F32> { static constexpr int size = 4; };
 template <> struct Elt<MIE_DTYPE_BF16> { static constexpr int size = 2; };
 
-template <int DT, int D>
+// KW: 32-bit words of K each lane holds per tile (the tile's rows are
+// KW / NW wave loads).  The partition kernels use 16 (64 B of K, 64 B of V per
+// lane per tile, two tiles in flight); the workgroup form uses kWgTileWords.
+template <int DT, int D, int KW = 16>
 struct Geometry {
   static constexpr int ELT = Elt<DT>::size;
   static constexpr int VEC = (16 / ELT) < D ? (16 / ELT) : D;  // elements per lane load
@@ -108,7 +117,7 @@ struct Geometry {
   static constexpr int NV = D / VEC;                            // lanes with data per token
   static constexpr int LPT = next_pow2(NV);                     // lanes per token
   static constexpr int TPL = 64 / LPT;                          // tokens per wave load
-  static constexpr int ROWS_BY_REGS = 16 / NW;                  // <= 64 B of K per lane per tile
+  static constexpr int ROWS_BY_REGS = KW / NW > 0 ? KW / NW : 1;  // <= 4 * KW bytes of K per lane per tile
   static constexpr int ROWS_BY_TILE = (64 / TPL) > 0 ? 64 / TPL : 1;
   static constexpr int ROWS = ROWS_BY_REGS < ROWS_BY_TILE ? ROWS_BY_REGS : ROWS_BY_TILE;
   static constexpr int TILE = ROWS * TPL;  // tokens per tile (a power of two)
@@ -215,10 +224,10 @@ __device__ __forceinline__ void store_out(char* base, int64_t elem_off, const fl
 // wave: m (running max, log2 units) and l are uniform across lanes; acc holds
 // the head_dim slice jl = lane % LPT; bad is wave-uniform and set when a block
 // id outside the pool was met.
-template <int DT, int D, bool FAST>
+template <int DT, int D, bool FAST, int KW = 16>
 __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, int t_begin, int t_end, int lane,
                                              float& m, float& l, float* acc, bool& bad, int32_t win_ids = -1) {
-  using G = Geometry<DT, D>;
+  using G = Geometry<DT, D, KW>;
   constexpr int ELT = G::ELT, VEC = G::VEC, NW = G::NW, LPT = G::LPT, TPL = G::TPL;
   constexpr int ROWS = G::ROWS, TILE = G::TILE;
   constexpr int64_t ROW_BYTES = static_cast<int64_t>(D) * ELT;
@@ -521,7 +530,7 @@ struct WgOrder {
 template <int DT, int D, bool FAST>
 __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
 void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
-  using G = Geometry<DT, D>;
+  using G = Geometry<DT, D, kWgTileWords>;
   constexpr int VEC = G::VEC, NW = G::NW, LPT = G::LPT, ELT = G::ELT;
   constexpr int kStates = kSplitWaves + 1;  // the waves' slices, then a fused append's new token
   __shared__ float s_m[kStates], s_l[kStates];
@@ -551,7 +560,8 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
   bool bad = false;
-  if (t_begin < t_end) attend_range<DT, D, FAST>(a, b, h, t_begin, t_end, lane, m, l, acc, bad, win_ids);
+  if (t_begin < t_end)
+    attend_range<DT, D, FAST, kWgTileWords>(a, b, h, t_begin, t_end, lane, m, l, acc, bad, win_ids);
   __syncthreads();  // s_bad is cleared
   const int g = lane / LPT;
   const int jl = lane % LPT;
