@@ -245,6 +245,11 @@ def timed_us(torch, fn, iters=50, warmup=5):
     return start.elapsed_time(end) / iters * 1e3
 
 
+# Bytes one replay must read to be "cold": more than MI355X's 256 MB last-level
+# (Infinity) cache.
+COLD_BYTES = 320 * 10**6
+
+
 def graph_replay_us(torch, calls, reps=5):
     """Device time per call of `calls` (a list of callables) captured back to
     back in one HIP graph: no host launch overhead between calls."""
@@ -328,14 +333,27 @@ def secondary_config3(torch):
         append_host = timed_us(torch, lambda: [f() for f in appends]) / L
         gb = workloads.gather_bytes(C, H, D, 2)
         ab = workloads.append_bytes(1, H, D, 2)
+        # Cold: S sequences with disjoint blocks, each gathered through all
+        # layers, so one replay reads more than the 256 MB last-level cache.
+        S = max(2, min(NB // nblk, -(-COLD_BYTES // (L * gb // 2))))
+        tables = []
+        for i in range(S):
+            t = torch.zeros(NB, dtype=torch.int32, device="cuda")
+            t[:nblk] = perm[i * nblk:(i + 1) * nblk]
+            tables.append(t)
+        cold = [lambda l=l, t=t: kv_ops.gather(k_pool, v_pool, l, t, C, outk, outv) for t in tables for l in range(L)]
+        gather_cold = graph_replay_us(torch, cold)
         res[f"c{C}"] = {
             "append_device_us_per_layer": round(append_dev, 2),
             "append_host_launched_us_per_layer": round(append_host, 2),
             "append_bytes_per_layer": ab,
             "gather_device_us_per_layer": round(gather_dev, 2),
             "gather_gbs": round(gb / gather_dev / 1e3, 1),
+            "gather_cold_device_us_per_layer": round(gather_cold, 2),
+            "gather_cold_gbs": round(gb / gather_cold / 1e3, 1),
             "gather_bytes_per_layer": gb,
         }
+        del tables
     # Prefill scatter: the whole context written through the table in one launch per layer.
     C = 8192
     table = torch.zeros(NB, dtype=torch.int32, device="cuda")
@@ -347,7 +365,8 @@ def secondary_config3(torch):
     pb = workloads.append_bytes(C, H, D, 2)  # C tokens, K and V read and written
     res["prefill_scatter_c8192"] = {"device_us_per_layer": round(prefill_dev, 2), "gbs": round(pb / prefill_dev / 1e3, 1)}
     res["note"] = ("device: the 12 layers' calls replayed from one HIP graph, time per layer; "
-                   "host_launched: back-to-back calls through the Python wrapper")
+                   "gather_cold: the same for several sequences with disjoint blocks in one graph, more than "
+                   "256 MB read per replay; host_launched: back-to-back calls through the Python wrapper")
     del k_pool, v_pool
     torch.cuda.empty_cache()
     return res
@@ -384,7 +403,9 @@ def secondary_config5(torch):
     """BASELINE config 5, the long-context split decode: batch 1 and 8,
     contexts 32768 and 131072, block 16 and 32, bf16 and fp32, 1 % of keys
     x20.  Device time per call from 10 graph-replayed calls, GB/s of the
-    algorithmic bytes."""
+    algorithmic bytes; cells under COLD_BYTES also from calls cycling over
+    copies of the workload in separate pools (cold_us, cold_gbs), so that one
+    replay reads more than the last-level cache holds."""
     from moe_engine import paged_attention, workloads
 
     res = {}
@@ -394,12 +415,27 @@ def secondary_config5(torch):
                 for bs in (16, 32):
                     w = workloads.make_workload([ctx] * batch, block_size=bs, dtype=dtype, seed=5, heavy_fraction=0.01)
                     nbytes = workloads.attention_bytes(w.lens, 12, 64, bs, w.k_pool.element_size())
-                    call = lambda: paged_attention.decode_batched(
+                    call = lambda w=w: paged_attention.decode_batched(
                         w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len, context_lens_host=w.lens
                     )
                     us = graph_replay_us(torch, [call] * 10)
-                    res[f"{tag}_b{batch}_c{ctx}_bs{bs}"] = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1)}
-                    del w
+                    cell = {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1)}
+                    if nbytes < COLD_BYTES:
+                        # Cold: copies of the workload in separate pools, cycled so one replay reads more
+                        # than the 256 MB last-level cache.
+                        copies = [w] + [
+                            workloads.make_workload([ctx] * batch, block_size=bs, dtype=dtype, seed=5 + i,
+                                                    heavy_fraction=0.01)
+                            for i in range(1, -(-COLD_BYTES // nbytes))
+                        ]
+                        calls = [lambda c=c: paged_attention.decode_batched(
+                            c.q, c.k_pool, c.v_pool, 0, c.block_tables, c.context_lens, c.max_len,
+                            context_lens_host=c.lens) for c in copies] * 3
+                        cold = graph_replay_us(torch, calls)
+                        cell.update(cold_us=round(cold, 2), cold_gbs=round(nbytes / cold / 1e3, 1))
+                        del copies, calls
+                    res[f"{tag}_b{batch}_c{ctx}_bs{bs}"] = cell
+                    del w, call
                     torch.cuda.empty_cache()
     return res
 
