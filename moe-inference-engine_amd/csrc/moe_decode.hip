@@ -260,6 +260,10 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   const int r0 = (blockIdx.x * 4 + wave) * 4;
   if (r0 >= a.hidden) return;
   const float* __restrict__ w = a.w1 + (static_cast<int64_t>(e) * a.hidden + r0) * dim;
+  // The bias of the row this lane stores, read with the weights rather than
+  // after the reduction.
+  const int r_out = r0 + (lane >> 4);
+  const float bias = (lane & 15) == 0 && r_out < a.hidden ? a.b1[static_cast<int64_t>(e) * a.hidden + r_out] : 0.f;
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
@@ -273,9 +277,8 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   }
   const float t = wave_sum4(s0, s1, s2, s3, lane);
   if ((lane & 15) == 0) {
-    const int r = r0 + (lane >> 4);
-    const float pre = t + a.b1[static_cast<int64_t>(e) * a.hidden + r];
-    a.h[static_cast<int64_t>(k) * a.hidden + r] = 0.5f * pre * (1.f + erff(pre * 0.70710678118654752440f));
+    const float pre = t + bias;
+    a.h[static_cast<int64_t>(k) * a.hidden + r_out] = 0.5f * pre * (1.f + erff(pre * 0.70710678118654752440f));
   }
 }
 
