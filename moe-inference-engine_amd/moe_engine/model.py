@@ -28,7 +28,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention, projection
+from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention
 
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")

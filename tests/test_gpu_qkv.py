@@ -17,7 +17,6 @@ import math
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 from conftest import print_case
 from moe_engine import kv_ops
