@@ -21,7 +21,7 @@ from conftest import print_case
 from moe_engine import _native, paged_attention
 from moe_engine.model import BlockAllocator, ModelConfig
 from oracle import paged_ref as ref
-from paged_cases import bf16_close, cfg4_lens, make_workload, oracle_outputs, sequence_kv
+from paged_cases import bf16_close, cfg4_lens, make_workload, oracle_outputs, sequence_kv, take_last_tokens
 
 pytestmark = pytest.mark.gpu
 
@@ -287,24 +287,6 @@ def test_explicit_scale():
     want = ref.attention_fp64(ref.to_f64(w.q[0]), ref.to_f64(k), ref.to_f64(v), scale=0.05)
     np.testing.assert_allclose(got[0].cpu().numpy(), want, rtol=0, atol=1e-5)
     assert math.isfinite(float(got.abs().max()))
-
-
-def take_last_tokens(w):
-    """The new rows of a fused append: each sequence's last token's K/V, read
-    from the pool and then zeroed there, so only the fused store can restore it."""
-    heads, dim = w.k_pool.shape[2], w.k_pool.shape[4]
-    bs = w.k_pool.shape[3]
-    k_new = torch.zeros(len(w.lens), heads, dim, dtype=w.k_pool.dtype, device=w.k_pool.device)
-    v_new = torch.zeros_like(k_new)
-    for b, ctx in enumerate(w.lens):
-        if ctx == 0:
-            continue
-        blk, slot = w.tables[b][(ctx - 1) // bs], (ctx - 1) % bs
-        k_new[b] = w.k_pool[w.layer, blk, :, slot]
-        v_new[b] = w.v_pool[w.layer, blk, :, slot]
-        w.k_pool[w.layer, blk, :, slot] = 0
-        w.v_pool[w.layer, blk, :, slot] = 0
-    return k_new, v_new
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -1,16 +1,21 @@
 """Randomized parity sweep of mie_paged_decode against the float64 oracle.
 
-48 seeded cases draw the batch (1-40), ragged context lengths (zero
-included), block size (power of two or not), head count and head_dim, dtype,
-output dtype, plan (automatic, workgroup form, fixed partitions) and whether
-host lengths size the launch.  Each case checks every sequence against
-oracle.paged_ref.attention_fp64 on the same pool contents: float32 inputs
-within 1e-5, bfloat16 inputs within 2e-3 with float32 output or
-2e-3 + 2^-8 |ref| with bf16 output (the tolerances of the north star and of
-tests/test_gpu_decode.py).  The cases print before they run, so a failure
-names its draw.
+Seeded cases (48 by default; MIE_RANDOM_CASES=N for a longer sweep) draw the
+batch (1-40), ragged context lengths (zero included), block size (power of
+two or not), head count and head_dim, dtype, output dtype, plan (automatic,
+workgroup form, fixed partitions), whether host lengths size the launch, and
+whether the step's new token comes through the fused append
+(mie_paged_decode_append: each sequence's last K/V row is taken out of the
+pool and passed as the new rows, so only the kernel's store can put it back).
+Each case checks every sequence against oracle.paged_ref.attention_fp64 on the
+same pool contents: float32 inputs within 1e-5, bfloat16 inputs within 2e-3
+with float32 output or 2e-3 + 2^-8 |ref| with bf16 output (the tolerances of
+the north star and of tests/test_gpu_decode.py); with the fused append the
+pool must also be bit-identical to its state before the rows were taken out.
+The cases print before they run, so a failure names its draw.
 """
 
+import os
 import random
 
 import numpy as np
@@ -19,7 +24,8 @@ import torch
 
 from conftest import print_case
 from moe_engine import _native, paged_attention
-from paged_cases import bf16_close, make_workload, oracle_outputs
+from oracle import paged_ref as ref
+from paged_cases import bf16_close, make_workload, oracle_outputs, take_last_tokens
 
 pytestmark = pytest.mark.gpu
 
@@ -39,22 +45,34 @@ def draw(seed):
         lens[0] = 1
     tile, _ = _native.decode_plan(batch, heads, head_dim, block_size, 1, dtype, 0)
     partition = rng.choice((0, -1, tile, 2 * tile, 8 * tile))
+    # A separate stream, so adding this draw left the other draws of each seed unchanged.
+    fused = random.Random(seed + 100_000).random() < 0.4
     return dict(dtype=dtype, head_dim=head_dim, heads=heads, block_size=block_size, lens=lens,
-                partition=partition, host_lens=rng.random() < 0.5, out_f32=rng.random() < 0.5)
+                partition=partition, host_lens=rng.random() < 0.5, out_f32=rng.random() < 0.5, fused=fused)
 
 
-@pytest.mark.parametrize("seed", range(48))
+CASES = int(os.environ.get("MIE_RANDOM_CASES", "48"))
+
+
+@pytest.mark.parametrize("seed", range(CASES))
 def test_random_decode_matches_oracle(seed):
     c = draw(seed)
     print_case("random decode", seed, {k: (v if k != "lens" else f"{len(v)} seqs, max {max(v)}") for k, v in c.items()})
     w = make_workload(c["lens"], num_heads=c["heads"], head_dim=c["head_dim"], block_size=c["block_size"],
                       dtype=c["dtype"], seed=seed, heavy_fraction=0.01)
+    want = oracle_outputs(w)
+    new = {}
+    if c["fused"]:
+        k_before, v_before = w.k_pool.clone(), w.v_pool.clone()
+        new["k_new"], new["v_new"] = take_last_tokens(w)
     got = paged_attention.decode_batched(
         w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
         partition_tokens=c["partition"], context_lens_host=w.lens if c["host_lens"] else None,
-        out_dtype=torch.float32 if c["out_f32"] else None,
+        out_dtype=torch.float32 if c["out_f32"] else None, **new,
     )
-    want = oracle_outputs(w)
+    if c["fused"]:
+        assert np.array_equal(ref.raw_bits(w.k_pool.cpu()), ref.raw_bits(k_before.cpu()))
+        assert np.array_equal(ref.raw_bits(w.v_pool.cpu()), ref.raw_bits(v_before.cpu()))
     zero = [b for b, n in enumerate(c["lens"]) if n == 0]
     for b in zero:  # no keys: zeros, as scaled_dot_product_attention returns
         assert torch.equal(got[b], torch.zeros_like(got[b]))
