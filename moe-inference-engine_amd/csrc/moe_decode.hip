@@ -41,6 +41,10 @@ namespace {
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
 constexpr int kMaxDim = 2048;  // the W1 kernel holds x in 8 16-byte loads per lane
+// W2 kernel: 16-byte loads per lane per slot per round, 8 for top-1 and
+// top-2 and 16 / K beyond, so a round holds 16 weight and 16 hidden loads.
+template <int K>
+constexpr int kW2Chunks = K <= 2 ? 8 : (16 / K > 0 ? 16 / K : 1);
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -308,13 +312,28 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
   float acc[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) acc[s] = 0.f;
-#pragma unroll 2
-  for (int i = lane * 4; i < a.hidden; i += 256) {
-    f32x4_t q[K];
+  // Rounds of kW2Chunks<K> 16-byte chunks per lane, every load of a round issued
+  // before its first multiply: one memory latency per 256 * kW2Chunks<K> hidden
+  // values (one round at FFN width 2048).  Each lane still accumulates its
+  // chunks in increasing order.
+  for (int i0 = lane * 4; i0 < a.hidden; i0 += 256 * kW2Chunks<K>) {
+    f32x4_t q[K][kW2Chunks<K>], hv[K][kW2Chunks<K>];
 #pragma unroll
-    for (int s = 0; s < K; ++s) q[s] = stream4(row[s] + i);
+    for (int u = 0; u < kW2Chunks<K>; ++u) {
+      const int i = i0 + u * 256;
+      const bool valid = i < a.hidden;
 #pragma unroll
-    for (int s = 0; s < K; ++s) acc[s] = dot4(q[s], load4(a.h + static_cast<int64_t>(s) * a.hidden + i), acc[s]);
+      for (int s = 0; s < K; ++s) {
+        q[s][u] = valid ? stream4(row[s] + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        hv[s][u] = valid ? load4(a.h + static_cast<int64_t>(s) * a.hidden + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kW2Chunks<K>; ++u) {
+      if (i0 + u * 256 >= a.hidden) break;
+#pragma unroll
+      for (int s = 0; s < K; ++s) acc[s] = dot4(q[s][u], hv[s][u], acc[s]);
+    }
   }
 #pragma unroll
   for (int s = 0; s < K; ++s) acc[s] = mie::wave_sum(acc[s]);
