@@ -16,6 +16,7 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kPerThread = 4;
 
 template <typename DT> struct Row;
 template <> struct Row<float> {
@@ -42,9 +43,21 @@ __global__ __launch_bounds__(kThreads) void embed_kernel(const int64_t* __restri
   const int64_t p = positions ? positions[i] : static_cast<int64_t>(position0) + i;
   const bool ok = id >= 0 && id < vocab && p >= 0 && p < max_positions;
   const int64_t o = static_cast<int64_t>(i) * dim;
-  for (int d = threadIdx.x; d < dim; d += kThreads) {
-    const float v = ok ? E::load(tok, id * dim + d) + E::load(pos_table, p * dim + d) : NAN;
-    E::store(out, o + d, v);
+  // kPerThread elements per thread per round, all loads before the stores
+  // (one round up to dim 1024).
+  for (int d0 = threadIdx.x; d0 < dim; d0 += kThreads * kPerThread) {
+    float t[kPerThread], q[kPerThread];
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+      const int d = d0 + u * kThreads;
+      t[u] = ok && d < dim ? E::load(tok, id * dim + d) : 0.f;
+      q[u] = ok && d < dim ? E::load(pos_table, p * dim + d) : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kPerThread; ++u) {
+      const int d = d0 + u * kThreads;
+      if (d < dim) E::store(out, o + d, ok ? t[u] + q[u] : NAN);
+    }
   }
 }
 

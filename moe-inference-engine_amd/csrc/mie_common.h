@@ -105,10 +105,9 @@ __device__ __forceinline__ float wave_max(float x) {
   for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, __shfl_xor(x, off));
   return x;
 }
-__device__ __forceinline__ float wave_sum(float x) {
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
-  return x;
-}
+// Sum over the wave, in every lane: four DPP stages inside each 16-lane row,
+// then two cross-row exchanges (group_sum<64>).
+__device__ __forceinline__ float wave_sum(float x) { return group_sum<64>(x); }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
