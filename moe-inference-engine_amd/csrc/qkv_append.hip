@@ -157,34 +157,47 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   int pos = -1;
   if constexpr (QKV) pos = a.position_dev ? *a.position_dev : a.position;
 
-  // 1. All global reads.  Rows past the end repeat the last row and are not
-  //    stored.
+  // 1. All global reads, unconditional so that they go out together: a load
+  //    under a branch whose result merges with a default at the join makes
+  //    the compiler wait for it there, before the loads after the branch.
+  //    Lanes past dim read element 0 and are zeroed afterwards; an absent norm
+  //    parameter, bias or residual reads a stand-in that is then ignored.
+  //    Rows past the end repeat the last row and are not stored.
   u32x4_t wr[R][NCH], xw[NCH], gw[NCH], gb[NCH];
   const DT* w = static_cast<const DT*>(a.w_in);
+  const DT* x = static_cast<const DT*>(a.x);
   const bool norm = a.ln_w != nullptr;
+  const DT* ln_w = norm ? static_cast<const DT*>(a.ln_w) : x;
+  const DT* ln_b = a.ln_b ? static_cast<const DT*>(a.ln_b) : x;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = (c * 64 + lane) * EPV;
-    xw[c] = gw[c] = gb[c] = u32x4_t{0u, 0u, 0u, 0u};
+    const int ic = i < dim ? i : 0;
 #pragma unroll
-    for (int r = 0; r < R; ++r) wr[r][c] = xw[c];
-    if (i < dim) {
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        wr[r][c] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(min(r0 + r, rows - 1)) * dim + i));
-      xw[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.x) + i);
-      if (norm) {
-        gw[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.ln_w) + i);
-        if (a.ln_b) gb[c] = *reinterpret_cast<const u32x4_t*>(static_cast<const DT*>(a.ln_b) + i);
-      }
-    }
+    for (int r = 0; r < R; ++r)
+      wr[r][c] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(min(r0 + r, rows - 1)) * dim + ic));
+    xw[c] = *reinterpret_cast<const u32x4_t*>(x + ic);
+    gw[c] = *reinterpret_cast<const u32x4_t*>(ln_w + ic);
+    gb[c] = *reinterpret_cast<const u32x4_t*>(ln_b + ic);
   }
   constexpr int kGroup = 64 / R;  // lanes that finish one row
   const int r_store = r0 + lane / kGroup;
   const bool storing = lane % kGroup == 0 && r_store < rows;
-  const float bias = a.b_in && storing ? E::load(a.b_in, r_store) : 0.f;
-  const float res = !QKV && a.residual && storing ? E::load(a.residual, r_store) : 0.f;
+  const int r_read = storing ? r_store : 0;  // w_in holds at least rows elements
+  const float bias_raw = E::load(a.b_in ? a.b_in : a.w_in, r_read);
+  const float res_raw = E::load(!QKV && a.residual ? a.residual : a.w_in, r_read);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const u32x4_t zero = {0u, 0u, 0u, 0u};
+    const bool in = (c * 64 + lane) * EPV < dim;
+#pragma unroll
+    for (int r = 0; r < R; ++r) wr[r][c] = in ? wr[r][c] : zero;
+    xw[c] = in ? xw[c] : zero;
+    gb[c] = a.ln_b ? gb[c] : zero;
+  }
+  const float bias = a.b_in && storing ? bias_raw : 0.f;
+  const float res = !QKV && a.residual && storing ? res_raw : 0.f;
   // The pool slot for the wave's K / V rows (wave-uniform); phys < 0 skips
   // the store, as the append kernel skips an unmapped block.
   int32_t phys = -1;
