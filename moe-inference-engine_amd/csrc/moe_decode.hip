@@ -85,12 +85,26 @@ __device__ __forceinline__ float wave_dot(const float* __restrict__ row, const f
   return mie::wave_sum(s);
 }
 
+// (v, i) against (ov, oi): the larger logit wins, the lower expert id on
+// ties - a total order, so any reduction tree gives the same pick.  Compares
+// and selects, no branches.
+__device__ __forceinline__ void topk_take(float& v, int& i, float ov, int oi) {
+  const bool b = (ov > v) | ((ov == v) & (oi < i));
+  v = b ? ov : v;
+  i = b ? oi : i;
+}
+
+template <int CTRL>
+__device__ __forceinline__ void topk_dpp(float& v, int& i) {
+  topk_take(v, i, mie::dpp<CTRL>(v), __builtin_amdgcn_update_dpp(0, i, CTRL, 0xF, 0xF, false));
+}
+
 // Top-k over a wave: lane e holds expert e's logit (-inf for lanes >= E).
-// Round kk takes the largest logit not yet taken, the lower expert id on ties,
-// with a (value, id) butterfly; ids and weights (the softmax of the selected
-// logits) come out uniform across the wave.  Fixed-size loops keep both arrays
-// in registers.
-__device__ __forceinline__ void wave_topk(float logit, int top_k, int lane, int* ids, float* weights) {
+// Round kk takes the largest logit not yet taken, the lower expert id on ties;
+// ids and weights (the softmax of the selected logits) come out uniform across
+// the wave.  Fixed-size loops keep both arrays in registers.
+__device__ __forceinline__ void wave_topk(float logit, int top_k, int num_experts, int lane, int* ids,
+                                          float* weights) {
   bool taken = false;
   float vals[kMaxTopK];
 #pragma unroll
@@ -98,17 +112,21 @@ __device__ __forceinline__ void wave_topk(float logit, int top_k, int lane, int*
     ids[kk] = 0;
     vals[kk] = 0.f;
     if (kk < top_k) {
+      // A taken expert also loses every tie, so a repeated -inf cannot pick it twice.
       float v = taken ? -INFINITY : logit;
-      int idx = lane;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(v, off);
-        const int oi = __shfl_xor(idx, off);
-        if (ov > v || (ov == v && oi < idx)) {
-          v = ov;
-          idx = oi;
-        }
-      }
+      int idx = taken ? lane + 64 : lane;
+      // Only the lanes holding experts take part: DPP stages over 2, 4, 8 and
+      // 16 lanes (quad xor-1 and xor-2, then half-row and row mirrors), then
+      // cross-row exchanges for more than 16 experts.
+      topk_dpp<0xB1>(v, idx);
+      topk_dpp<0x4E>(v, idx);
+      if (num_experts > 4) topk_dpp<0x141>(v, idx);
+      if (num_experts > 8) topk_dpp<0x140>(v, idx);
+      if (num_experts > 16) topk_take(v, idx, __shfl_xor(v, 16), __shfl_xor(idx, 16));
+      if (num_experts > 32) topk_take(v, idx, __shfl_xor(v, 32), __shfl_xor(idx, 32));
+      // Lane 0 holds the pick; every lane takes it from a scalar register.
+      idx = __builtin_amdgcn_readfirstlane(idx);
+      v = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
       ids[kk] = idx;
       vals[kk] = v;
       taken = taken || lane == idx;
@@ -141,7 +159,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(MoeArgs a) {
   if (wave != 0) return;
   int ids[kMaxTopK];
   float p[kMaxTopK];
-  wave_topk(lane < a.E ? logits[lane] : -INFINITY, a.top_k, lane, ids, p);
+  wave_topk(lane < a.E ? logits[lane] : -INFINITY, a.top_k, a.E, lane, ids, p);
 #pragma unroll
   for (int kk = 0; kk < kMaxTopK; ++kk) {
     if (kk < a.top_k && lane == kk) {
@@ -245,7 +263,7 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   int ids[kMaxTopK];
   float p[kMaxTopK];
   const float logit = lane < a.E ? s_logits[lane] : -INFINITY;
-  wave_topk(logit, a.top_k, lane, ids, p);
+  wave_topk(logit, a.top_k, a.E, lane, ids, p);
   if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
     if (lane < a.E) a.logits[lane] = logit;
 #pragma unroll
