@@ -248,7 +248,8 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
   }
 
   const int32_t* bt = a.bt + b * a.bt_stride;
-  const int64_t lane_off = (h * a.kv_sh + jl * VEC) * ELT;
+  // A lane without head_dim data (jl >= NV) reads its row's first vector.
+  const int64_t lane_off = (h * a.kv_sh + (jv ? jl : 0) * VEC) * ELT;
   const char* kbase = a.k + lane_off;
   const char* vbase = a.v + lane_off;
   const int64_t blk_bytes = a.kv_sblk * ELT;
@@ -271,36 +272,34 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
     }
   }
 
+  // Every load is unconditional, so that a tile's loads go out together and
+  // the wait before consuming the previous tile counts exactly the loads in
+  // flight: a load under a branch makes the compiler assume the other path and
+  // wait for everything.  Rows past the range re-read the range's last row,
+  // and a table entry outside the pool reads block 0 (its sequence is already
+  // marked bad); consume() masks both.
+  const int last_row = (t_end - 1) & ~(TPL - 1);
   auto issue = [&](int t0, Words<NW>* kr, Words<NW>* vr) {
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-#pragma unroll
-      for (int w = 0; w < NW; ++w) { kr[r].w[w] = 0u; vr[r].w[w] = 0u; }
+      int64_t off;
       if constexpr (FAST) {
-        const int tr = t0 + r * TPL;  // first token of the row (wave-uniform)
-        if (tr < t_end && !bad) {
-          const int phys = __builtin_amdgcn_readlane(ids, (tr >> a.bs.shift) - fb);
-          const int64_t off = phys * blk_bytes + static_cast<int64_t>((tr & (a.bs.d - 1)) + g) * ROW_BYTES;
-          if (jv && tr + g < t_end) {
-            kr[r] = load_words_nt<NW>(kbase + off);
-            vr[r] = load_words_nt<NW>(vbase + off);
-          }
-        }
+        const int tr = min(t0 + r * TPL, last_row);  // first token of the row (wave-uniform)
+        int phys = __builtin_amdgcn_readlane(ids, (tr >> a.bs.shift) - fb);
+        phys = static_cast<uint32_t>(phys) < static_cast<uint32_t>(a.num_blocks) ? phys : 0;
+        off = phys * blk_bytes + static_cast<int64_t>((tr & (a.bs.d - 1)) + g) * ROW_BYTES;
       } else {
-        const int t = t0 + r * TPL + g;
-        if (t < t_end) {
-          const uint32_t blk = a.bs.div(static_cast<uint32_t>(t));
-          const uint32_t slot = static_cast<uint32_t>(t) - blk * a.bs.d;
-          const int32_t phys = blk < a.bt_cap ? bt[blk] : -1;
-          if (phys < 0 || phys >= a.num_blocks) {
-            bad = true;
-          } else if (jv) {
-            const int64_t off = phys * blk_bytes + static_cast<int64_t>(slot) * ROW_BYTES;
-            kr[r] = load_words_nt<NW>(kbase + off);
-            vr[r] = load_words_nt<NW>(vbase + off);
-          }
-        }
+        const int t_raw = t0 + r * TPL + g;
+        const int t = min(t_raw, t_end - 1);
+        const uint32_t blk = a.bs.div(static_cast<uint32_t>(t));
+        const uint32_t slot = static_cast<uint32_t>(t) - blk * a.bs.d;
+        const int32_t entry = bt[min(blk, a.bt_cap - 1)];
+        const bool ok = blk < a.bt_cap && entry >= 0 && entry < a.num_blocks;
+        bad = bad || (!ok && t_raw < t_end);
+        off = (ok ? entry : 0) * blk_bytes + static_cast<int64_t>(slot) * ROW_BYTES;
       }
+      kr[r] = load_words_nt<NW>(kbase + off);
+      vr[r] = load_words_nt<NW>(vbase + off);
     }
   };
 
@@ -309,7 +308,19 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
 #pragma unroll
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
 
-  auto consume = [&](int t0, const Words<NW>* kr, const Words<NW>* vr) {
+  auto consume = [&](int t0, const Words<NW>* kr_in, const Words<NW>* vr_in) {
+    // Rows past the range and lanes without head_dim data hold stand-in
+    // values: zero them so that no Inf or NaN stored there reaches the sums.
+    Words<NW> kr[ROWS], vr[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+      const bool live = t0 + r * TPL + g < t_end;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        kr[r].w[w] = (G::NV < LPT && !jv) ? 0u : kr_in[r].w[w];
+        vr[r].w[w] = live ? vr_in[r].w[w] : 0u;
+      }
+    }
     float s[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -359,15 +370,25 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
     m = m_new;
   };
 
-  // Two register sets: tile i+1 is in flight while tile i is consumed.
+  // Two register sets: tile i+1 is in flight while tile i is consumed.  The
+  // steady state issues unconditionally; the last one or two tiles are peeled,
+  // so no tile past the range is read.
   Words<NW> kA[ROWS], vA[ROWS], kB[ROWS], vB[ROWS];
+  const int ntiles = (t_end - t_begin + TILE - 1) / TILE;  // >= 1
   issue(t_begin, kA, vA);
-  for (int t0 = t_begin; t0 < t_end; t0 += 2 * TILE) {
-    if (t0 + TILE < t_end) issue(t0 + TILE, kB, vB);
+  int t0 = t_begin;
+  for (int i = 0; i + 2 < ntiles; i += 2, t0 += 2 * TILE) {
+    issue(t0 + TILE, kB, vB);
     consume(t0, kA, vA);
-    if (t0 + TILE >= t_end) break;
-    if (t0 + 2 * TILE < t_end) issue(t0 + 2 * TILE, kA, vA);
+    issue(t0 + 2 * TILE, kA, vA);
     consume(t0 + TILE, kB, vB);
+  }
+  if (t0 + TILE < t_end) {
+    issue(t0 + TILE, kB, vB);
+    consume(t0, kA, vA);
+    consume(t0 + TILE, kB, vB);
+  } else {
+    consume(t0, kA, vA);
   }
 
   // Merge the TPL token groups (lanes jl, jl + LPT, ...) with log-sum-exp.
