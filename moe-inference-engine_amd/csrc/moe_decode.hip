@@ -286,15 +286,26 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   // after the reduction.
   const int r_out = r0 + (lane >> 4);
   const float bias = (lane & 15) == 0 && r_out < a.hidden ? a.b1[static_cast<int64_t>(e) * a.hidden + r_out] : 0.f;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  // All 4 x NCH row loads go out before the first multiply: unconditional,
+  // with lanes past dim reading element 0 (y is zero there, and the product
+  // is dropped below), since a load under a branch makes the compiler wait
+  // for it before the next one.
+  f32x4_t wv[4][NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = c * 256 + lane * 4;
-    if (i < dim) {
-      s0 = dot4(stream4(w + i), y[c], s0);
-      s1 = dot4(stream4(w + dim + i), y[c], s1);
-      s2 = dot4(stream4(w + 2 * dim + i), y[c], s2);
-      s3 = dot4(stream4(w + 3 * dim + i), y[c], s3);
+    const int ic = i < dim ? i : 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wv[r][c] = stream4(w + r * dim + ic);
+  }
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    if (c * 256 + lane * 4 < dim) {
+      s0 = dot4(wv[0][c], y[c], s0);
+      s1 = dot4(wv[1][c], y[c], s1);
+      s2 = dot4(wv[2][c], y[c], s2);
+      s3 = dot4(wv[3][c], y[c], s3);
     }
   }
   const float t = wave_sum4(s0, s1, s2, s3, lane);
