@@ -52,6 +52,11 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   const int h = r / a.vecs_per_row;
   const int vec = r - h * a.vecs_per_row;
 
+  // The new row's vector does not depend on the position or the table, so it
+  // is read first and travels with those reads.
+  const char* src = (is_v ? a.v_new : a.k_new) + b * a.new_sb + h * a.new_sh + s * a.new_ss +
+                    static_cast<int64_t>(vec) * VB;
+  const T v = *reinterpret_cast<const T*>(src);
   const int pos = (a.positions ? a.positions[b] : a.position) + a.pos_bias + s;
   if (pos < 0) return;
   const uint32_t blk = a.bs.div(static_cast<uint32_t>(pos));
@@ -59,12 +64,9 @@ __global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
   if (blk >= a.bt_cap) return;
   const int32_t phys = a.block_tables[b * a.bt_stride + blk];
   if (phys < 0 || phys >= a.num_blocks) return;
-
-  const char* src = (is_v ? a.v_new : a.k_new) + b * a.new_sb + h * a.new_sh + s * a.new_ss +
-                    static_cast<int64_t>(vec) * VB;
   char* dst = (is_v ? a.v_pool : a.k_pool) + phys * a.pool_sblk + h * a.pool_shead +
               static_cast<int64_t>(slot) * a.row_bytes + static_cast<int64_t>(vec) * VB;
-  *reinterpret_cast<T*>(dst) = *reinterpret_cast<const T*>(src);
+  *reinterpret_cast<T*>(dst) = v;
 }
 
 struct GatherArgs {
