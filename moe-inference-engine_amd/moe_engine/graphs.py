@@ -1,23 +1,25 @@
 """Whole decode steps captured as HIP graphs (paged-direct cache, greedy).
 
-A decode step of the engine launches ~15 kernels per layer; on the eager path
-the host spends longer issuing them than the GPU spends running them.  Here
-one step - embeddings, every layer (QKV projection, HIP KV append, HIP paged
-decode, fused HIP MoE), final norm, output projection - is captured once and
-replayed for every later token, the greedy pick included.
+One greedy decode step is captured once and replayed for every later token:
+the embedding (mie_embed), every layer's five launches (QKV into the pool,
+paged decode, out_proj with the residual, the two MoE launches), and the head
+(mie_lm_head: final norm, LM head, greedy pick).  Eagerly the host spends
+longer issuing those launches than the GPU spends running them.
 
 Everything that changes from step to step lives on the device: the token fed
-in (the previous step's argmax, written by the graph into a fixed buffer), the
-position of the new token and the context length (incremented by the graph).  The paged cache
-is put in graph mode (PagedKVCache.graph_pos / graph_ctx), so the append and
-the decode read those device values and the decode launch is sized for the
-pool's capacity (partition_tokens 0 lets the library plan it for that bound:
-one workgroup per head for pools of up to 4096 tokens).  The host keeps only the block bookkeeping: before each
+in (the previous step's pick, which the graph writes into a fixed buffer), the
+position of the new token and the context length (advanced by the graph's
+last launch).  The paged cache is put in graph mode (PagedKVCache.graph_pos /
+graph_ctx), so the append and the decode read those device values, and the
+decode launch is planned for the model's capacity (partition_tokens 0 lets
+the library choose; for 12 heads and up to 1024 positions that is one
+workgroup per head).  The host keeps only the block bookkeeping: before each
 replay it reserves the block the new token needs (one host-to-device copy of
-one block id every block_size tokens) - the replay itself never allocates.
+one block id every block_size tokens); the replay itself never allocates.
 
 Only greedy decoding (temperature 0) over a PagedKVCache whose attention can
-run the direct kernel is captured; everything else uses Model.generate.
+run the direct kernel, with the fused float32 MoE, is captured; everything
+else uses Model.generate.
 """
 
 import torch
