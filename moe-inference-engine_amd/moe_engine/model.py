@@ -320,10 +320,27 @@ class CachedAttention(nn.Module):
         Applies to a paged cache on a ROCm device whose decode runs the direct
         kernel, a float32 / bfloat16 model of a built width, and a plain
         LayerNorm; results equal forward()'s to float32 rounding."""
+        if position <= 0 or not self.fused_decode_supported(x, norm, cache):
+            return None
+        alloc = cache.allocator
+        q = cache.write_projected(layer_idx, position, x, self.in_proj_weight, self.in_proj_bias, norm)
+        attn = paged_attention.decode(q, cache, layer_idx, context_len=position + 1)  # [1, H, 1, D]: heads in order
+        w, b = self.out_proj.weight, self.out_proj.bias
+        out = torch.empty_like(x)
+        rc = _native.lib().mie_linear_residual(
+            attn.data_ptr(), w.data_ptr(), _native.ptr(b), x.data_ptr(), out.data_ptr(),
+            w.shape[0], w.shape[1], alloc._launch[3], _native.stream_of(x),
+        )
+        if rc:
+            _native.check(rc, "mie_linear_residual")
+        return out
+
+    def fused_decode_supported(self, x, norm, cache) -> bool:
+        """Whether fused_decode's three launches apply to this token, cache
+        and norm (everything but the position)."""
         alloc = getattr(cache, "allocator", None)
-        if (
-            position <= 0
-            or alloc is None
+        return not (
+            alloc is None
             or not getattr(alloc, "fuse_qkv", False)
             or cache.attention_mode == "gather"
             or x.shape[:2] != (1, 1)
@@ -339,19 +356,7 @@ class CachedAttention(nn.Module):
             or self.out_proj.weight.dtype != x.dtype
             or not self.out_proj.weight.is_contiguous()
             or not paged_attention.is_supported(x, self.head_dim)
-        ):
-            return None
-        q = cache.write_projected(layer_idx, position, x, self.in_proj_weight, self.in_proj_bias, norm)
-        attn = paged_attention.decode(q, cache, layer_idx, context_len=position + 1)  # [1, H, 1, D]: heads in order
-        w, b = self.out_proj.weight, self.out_proj.bias
-        out = torch.empty_like(x)
-        rc = _native.lib().mie_linear_residual(
-            attn.data_ptr(), w.data_ptr(), _native.ptr(b), x.data_ptr(), out.data_ptr(),
-            w.shape[0], w.shape[1], alloc._launch[3], _native.stream_of(x),
         )
-        if rc:
-            _native.check(rc, "mie_linear_residual")
-        return out
 
     def forward(self, x, cache, layer_idx, position: int):
         batch, seq_len, dim = x.shape
@@ -597,13 +602,9 @@ class MoEFeedForward(nn.Module):
             return self._forward_dense(x)
         return self._forward_reference(x)
 
-    def fused_block_decode(self, x, norm):
-        """x + self(norm(x), decode=True) for one token in two launches
-        (mie_moe_decode_block: the norm and routing in the W1 launch, the
-        residual add in the W2 launch), or None when the fused kernels do not
-        apply - mode 'reference', an unsupported configuration, or a norm that
-        is not a float32 LayerNorm over the hidden size."""
-        if (
+    def fused_block_supported(self, x, norm) -> bool:
+        """Whether fused_block_decode's two launches apply to this token and norm."""
+        return not (
             self.mode == "reference"
             or not isinstance(norm, nn.LayerNorm)
             or norm.weight is None
@@ -611,7 +612,15 @@ class MoEFeedForward(nn.Module):
             or (norm.bias is not None and norm.bias.dtype != torch.float32)
             or tuple(norm.normalized_shape) != (self.dim,)
             or not self._direct_supported(x)
-        ):
+        )
+
+    def fused_block_decode(self, x, norm):
+        """x + self(norm(x), decode=True) for one token in two launches
+        (mie_moe_decode_block: the norm and routing in the W1 launch, the
+        residual add in the W2 launch), or None when the fused kernels do not
+        apply - mode 'reference', an unsupported configuration, or a norm that
+        is not a float32 LayerNorm over the hidden size."""
+        if not self.fused_block_supported(x, norm):
             return None
         s = self._expert_storage
         return fused_moe.decode_block(
@@ -628,11 +637,17 @@ class TransformerMoEBlock(nn.Module):
         self.moe = MoEFeedForward(config.hidden_dim, config.expert_hidden_dim, config.num_experts, config.top_k)
         self.attn_norm = nn.LayerNorm(config.hidden_dim)
         self.moe_norm = nn.LayerNorm(config.hidden_dim)
+        self._one_token = None  # (key, launcher or None): see _decode_one_token
 
     def forward(self, x, cache, layer_idx, position):
-        # One-token decode takes the fused halves where they apply (same
-        # results to float32 rounding); everything else is the reference's
+        # One-token eager decode with both fused halves runs from a cached
+        # launch plan; otherwise each half takes its fused path where it
+        # applies (same results to float32 rounding), else the reference's
         # block (model.py:446-449).
+        if position > 0 and x.shape[1] == 1 and getattr(cache, "graph_pos", None) is None:
+            out = self._decode_one_token(x, cache, layer_idx, position)
+            if out is not None:
+                return out
         h = self.attention.fused_decode(x, self.attn_norm, cache, layer_idx, position)
         if h is None:
             h = x + self.attention(self.attn_norm(x), cache, layer_idx, position)
@@ -641,6 +656,110 @@ class TransformerMoEBlock(nn.Module):
         if out is None:
             out = h + self.moe(self.moe_norm(h), decode=decode)
         return out
+
+    def _one_token_key(self, x, cache, layer_idx):
+        """Every value the cached launch arguments are computed from: the
+        cache, pool and table addresses and shapes, the block's parameter and
+        expert-storage addresses, the norms' eps, the MoE mode, and x's dtype
+        and device.  A change to any of them (a new cache, a model moved or
+        reloaded) builds a new plan."""
+        alloc = cache.allocator
+        m = self._modules
+        att, moe = m["attention"], m["moe"]
+        an, mn = m["attn_norm"], m["moe_norm"]
+        pa, po = att._parameters, att._modules["out_proj"]._parameters
+        pan, pmn = an._parameters, mn._parameters
+        st, bf = moe._expert_storage, moe._buffers
+        ptr = _native.ptr
+        return (
+            layer_idx, cache.attention_mode, getattr(alloc, "fuse_qkv", False), alloc._launch, alloc.num_blocks,
+            alloc.block_size, alloc.num_heads, alloc.head_dim, x.dtype, x.device, x.shape[-1], moe.mode,
+            an.eps, mn.eps, alloc.k_pool.data_ptr(), alloc.v_pool.data_ptr(), cache.block_table_device.data_ptr(),
+            ptr(pa["in_proj_weight"]), ptr(pa["in_proj_bias"]), ptr(po["weight"]), ptr(po["bias"]),
+            ptr(pan["weight"]), ptr(pan["bias"]), ptr(pmn["weight"]), ptr(pmn["bias"]),
+            ptr(moe._modules["router"]._parameters["weight"]), ptr(st["w1"]), ptr(st["b1"]), ptr(st["w2"]),
+            ptr(st["b2"]), ptr(bf["_router_logits"]), ptr(bf["_expert_ids"]), ptr(bf["_route_weights"]),
+            ptr(bf["_expert_hidden"]), ptr(bf["_direct_out"]),
+        )
+
+    def _decode_one_token(self, x, cache, layer_idx, position):
+        """The block for one eager decode token when both fused halves apply:
+        the same five launches as fused_decode + fused_block_decode, with the
+        checks and the static launch arguments computed once per plan key
+        rather than per token.  Returns None when the fused halves do not
+        both apply."""
+        if getattr(cache, "allocator", None) is None or x.dim() != 3 or x.shape[0] != 1 or not x.is_contiguous():
+            return None
+        key = self._one_token_key(x, cache, layer_idx)
+        plan = self._one_token
+        if plan is None or plan[0] != key:
+            launcher = None
+            if self.attention.fused_decode_supported(x, self.attn_norm, cache) and self.moe.fused_block_supported(
+                    x, self.moe_norm):
+                launcher = self._build_one_token(x, cache, layer_idx)
+            plan = self._one_token = (key, launcher)
+        return None if plan[1] is None else plan[1](x, cache, position)
+
+    def _build_one_token(self, x, cache, layer_idx):
+        alloc = cache.allocator
+        att, moe = self.attention, self.moe
+        lib = _native.lib()
+        qkv_fn, dec_fn, lin_fn, moe_fn = (lib.mie_qkv_append, lib.mie_paged_decode, lib.mie_linear_residual,
+                                          lib.mie_moe_decode_block)
+        ptr, check, stream_of, decode_plan = _native.ptr, _native.check, _native.stream_of, _native.decode_plan
+        workspace = paged_attention._workspace
+        layer_bytes, sblk, shead, code = alloc._launch
+        heads, head_dim, block_size, num_blocks = alloc.num_heads, alloc.head_dim, alloc.block_size, alloc.num_blocks
+        dim = x.shape[-1]
+        dtype, device = x.dtype, x.device
+        off = layer_idx * layer_bytes
+        k_ptr, v_ptr = alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off
+        table = cache.block_table_device.data_ptr()
+        an, mn = self.attn_norm, self.moe_norm
+        ln_w, ln_b, ln_eps = ptr(an.weight), ptr(an.bias), float(an.eps)
+        w_in, b_in = att.in_proj_weight.data_ptr(), ptr(att.in_proj_bias)
+        w_o, b_o = att.out_proj.weight.data_ptr(), ptr(att.out_proj.bias)
+        s = moe._expert_storage
+        moe_args = (ptr(mn.weight), ptr(mn.bias), float(mn.eps), moe.router.weight.data_ptr(), s["w1"].data_ptr(),
+                    s["b1"].data_ptr(), s["w2"].data_ptr(), s["b2"].data_ptr(), moe.router.weight.shape[0],
+                    moe._expert_ids.numel(), dim, s["w1"].shape[1], moe._router_logits.data_ptr(),
+                    moe._expert_ids.data_ptr(), moe._route_weights.data_ptr(), moe._expert_hidden.data_ptr(),
+                    moe._direct_out.data_ptr(), code)
+        out = moe._direct_out.view(1, 1, dim)
+        # The block's intermediates, reused by every token: q, the attention
+        # output and the attention half's output are consumed within the call.
+        q = torch.empty((1, heads, 1, head_dim), dtype=dtype, device=device)
+        attn = torch.empty_like(q)
+        h = torch.empty((1, 1, dim), dtype=dtype, device=device)
+        q_ptr, attn_ptr, h_ptr = q.data_ptr(), attn.data_ptr(), h.data_ptr()
+        scale = 1.0 / math.sqrt(head_dim)
+
+        def launch(x, cache, position):
+            cache._reserve(position + 1)
+            stream = stream_of(x)
+            x_ptr = x.data_ptr()
+            rc = qkv_fn(x_ptr, ln_w, ln_b, ln_eps, w_in, b_in, dim, k_ptr, v_ptr, sblk, shead, num_blocks, table,
+                        num_blocks, None, position, q_ptr, heads, head_dim, block_size, code, stream)
+            if rc:
+                check(rc, "mie_qkv_append")
+            ctx = position + 1
+            _, ws_bytes = decode_plan(1, heads, head_dim, block_size, ctx, dtype, 0)
+            ws = workspace(ws_bytes, device)
+            rc = dec_fn(q_ptr, heads * head_dim, head_dim, k_ptr, v_ptr, sblk, shead, num_blocks, table, 0,
+                        None, None, ctx, ctx, 1, heads, head_dim, block_size, scale, attn_ptr, heads * head_dim,
+                        head_dim, code, ptr(ws), ws_bytes, 0, code, stream)
+            if rc:
+                check(rc, "mie_paged_decode")
+            rc = lin_fn(attn_ptr, w_o, b_o, x_ptr, h_ptr, dim, dim, code, stream)
+            if rc:
+                check(rc, "mie_linear_residual")
+            rc = moe_fn(h_ptr, *moe_args, stream)
+            if rc:
+                check(rc, "mie_moe_decode_block")
+            return out
+
+        launch.buffers = (q, attn, h)  # kept alive with the plan
+        return launch
 
 
 class Model(nn.Module):
