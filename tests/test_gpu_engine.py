@@ -145,3 +145,56 @@ def test_config1_greedy_tokens_identical_across_paths():
     diff = (gpu_logits - cpu_logits[:, 31:]).abs().max().item()
     print(f"config1 max |logit diff| GPU paged-direct vs CPU contiguous: {diff:.3e}", flush=True)
     assert diff < 1e-2
+
+
+def test_cached_one_token_plan_follows_cache_and_weight_changes():
+    """The eager one-token decode runs each block from a cached launch plan
+    (TransformerMoEBlock._decode_one_token).  Every decode below is checked
+    against the same step with the plan disabled (the per-call fused path)
+    after changing what the plan depends on: a second cache on another
+    allocator, reloaded weights (new tensors, assign=True), the MoE mode, and
+    the allocator's fuse_qkv switch."""
+    print_case("cached one-token plan")
+    torch.manual_seed(0)
+    model = Model(ModelConfig(**TINY)).to("cuda").eval()
+    ids = torch.randint(0, TINY["vocab_size"], (1, 12), device="cuda")
+
+    def run(cache_factory, use_plan):
+        blocks = list(model.MoEBlocks)
+        saved = [b._decode_one_token for b in blocks]
+        if not use_plan:
+            for b in blocks:
+                b._decode_one_token = lambda *args, **kwargs: None
+        try:
+            cache = cache_factory()
+            out = stepwise_logits(model, ids, cache, 5)
+            cache.free()
+            return out
+        finally:
+            for b, f in zip(blocks, saved):
+                b._decode_one_token = f
+
+    alloc_a = model.new_block_allocator(num_blocks=16, block_size=4, attention_mode="direct")
+    alloc_b = model.new_block_allocator(num_blocks=24, block_size=8, attention_mode="direct")
+
+    def check(factory):
+        torch.testing.assert_close(run(factory, True), run(factory, False), atol=1e-5, rtol=1e-5)
+
+    check(alloc_a.new_cache)
+    assert all(b._one_token is not None and b._one_token[1] is not None for b in model.MoEBlocks)
+    check(alloc_b.new_cache)
+    check(alloc_a.new_cache)
+    # New parameter tensors at new addresses.
+    state = {k: v.clone() * 0.5 for k, v in model.state_dict().items()}
+    model.load_state_dict(state, assign=True)
+    check(alloc_a.new_cache)
+    # The PyTorch MoE path (no plan), then back.
+    model.set_moe_mode("reference")
+    check(alloc_a.new_cache)
+    assert all(b._one_token[1] is None for b in model.MoEBlocks)
+    model.set_moe_mode("auto")
+    check(alloc_a.new_cache)
+    # The reference's projection + append sequence for the attention half.
+    alloc_a.fuse_qkv = False
+    check(alloc_a.new_cache)
+    assert all(b._one_token[1] is None for b in model.MoEBlocks)
