@@ -37,6 +37,8 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
+SECONDARY_NAMES = ("config2_single_layer", "config3_append_gather", "config5_long_context", "fused_moe_decode",
+                   "config1_e2e_decode")
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
 
@@ -48,6 +50,8 @@ def parse_args():
     p.add_argument("--partition-tokens", type=int, default=0, help="0 = the library's automatic choice")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-secondary", action="store_true")
+    p.add_argument("--secondary", default="",
+                   help="comma-separated secondary figures to run (default: all): " + ", ".join(SECONDARY_NAMES))
     p.add_argument("--unfused", action="store_true",
                    help="run the step's append and decode as two launches instead of mie_paged_decode_append")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
@@ -58,7 +62,11 @@ def parse_args():
         help="first run 10 plain device copies of this many MiB (reads and writes that many bytes "
         "each), to scale hardware byte counters against a kernel of known traffic",
     )
-    return p.parse_args()
+    args = p.parse_args()
+    unknown = sorted({n for n in args.secondary.split(",") if n} - set(SECONDARY_NAMES))
+    if unknown:
+        p.error(f"unknown secondary {', '.join(unknown)} (known: {', '.join(SECONDARY_NAMES)})")
+    return args
 
 
 def copy_calibration(torch, mib):
@@ -491,6 +499,7 @@ def main():
 
     secondary = {}
     if not args.no_secondary:
+        chosen = [n for n in args.secondary.split(",") if n] or list(SECONDARY_NAMES)
         for name, fn in (
             ("config2_single_layer", secondary_config2),
             ("config3_append_gather", secondary_config3),
@@ -498,6 +507,8 @@ def main():
             ("fused_moe_decode", secondary_moe),
             ("config1_e2e_decode", secondary_e2e),
         ):
+            if name not in chosen:
+                continue
             log(f"secondary {name}")
             try:
                 secondary[name] = fn(torch)
