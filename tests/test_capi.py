@@ -87,3 +87,35 @@ def test_invalid_arguments_fail_before_launch():
         0, 0, 0, 0, 0, 0, 0, 1, 0, 0, 0, None, 10, 5, 1, 1, 64, 16, 1.0, 0, 0, 0, 0, 0, 0, 0, 1, 0
     )
     assert rc == 1 and b"ctx_len" in lib.mie_last_error()
+
+
+def test_integration_binding_matches_the_library_signatures():
+    """The ctypes binding INTEGRATION.md offers the reference declares, for
+    every entry point it binds, the argument types moe_engine._native uses."""
+    import types
+
+    text = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    block = re.search(r"## ctypes binding.*?```python\n(.*?)```", text, flags=re.S).group(1)
+    fake = types.SimpleNamespace()
+
+    class Entry:
+        pass
+
+    class FakeLib:
+        def __getattr__(self, name):
+            entry = Entry()
+            setattr(self, name, entry)
+            return entry
+
+    lib = FakeLib()
+    fake.CDLL = lambda path: lib
+    ns = {}
+    code = block.replace("import ctypes, math, torch", "import math, torch")
+    ns["ctypes"] = types.SimpleNamespace(**{k: getattr(ctypes, k) for k in dir(ctypes) if not k.startswith("_")})
+    ns["ctypes"].CDLL = fake.CDLL
+    exec(code, ns)
+    bound = {name: entry.argtypes for name, entry in vars(lib).items() if hasattr(entry, "argtypes")}
+    assert len(bound) >= 10
+    for name, argtypes in bound.items():
+        want = _native._SIGNATURES[name][1]
+        assert [t.__name__ for t in argtypes] == [t.__name__ for t in want], name
