@@ -21,6 +21,9 @@
  *   mie_lm_head       <- final_norm + output_projection (model.py:564-565) and,
  *                        optionally, the greedy argmax (:603) for one token
  *   mie_embed         <- token_embedding(ids) + positional_embedding(pos)  src/moe_engine/model.py:558
+ *   mie_block_plan_init, mie_block_decode <- one TransformerMoEBlock.forward for one
+ *                        decode token (model.py:446-449 with :226-269): the five
+ *                        launches above from a stored plan, one call per token
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -74,7 +77,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 9
+#define MIE_ABI_VERSION 10
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -361,6 +364,45 @@ int64_t mie_lm_head_workspace(int32_t vocab);
 int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* weight,
                     const void* bias, int32_t vocab, int32_t dim, void* logits, void* token_out, void* workspace,
                     int64_t workspace_bytes, int32_t* advance, int32_t n_advance, int32_t dtype, void* stream);
+
+/*
+ * One decoder block for ONE decode token (TransformerMoEBlock.forward,
+ * model.py:446-449, with the attention half model.py:226-269) from a launch
+ * plan stored in caller-owned host memory of mie_block_plan_bytes() bytes.
+ * mie_block_decode(plan, x, position, stream) issues, on `stream`:
+ *
+ *   mie_qkv_append(x, attn norm, in_proj, pools, block_table, position) -> q
+ *   mie_paged_decode(q, pools, block_table, ctx = position + 1)           -> attn
+ *   mie_linear_residual(attn, out_proj, residual x)                        -> h
+ *   mie_moe_decode_block(h, moe norm, router, experts)                     -> out
+ *
+ * with the other arguments those entry points take stored by
+ * mie_block_plan_init: the block's weights and norms, the layer's pools
+ * (element strides) and block table, the rows q, attn and h ([num_heads *
+ * head_dim], [num_heads * head_dim], [dim], written by the call), the MoE
+ * scratch and the output row.  The results are those of calling the entry
+ * points in turn.  `workspace` (may be NULL) serves the decode's split
+ * context; a position whose decode needs more than workspace_bytes (see
+ * mie_paged_decode_plan at batch 1 and max_ctx_len = position + 1) fails
+ * with MIE_ERR_WORKSPACE before anything is launched, and the caller
+ * initialises the plan again with a larger workspace.  The plan holds
+ * pointers only: the caller keeps every buffer alive while the plan is used,
+ * and one plan serves calls in stream order.
+ */
+int64_t mie_block_plan_bytes(void);
+int32_t mie_block_plan_init(void* plan, int64_t plan_bytes, int32_t dim, int32_t num_heads, int32_t head_dim,
+                            int32_t block_size, int32_t dtype, const void* attn_ln_weight,
+                            const void* attn_ln_bias, float attn_ln_eps, const void* w_in, const void* b_in,
+                            const void* w_out, const void* b_out, void* k_pool, void* v_pool,
+                            int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                            const int32_t* block_table, int32_t block_table_len, float scale, void* q,
+                            void* attn, void* h, void* workspace, int64_t workspace_bytes,
+                            const void* moe_ln_weight, const void* moe_ln_bias, float moe_ln_eps,
+                            const void* router_weight, const void* w1, const void* b1, const void* w2,
+                            const void* b2, int32_t num_experts, int32_t top_k, int32_t hidden,
+                            void* router_logits, void* expert_ids, void* route_weights, void* hidden_act,
+                            void* out);
+int32_t mie_block_decode(const void* plan, const void* x, int32_t position, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,146 @@
+// One decoder block for one decode token from a stored launch plan.
+//
+// The block of the reference (src/moe_engine/model.py:446-449, attention half
+// :226-269) for a single new token is five launches of this library: the QKV
+// projection into the pool (mie_qkv_append), the paged decode attention
+// (mie_paged_decode), out_proj with the residual add (mie_linear_residual) and
+// the MoE half (mie_moe_decode_block, two launches).  Issued one by one from
+// Python, each costs a foreign call of two dozen arguments; the eager decode
+// step is then bound by the host.  Here the arguments that do not change from
+// token to token (weights, pools, table, scratch rows, shapes) are stored once
+// in caller-owned host memory, and each token is one call with the input row,
+// the position and the stream.  The launches and their arguments are exactly
+// those of the five entry points, so the results are bit-identical to calling
+// them in turn.
+#include <string.h>
+
+#include "mie_common.h"
+
+namespace {
+
+constexpr uint32_t kPlanMagic = 0x6d696562;  // "mieb"
+
+struct BlockPlan {
+  uint32_t magic;
+  int32_t dtype;
+  int32_t dim, num_heads, head_dim, block_size;
+  // attention half
+  const void *attn_ln_w, *attn_ln_b;
+  float attn_ln_eps;
+  const void *w_in, *b_in, *w_out, *b_out;
+  void *k_pool, *v_pool;
+  int64_t pool_stride_block, pool_stride_head;
+  int32_t num_blocks;
+  const int32_t* block_table;
+  int32_t block_table_len;
+  float scale;
+  void *q, *attn, *h;
+  void* workspace;
+  int64_t workspace_bytes;
+  // MoE half
+  const void *moe_ln_w, *moe_ln_b;
+  float moe_ln_eps;
+  const void *router, *w1, *b1, *w2, *b2;
+  int32_t num_experts, top_k, hidden;
+  void *router_logits, *expert_ids, *route_weights, *hidden_act, *out;
+};
+
+}  // namespace
+
+extern "C" int64_t mie_block_plan_bytes(void) { return static_cast<int64_t>(sizeof(BlockPlan)); }
+
+extern "C" int32_t mie_block_plan_init(
+    void* plan, int64_t plan_bytes, int32_t dim, int32_t num_heads, int32_t head_dim, int32_t block_size,
+    int32_t dtype, const void* attn_ln_weight, const void* attn_ln_bias, float attn_ln_eps, const void* w_in,
+    const void* b_in, const void* w_out, const void* b_out, void* k_pool, void* v_pool, int64_t pool_stride_block,
+    int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table, int32_t block_table_len, float scale,
+    void* q, void* attn, void* h, void* workspace, int64_t workspace_bytes, const void* moe_ln_weight,
+    const void* moe_ln_bias, float moe_ln_eps, const void* router_weight, const void* w1, const void* b1,
+    const void* w2, const void* b2, int32_t num_experts, int32_t top_k, int32_t hidden, void* router_logits,
+    void* expert_ids, void* route_weights, void* hidden_act, void* out) {
+  if (!plan || plan_bytes < static_cast<int64_t>(sizeof(BlockPlan)))
+    return mie::fail(MIE_ERR_INVALID, "mie_block_plan_init: plan needs %lld bytes",
+                     static_cast<long long>(sizeof(BlockPlan)));
+  if (dim <= 0 || num_heads <= 0 || head_dim <= 0 || block_size <= 0 || workspace_bytes < 0)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_plan_init: dim %d heads %d head_dim %d block_size %d", dim,
+                     num_heads, head_dim, block_size);
+  if (!q || !attn || !h || !out)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_plan_init: null scratch or output row");
+  BlockPlan p{};
+  p.magic = kPlanMagic;
+  p.dtype = dtype;
+  p.dim = dim;
+  p.num_heads = num_heads;
+  p.head_dim = head_dim;
+  p.block_size = block_size;
+  p.attn_ln_w = attn_ln_weight;
+  p.attn_ln_b = attn_ln_bias;
+  p.attn_ln_eps = attn_ln_eps;
+  p.w_in = w_in;
+  p.b_in = b_in;
+  p.w_out = w_out;
+  p.b_out = b_out;
+  p.k_pool = k_pool;
+  p.v_pool = v_pool;
+  p.pool_stride_block = pool_stride_block;
+  p.pool_stride_head = pool_stride_head;
+  p.num_blocks = num_blocks;
+  p.block_table = block_table;
+  p.block_table_len = block_table_len;
+  p.scale = scale;
+  p.q = q;
+  p.attn = attn;
+  p.h = h;
+  p.workspace = workspace;
+  p.workspace_bytes = workspace ? workspace_bytes : 0;
+  p.moe_ln_w = moe_ln_weight;
+  p.moe_ln_b = moe_ln_bias;
+  p.moe_ln_eps = moe_ln_eps;
+  p.router = router_weight;
+  p.w1 = w1;
+  p.b1 = b1;
+  p.w2 = w2;
+  p.b2 = b2;
+  p.num_experts = num_experts;
+  p.top_k = top_k;
+  p.hidden = hidden;
+  p.router_logits = router_logits;
+  p.expert_ids = expert_ids;
+  p.route_weights = route_weights;
+  p.hidden_act = hidden_act;
+  p.out = out;
+  memcpy(plan, &p, sizeof(p));
+  return MIE_OK;
+}
+
+extern "C" int32_t mie_block_decode(const void* plan, const void* x, int32_t position, void* stream) {
+  if (!plan) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: null plan");
+  BlockPlan p;
+  memcpy(&p, plan, sizeof(p));
+  if (p.magic != kPlanMagic) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: plan not initialised");
+  if (!x || position < 0) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: x %p position %d", x, position);
+  // The decode's split-context workspace is checked before anything is
+  // launched, so a call that cannot finish changes nothing.
+  const int32_t ctx = position + 1;
+  int64_t ws_need = 0;
+  int32_t rc = mie_paged_decode_plan(1, p.num_heads, p.head_dim, p.block_size, ctx, p.dtype, 0, nullptr, &ws_need);
+  if (rc != MIE_OK) return rc;
+  if (ws_need > p.workspace_bytes)
+    return mie::fail(MIE_ERR_WORKSPACE, "mie_block_decode: position %d needs a %lld-byte workspace, plan has %lld",
+                     position, static_cast<long long>(ws_need), static_cast<long long>(p.workspace_bytes));
+  rc = mie_qkv_append(x, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool, p.v_pool,
+                      p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table, p.block_table_len,
+                      nullptr, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
+  if (rc != MIE_OK) return rc;
+  const int64_t row = static_cast<int64_t>(p.num_heads) * p.head_dim;
+  rc = mie_paged_decode(p.q, row, p.head_dim, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head,
+                        p.num_blocks, p.block_table, 0, nullptr, nullptr, ctx, ctx, 1, p.num_heads, p.head_dim,
+                        p.block_size, p.scale, p.attn, row, p.head_dim, p.dtype, ws_need ? p.workspace : nullptr,
+                        ws_need, 0, p.dtype, stream);
+  if (rc != MIE_OK) return rc;
+  rc = mie_linear_residual(p.attn, p.w_out, p.b_out, x, p.h, p.dim, p.dim, p.dtype, stream);
+  if (rc != MIE_OK) return rc;
+  return mie_moe_decode_block(p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1, p.b1, p.w2, p.b2,
+                              p.num_experts, p.top_k, p.dim, p.hidden, p.router_logits, p.expert_ids,
+                              p.route_weights, p.hidden_act, p.out, p.dtype, stream);
+}

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -27,6 +27,9 @@ DTYPE_CODES = {
     torch.float64: 3,
 }
 DECODE_DTYPES = (torch.float32, torch.bfloat16)
+
+# enum mie_status codes the host acts on
+ERR_WORKSPACE = 3
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -117,6 +120,18 @@ _SIGNATURES = {
          _c_void_p, _i32, _c_void_p],  # out, dtype, stream
     ),
     "mie_lm_head_workspace": (_i64, [_i32]),
+    "mie_block_plan_bytes": (_i64, []),
+    "mie_block_plan_init": (
+        _i32,
+        [_c_void_p, _i64, _i32, _i32, _i32, _i32, _i32,  # plan, its bytes, dim, heads, head_dim, block_size, dtype
+         _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # attn norm, eps, in/out proj
+         _c_void_p, _c_void_p, _i64, _i64, _i32, _c_void_p, _i32, _f32,  # pools, strides, blocks, table, len, scale
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,  # q, attn, h rows, workspace, its bytes
+         _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # moe norm, router, experts
+         _i32, _i32, _i32,  # experts, top_k, hidden
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],  # router logits, ids, weights, hidden, out
+    ),
+    "mie_block_decode": (_i32, [_c_void_p, _c_void_p, _i32, _c_void_p]),
     "mie_lm_head": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p,  # x, norm weight, norm bias, eps, W, bias

@@ -20,6 +20,7 @@ attention out_proj, in_proj xavier, the experts' two linears each, router), so
 a seeded model has the reference's weights.
 """
 
+import ctypes
 import math
 from dataclasses import dataclass
 from typing import Optional
@@ -28,7 +29,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention
+from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention, projection
 
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
@@ -638,6 +639,25 @@ class TransformerMoEBlock(nn.Module):
         self.attn_norm = nn.LayerNorm(config.hidden_dim)
         self.moe_norm = nn.LayerNorm(config.hidden_dim)
         self._one_token = None  # (key, launcher or None): see _decode_one_token
+        self.register_load_state_dict_post_hook(TransformerMoEBlock._drop_plan_after_load)
+
+    def drop_decode_plan(self) -> None:
+        """Forget the one-token launch plan; the next decode token builds a
+        new one.  .to() / .float() / ... and load_state_dict call this
+        themselves; code that replaces a parameter of the block any other way
+        calls it too."""
+        self._one_token = None
+
+    @staticmethod
+    def _drop_plan_after_load(module, _incompatible_keys) -> None:
+        # A load replaces the expert storage (MoEFeedForward repacks), and
+        # assign=True replaces every parameter.
+        module.drop_decode_plan()
+
+    def _apply(self, fn, recurse=True):
+        # Device / dtype conversion replaces the parameters.
+        self.drop_decode_plan()
+        return super()._apply(fn, recurse=recurse)
 
     def forward(self, x, cache, layer_idx, position):
         # One-token eager decode with both fused halves runs from a cached
@@ -658,29 +678,15 @@ class TransformerMoEBlock(nn.Module):
         return out
 
     def _one_token_key(self, x, cache, layer_idx):
-        """Every value the cached launch arguments are computed from: the
-        cache, pool and table addresses and shapes, the block's parameter and
-        expert-storage addresses, the norms' eps, the MoE mode, and x's dtype
-        and device.  A change to any of them (a new cache, a model moved or
-        reloaded) builds a new plan."""
-        alloc = cache.allocator
+        """What a plan is built for besides the block's own tensors: the
+        cache (its pools, table and attention mode), the allocator's fuse_qkv
+        switch, the MoE mode, the norms' eps, and x's dtype, device and width.
+        The block's parameters and expert storage are covered by dropping the
+        plan whenever they can be replaced (_apply, load_state_dict,
+        drop_decode_plan), so each token compares this short key only."""
         m = self._modules
-        att, moe = m["attention"], m["moe"]
-        an, mn = m["attn_norm"], m["moe_norm"]
-        pa, po = att._parameters, att._modules["out_proj"]._parameters
-        pan, pmn = an._parameters, mn._parameters
-        st, bf = moe._expert_storage, moe._buffers
-        ptr = _native.ptr
-        return (
-            layer_idx, cache.attention_mode, getattr(alloc, "fuse_qkv", False), alloc._launch, alloc.num_blocks,
-            alloc.block_size, alloc.num_heads, alloc.head_dim, x.dtype, x.device, x.shape[-1], moe.mode,
-            an.eps, mn.eps, alloc.k_pool.data_ptr(), alloc.v_pool.data_ptr(), cache.block_table_device.data_ptr(),
-            ptr(pa["in_proj_weight"]), ptr(pa["in_proj_bias"]), ptr(po["weight"]), ptr(po["bias"]),
-            ptr(pan["weight"]), ptr(pan["bias"]), ptr(pmn["weight"]), ptr(pmn["bias"]),
-            ptr(moe._modules["router"]._parameters["weight"]), ptr(st["w1"]), ptr(st["b1"]), ptr(st["w2"]),
-            ptr(st["b2"]), ptr(bf["_router_logits"]), ptr(bf["_expert_ids"]), ptr(bf["_route_weights"]),
-            ptr(bf["_expert_hidden"]), ptr(bf["_direct_out"]),
-        )
+        return (layer_idx, cache, cache.attention_mode, cache.allocator.fuse_qkv, m["moe"].mode,
+                m["attn_norm"].eps, m["moe_norm"].eps, x.dtype, x.device, x.shape[-1])
 
     def _decode_one_token(self, x, cache, layer_idx, position):
         """The block for one eager decode token when both fused halves apply:
@@ -701,64 +707,64 @@ class TransformerMoEBlock(nn.Module):
         return None if plan[1] is None else plan[1](x, cache, position)
 
     def _build_one_token(self, x, cache, layer_idx):
+        """A launch plan of the block's five launches (mie_block_plan_init):
+        each token is then one call, mie_block_decode(plan, x, position)."""
         alloc = cache.allocator
         att, moe = self.attention, self.moe
         lib = _native.lib()
-        qkv_fn, dec_fn, lin_fn, moe_fn = (lib.mie_qkv_append, lib.mie_paged_decode, lib.mie_linear_residual,
-                                          lib.mie_moe_decode_block)
         ptr, check, stream_of, decode_plan = _native.ptr, _native.check, _native.stream_of, _native.decode_plan
-        workspace = paged_attention._workspace
         layer_bytes, sblk, shead, code = alloc._launch
         heads, head_dim, block_size, num_blocks = alloc.num_heads, alloc.head_dim, alloc.block_size, alloc.num_blocks
         dim = x.shape[-1]
         dtype, device = x.dtype, x.device
         off = layer_idx * layer_bytes
-        k_ptr, v_ptr = alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off
-        table = cache.block_table_device.data_ptr()
         an, mn = self.attn_norm, self.moe_norm
-        ln_w, ln_b, ln_eps = ptr(an.weight), ptr(an.bias), float(an.eps)
-        w_in, b_in = att.in_proj_weight.data_ptr(), ptr(att.in_proj_bias)
-        w_o, b_o = att.out_proj.weight.data_ptr(), ptr(att.out_proj.bias)
         s = moe._expert_storage
-        moe_args = (ptr(mn.weight), ptr(mn.bias), float(mn.eps), moe.router.weight.data_ptr(), s["w1"].data_ptr(),
-                    s["b1"].data_ptr(), s["w2"].data_ptr(), s["b2"].data_ptr(), moe.router.weight.shape[0],
-                    moe._expert_ids.numel(), dim, s["w1"].shape[1], moe._router_logits.data_ptr(),
-                    moe._expert_ids.data_ptr(), moe._route_weights.data_ptr(), moe._expert_hidden.data_ptr(),
-                    moe._direct_out.data_ptr(), code)
         out = moe._direct_out.view(1, 1, dim)
         # The block's intermediates, reused by every token: q, the attention
         # output and the attention half's output are consumed within the call.
         q = torch.empty((1, heads, 1, head_dim), dtype=dtype, device=device)
         attn = torch.empty_like(q)
         h = torch.empty((1, 1, dim), dtype=dtype, device=device)
-        q_ptr, attn_ptr, h_ptr = q.data_ptr(), attn.data_ptr(), h.data_ptr()
-        scale = 1.0 / math.sqrt(head_dim)
+        plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
+        held = {}  # the split-context workspace the plan points at
+
+        def init(ws):
+            held["ws"] = ws
+            check(lib.mie_block_plan_init(
+                plan, len(plan), dim, heads, head_dim, block_size, code,
+                ptr(an.weight), ptr(an.bias), float(an.eps), att.in_proj_weight.data_ptr(), ptr(att.in_proj_bias),
+                att.out_proj.weight.data_ptr(), ptr(att.out_proj.bias),
+                alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off, sblk, shead, num_blocks,
+                cache.block_table_device.data_ptr(), num_blocks, 1.0 / math.sqrt(head_dim),
+                q.data_ptr(), attn.data_ptr(), h.data_ptr(), ptr(ws), 0 if ws is None else ws.numel(),
+                ptr(mn.weight), ptr(mn.bias), float(mn.eps), moe.router.weight.data_ptr(),
+                s["w1"].data_ptr(), s["b1"].data_ptr(), s["w2"].data_ptr(), s["b2"].data_ptr(),
+                moe.router.weight.shape[0], moe._expert_ids.numel(), s["w1"].shape[1],
+                moe._router_logits.data_ptr(), moe._expert_ids.data_ptr(), moe._route_weights.data_ptr(),
+                moe._expert_hidden.data_ptr(), moe._direct_out.data_ptr(),
+            ), "mie_block_plan_init")
+
+        init(None)
+        run = lib.mie_block_decode
 
         def launch(x, cache, position):
             cache._reserve(position + 1)
             stream = stream_of(x)
-            x_ptr = x.data_ptr()
-            rc = qkv_fn(x_ptr, ln_w, ln_b, ln_eps, w_in, b_in, dim, k_ptr, v_ptr, sblk, shead, num_blocks, table,
-                        num_blocks, None, position, q_ptr, heads, head_dim, block_size, code, stream)
+            rc = run(plan, x.data_ptr(), position, stream)
+            if rc == _native.ERR_WORKSPACE:
+                # A longer context splits into partitions: the plan is set up
+                # again with a workspace at least twice the last one (nothing
+                # was launched).
+                _, need = decode_plan(1, heads, head_dim, block_size, position + 1, dtype, 0)
+                old = held["ws"]
+                init(torch.empty(max(need, 0 if old is None else 2 * old.numel()), dtype=torch.uint8, device=device))
+                rc = run(plan, x.data_ptr(), position, stream)
             if rc:
-                check(rc, "mie_qkv_append")
-            ctx = position + 1
-            _, ws_bytes = decode_plan(1, heads, head_dim, block_size, ctx, dtype, 0)
-            ws = workspace(ws_bytes, device)
-            rc = dec_fn(q_ptr, heads * head_dim, head_dim, k_ptr, v_ptr, sblk, shead, num_blocks, table, 0,
-                        None, None, ctx, ctx, 1, heads, head_dim, block_size, scale, attn_ptr, heads * head_dim,
-                        head_dim, code, ptr(ws), ws_bytes, 0, code, stream)
-            if rc:
-                check(rc, "mie_paged_decode")
-            rc = lin_fn(attn_ptr, w_o, b_o, x_ptr, h_ptr, dim, dim, code, stream)
-            if rc:
-                check(rc, "mie_linear_residual")
-            rc = moe_fn(h_ptr, *moe_args, stream)
-            if rc:
-                check(rc, "mie_moe_decode_block")
+                check(rc, "mie_block_decode")
             return out
 
-        launch.buffers = (q, attn, h)  # kept alive with the plan
+        launch.buffers = (q, attn, h, plan, held)  # kept alive with the plan
         return launch
 
 
@@ -790,7 +796,15 @@ class Model(nn.Module):
 
     def forward(self, token_ids, cache):
         x = self.hidden_states(token_ids, cache)
+        if x.shape[0] == 1 and x.shape[1] == 1 and self._head_on_device(x):
+            # One decode token: final norm and LM head in one launch.
+            return projection.lm_head(x.view(-1), self.final_norm, self.output_projection).view(1, 1, -1)
         return self.output_projection(self.final_norm(x))
+
+    def _head_on_device(self, x) -> bool:
+        w = self.output_projection.weight
+        return (_native.is_rocm_device(x) and x.is_contiguous() and x.dtype == w.dtype
+                and projection.supported(x.shape[-1], x.dtype) and w.is_contiguous())
 
     def hidden_states(self, token_ids, cache):
         """The forward pass up to the final norm (model.py:543-562): the
@@ -806,6 +820,10 @@ class Model(nn.Module):
         graph_pos = getattr(cache, "graph_pos", None)
         if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
             x = embedding.embed(token_ids, graph_pos, self.token_embedding, self.positional_embedding)
+        elif (batch == 1 and seq_len <= 65535 and token_ids.dtype == torch.int64 and token_ids.is_contiguous()
+              and embedding.supported(self.token_embedding, self.positional_embedding)):
+            # One launch for the two lookups and the add (bit-identical sum).
+            x = embedding.embed(token_ids, position, self.token_embedding, self.positional_embedding)
         else:
             pos = torch.arange(position, position + seq_len, device=token_ids.device)
             x = self.token_embedding(token_ids) + self.positional_embedding(pos)
@@ -842,7 +860,10 @@ class Model(nn.Module):
         for _ in range(max_new_tokens):
             logits = self(step_input, cache)[:, -1, :]
             if temperature == 0:
-                next_token = torch.argmax(logits, dim=-1, keepdim=True)
+                if logits.dtype == torch.float32 and logits.is_contiguous() and _native.is_rocm_device(logits):
+                    next_token = projection.argmax(logits.view(-1)).view(1, 1)  # one launch, same pick
+                else:
+                    next_token = torch.argmax(logits, dim=-1, keepdim=True)
             else:
                 logits = logits / temperature
                 if top_k is not None:

@@ -6,6 +6,8 @@
 - lm_head (mie_lm_head): the decode step's head, final_norm + output_projection
   (model.py:564-565), optionally with generate's greedy torch.argmax (:603)
   written to a device token, in two launches.
+- argmax (mie_argmax): generate's greedy torch.argmax (model.py:603) over one
+  row of float32 logits, in one launch.
 
 float32 or bfloat16.
 """
@@ -114,6 +116,24 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
             _native.dtype_code(dtype), _native.stream_of(weight),
         ),
         "mie_lm_head",
+    )
+    return out
+
+
+def argmax(x, out=None):
+    """torch.argmax of the contiguous float32 device vector x (the first index
+    of the maximum, NaN counting as the largest), written to `out` (an int64
+    device tensor of one element, allocated when None).  Returns out."""
+    if not (_native.is_rocm_device(x) and x.dtype == torch.float32 and x.is_contiguous()) or x.numel() == 0:
+        raise ValueError("mie_argmax takes a non-empty contiguous float32 vector on a ROCm device")
+    if out is None:
+        out = torch.empty(1, dtype=torch.int64, device=x.device)
+    elif out.dtype != torch.int64 or out.numel() != 1 or out.device != x.device:
+        raise ValueError("out must be one int64 value on x's device")
+    _native.check(
+        _native.lib().mie_argmax(x.data_ptr(), x.numel(), out.data_ptr(), _native.dtype_code(x.dtype),
+                                 _native.stream_of(x)),
+        "mie_argmax",
     )
     return out
 

@@ -152,8 +152,9 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
     (TransformerMoEBlock._decode_one_token).  Every decode below is checked
     against the same step with the plan disabled (the per-call fused path)
     after changing what the plan depends on: a second cache on another
-    allocator, reloaded weights (new tensors, assign=True), the MoE mode, and
-    the allocator's fuse_qkv switch."""
+    allocator, reloaded weights (new tensors, assign=True), the MoE mode, a
+    module conversion, a parameter replaced by hand (with drop_decode_plan),
+    and the allocator's fuse_qkv switch."""
     print_case("cached one-token plan")
     torch.manual_seed(0)
     model = Model(ModelConfig(**TINY)).to("cuda").eval()
@@ -194,7 +195,50 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
     assert all(b._one_token[1] is None for b in model.MoEBlocks)
     model.set_moe_mode("auto")
     check(alloc_a.new_cache)
+    # A conversion (.float() is one even when nothing changes) drops the plans.
+    model.float()
+    assert all(b._one_token is None for b in model.MoEBlocks)
+    check(alloc_a.new_cache)
+    # A parameter replaced by hand, then the plan dropped by hand.
+    out_proj = model.MoEBlocks[1].attention.out_proj
+    out_proj.weight = torch.nn.Parameter(out_proj.weight.detach() * 0.25)
+    model.MoEBlocks[1].drop_decode_plan()
+    check(alloc_a.new_cache)
     # The reference's projection + append sequence for the attention half.
     alloc_a.fuse_qkv = False
     check(alloc_a.new_cache)
     assert all(b._one_token[1] is None for b in model.MoEBlocks)
+
+
+def test_block_plan_grows_its_workspace_for_split_contexts():
+    """Past 1024 cached tokens with few heads, the decode splits the context
+    into partitions and needs a workspace: the block's launch plan
+    (mie_block_decode) refuses such a position before launching anything,
+    and the block sets the plan up again with a workspace.  Logits match the
+    per-call fused path at every step, and a plan holds a workspace after."""
+    print_case("block plan workspace growth")
+    torch.manual_seed(1)
+    cfg = dict(max_seq_length=1200, vocab_size=96, num_layers=2, hidden_dim=64, num_heads=2, num_experts=4, top_k=2)
+    model = Model(ModelConfig(**cfg)).to("cuda").eval()
+    ids = torch.randint(0, cfg["vocab_size"], (1, 1030), device="cuda")
+    alloc = model.new_block_allocator(num_blocks=80, block_size=16, attention_mode="direct")
+
+    def run(use_plan):
+        blocks = list(model.MoEBlocks)
+        saved = [b._decode_one_token for b in blocks]
+        if not use_plan:
+            for b in blocks:
+                b._decode_one_token = lambda *args, **kwargs: None
+        try:
+            cache = alloc.new_cache()
+            out = stepwise_logits(model, ids, cache, 1020)
+            cache.free()
+            return out
+        finally:
+            for b, f in zip(blocks, saved):
+                b._decode_one_token = f
+
+    torch.testing.assert_close(run(True), run(False), atol=1e-5, rtol=1e-5)
+    for b in model.MoEBlocks:
+        launcher = b._one_token[1]
+        assert launcher is not None and launcher.buffers[-1]["ws"] is not None
