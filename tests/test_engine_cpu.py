@@ -343,3 +343,26 @@ def test_moe_auto_falls_back_on_cpu_and_forced_direct_fails():
         torch.testing.assert_close(moe(prefill, decode=False), moe._forward_reference(prefill), atol=0, rtol=0)
     with pytest.raises(ValueError, match="unknown MoE mode"):
         moe.set_mode("fast")
+
+
+def test_decode_plans_are_dropped_when_parameters_can_change():
+    """A block's one-token launch plan holds parameter addresses; conversions
+    (.to / .float / .double), load_state_dict (copy and assign) and
+    drop_decode_plan() forget it, so the next decode token builds a new one."""
+    model = Model(ModelConfig(**TINY)).eval()
+    blocks = list(model.MoEBlocks)
+
+    def plant():
+        for b in blocks:
+            b._one_token = ("stale key", None)
+
+    for change in (
+        lambda: model.float(),
+        lambda: model.to("cpu"),
+        lambda: model.load_state_dict(model.state_dict()),
+        lambda: model.load_state_dict({k: v.clone() for k, v in model.state_dict().items()}, assign=True),
+        lambda: [b.drop_decode_plan() for b in blocks],
+    ):
+        plant()
+        change()
+        assert all(b._one_token is None for b in blocks)
