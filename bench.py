@@ -217,6 +217,18 @@ def run_config4(torch, args):
 # ---- CPU baseline (the oracle's gather + SDPA path, on the host cores) -------------
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo ("unknown" elsewhere)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(torch, w, budget_s):
     from oracle import paged_ref as ref
     from moe_engine import workloads
@@ -244,7 +256,7 @@ def cpu_baseline(torch, w, budget_s):
         "sample": (
             f"sequences {sample} of config 4 ({sum(lens)} tokens, bf16), {passes} passes of "
             f"per-sequence gather + torch scaled_dot_product_attention in {elapsed:.1f} s; "
-            f"host {os.cpu_count()} logical CPUs, torch threads {threads}"
+            f"host {os.cpu_count()} logical CPUs ({cpu_model()}), torch threads {threads}"
         ),
         "ms_per_pass": round(elapsed / passes * 1e3, 2),
     }
