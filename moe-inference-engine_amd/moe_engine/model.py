@@ -796,8 +796,9 @@ class Model(nn.Module):
 
     def forward(self, token_ids, cache):
         x = self.hidden_states(token_ids, cache)
-        if x.shape[0] == 1 and x.shape[1] == 1 and self._head_on_device(x):
-            # One decode token: final norm and LM head in one launch.
+        if x.shape[0] == 1 and x.shape[1] == 1 and not torch.is_grad_enabled() and self._head_on_device(x):
+            # One decode token at inference: final norm and LM head in one
+            # launch (no autograd graph; with gradients on, the modules run).
             return projection.lm_head(x.view(-1), self.final_norm, self.output_projection).view(1, 1, -1)
         return self.output_projection(self.final_norm(x))
 
@@ -821,8 +822,9 @@ class Model(nn.Module):
         if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
             x = embedding.embed(token_ids, graph_pos, self.token_embedding, self.positional_embedding)
         elif (batch == 1 and seq_len <= 65535 and token_ids.dtype == torch.int64 and token_ids.is_contiguous()
-              and embedding.supported(self.token_embedding, self.positional_embedding)):
-            # One launch for the two lookups and the add (bit-identical sum).
+              and not torch.is_grad_enabled() and embedding.supported(self.token_embedding, self.positional_embedding)):
+            # At inference, one launch for the two lookups and the add
+            # (bit-identical sum).
             x = embedding.embed(token_ids, position, self.token_embedding, self.positional_embedding)
         else:
             pos = torch.arange(position, position + seq_len, device=token_ids.device)
