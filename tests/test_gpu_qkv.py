@@ -110,6 +110,28 @@ def test_qkv_append_matches_oracle(dtype, heads, head_dim, block_size, norm, bia
         assert np.array_equal(ref.raw_bits(got), ref.raw_bits(before))
 
 
+def draw_qkv(seed):
+    """A random supported case: dtype, heads, head_dim (widths up to 2048),
+    block size, norm and bias present or not, position, host or device."""
+    import random
+
+    rng = random.Random(seed)
+    while True:
+        dtype = rng.choice((torch.float32, torch.bfloat16))
+        heads = rng.choice((1, 2, 3, 5, 8, 12, 16))
+        head_dim = rng.choice((4, 8, 12, 16, 24, 32, 40, 64, 96, 128))
+        if heads * head_dim <= 2048 and kv_ops.qkv_append_supported(heads * head_dim, dtype):
+            break
+    return (dtype, heads, head_dim, rng.choice((1, 3, 4, 16, 32)), rng.random() < 0.7, rng.random() < 0.7,
+            rng.randint(0, 300), rng.random() < 0.5)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_qkv_append_matches_oracle(seed):
+    """Drawn cases through the same checks as the fixed ones above."""
+    test_qkv_append_matches_oracle(*draw_qkv(seed))
+
+
 def test_rows_land_where_append_rows_puts_them():
     """Placement against the oracle's append: the pool after the fused call
     equals append_rows of the kernel's own K/V values at every position."""
