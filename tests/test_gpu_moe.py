@@ -58,6 +58,37 @@ def test_fused_decode_matches_pytorch_path(dim, hidden, experts, top_k):
         assert_output_close(got, want)
 
 
+@pytest.mark.parametrize("seed", range(16))
+def test_random_fused_decode_and_block_match_pytorch_path(seed):
+    """Drawn widths (multiples of 4 up to 2048), hidden sizes, expert counts
+    (up to 64) and top-k (up to 8): the fused decode and the block form
+    against the module's PyTorch path, as in the fixed cases."""
+    import random
+
+    rng = random.Random(seed)
+    dim = rng.choice((4, 16, 36, 64, 100, 256, 768, 2048))
+    hidden = rng.choice((4, 12, 64, 200, 1024, 2048))
+    experts = rng.choice((1, 2, 3, 8, 17, 64))
+    top_k = rng.randint(1, min(8, experts))
+    print_case("random moe", seed, dim, hidden, experts, top_k)
+    layer = moe(dim, hidden, experts, top_k, seed=seed)
+    if not layer.direct_configuration_supported(1):
+        pytest.skip(f"dim {dim} hidden {hidden} experts {experts} top_k {top_k} is not built")
+    norm = torch.nn.LayerNorm(dim).to("cuda")
+    with torch.no_grad():
+        norm.weight.uniform_(0.5, 1.5)
+        norm.bias.uniform_(-0.1, 0.1)
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    for _ in range(3):
+        x = torch.randn(1, 1, dim, generator=gen, device="cuda")
+        with torch.no_grad():
+            assert_output_close(layer(x, decode=True).clone(), layer._forward_reference(x))
+            want = x + layer._forward_reference(norm(x))
+            got = layer.fused_block_decode(x, norm)
+            assert got is not None
+            assert_output_close(got.clone(), want)
+
+
 @pytest.mark.parametrize("experts,top_k", [(8, 2), (16, 4), (64, 8)])
 def test_router_logits_topk_ids_and_normalized_weights_match_pytorch(experts, top_k):
     layer = moe(768, 256, experts, top_k)
