@@ -119,3 +119,22 @@ def test_integration_binding_matches_the_library_signatures():
     for name, argtypes in bound.items():
         want = _native._SIGNATURES[name][1]
         assert [t.__name__ for t in argtypes] == [t.__name__ for t in want], name
+
+
+def test_block_plan_checks_fail_before_launch():
+    """mie_block_plan_init refuses a short plan buffer and missing rows;
+    mie_block_decode refuses a buffer that was never initialised - all on the
+    host, before any launch."""
+    lib = _native.lib()
+    size = lib.mie_block_plan_bytes()
+    assert 64 <= size <= 4096
+    small = ctypes.create_string_buffer(size - 1)
+    args = [0] * 41  # dim .. out after (plan, plan_bytes); zeros are never dereferenced
+    args[0:5] = [64, 2, 32, 16, 0]  # dim, heads, head_dim, block_size, dtype
+    rc = lib.mie_block_plan_init(small, len(small), *args)
+    assert rc == 1 and b"plan needs" in lib.mie_last_error()
+    plan = ctypes.create_string_buffer(size)
+    rc = lib.mie_block_plan_init(plan, len(plan), *args)
+    assert rc == 1 and b"null scratch" in lib.mie_last_error()
+    rc = lib.mie_block_decode(ctypes.create_string_buffer(size), 1 << 20, 5, None)
+    assert rc == 1 and b"not initialised" in lib.mie_last_error()
