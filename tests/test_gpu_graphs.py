@@ -6,9 +6,11 @@ eager work of the same model (another sequence in the same block pool) and a
 device synchronization between replays, and checks every replay: its logits
 against the eager step's for the same token and position, and the greedy
 tokens against Model.generate (reference model.py:567-621).  The graph's
-decode launch is sized for the pool's capacity and splits the context into
-128-token partitions, while the eager launch is sized for the exact length,
-so float32 logits agree to rounding, not bit for bit.
+decode launch is sized for the pool's capacity: at block size 16 (1280
+positions) it splits the context into 64-token partitions merged by a second
+launch, at block size 4 (320 positions) it is the one-launch workgroup form.
+The eager launch is sized for the exact length, so float32 logits agree to
+rounding, not bit for bit.
 """
 
 import pytest
