@@ -9,6 +9,10 @@ underneath the paged cache on a ROCm device:
   * PagedKVCache.read   -> one mie_kv_gather launch (K and V)
   * direct decode       -> mie_paged_decode (moe_engine.paged_attention)
   * one-token MoE       -> mie_moe_decode (moe_engine.fused_moe)
+  * one decode token through a whole block (both halves fused) -> one
+    mie_block_decode call into a stored launch plan (five launches)
+  * at inference, the embedding, the one-token head and the greedy pick ->
+    mie_embed, mie_lm_head, mie_argmax
 
 A paged pool on a ROCm device requires the HIP library and raises at
 construction without it.  Pools on the CPU use PyTorch indexing, which is the
