@@ -817,11 +817,6 @@ class Model(nn.Module):
         batch, seq_len = token_ids.shape
         position = cache.position
         assert position + seq_len <= self.max_seq_length, "KV cache is full"
-        # A forced-direct MoE must fail before layer 0 writes K/V or reserves a block.
-        if position > 0 and seq_len == 1:
-            for block in self.MoEBlocks:
-                block.moe.preflight_direct_decode(batch_size=batch)
-
         graph_pos = getattr(cache, "graph_pos", None)
         if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
             x = embedding.embed(token_ids, graph_pos, self.token_embedding, self.positional_embedding)
@@ -833,6 +828,14 @@ class Model(nn.Module):
         else:
             pos = torch.arange(position, position + seq_len, device=token_ids.device)
             x = self.token_embedding(token_ids) + self.positional_embedding(pos)
+        # A forced-direct MoE must fail before layer 0 writes K/V or reserves a
+        # block (the embedding above touches no cache).  Only mode 'direct'
+        # can fail, so the others are skipped without a call.
+        if position > 0 and seq_len == 1:
+            for block in self.MoEBlocks:
+                moe = block._modules["moe"]
+                if moe.mode == "direct":
+                    moe.preflight_direct_decode(batch_size=batch)
         for i, block in enumerate(self.MoEBlocks):
             x = block(x, cache, i, position)
         cache.position += seq_len
