@@ -327,6 +327,19 @@ int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* l
 int32_t mie_argmax(const void* x, int64_t n, void* out, int32_t dtype, void* stream);
 
 /*
+ * Token plus positional embedding (model.py:558) of n tokens:
+ *     out[i, :] = round(token_table[token_ids[i], :] + pos_table[pos_i, :])
+ * with pos_i = positions[i] (device int32) or, when positions is NULL,
+ * position + i.  token_ids are int64; tables [vocab, dim] and
+ * [max_positions, dim] and out [n, dim] in `dtype` (float32 or bfloat16),
+ * summed in float32 and rounded once.  An id or position outside its table
+ * writes a row of NaN.  n <= 65535.
+ */
+int32_t mie_embed(const void* token_ids, const int32_t* positions, int32_t position, int32_t n,
+                  const void* token_table, int32_t vocab, const void* pos_table, int32_t max_positions, int32_t dim,
+                  void* out, int32_t dtype, void* stream);
+
+/*
  * The decode step's head for one token (model.py:564-565, then :603):
  *     logits[v] = round(W[v, :] . round(LayerNorm(x)) + bias[v])   v < vocab
  * with the norm skipped when ln_weight is NULL and the bias when bias is NULL
@@ -347,19 +360,6 @@ int32_t mie_argmax(const void* x, int64_t n, void* out, int32_t dtype, void* str
  * captured decode step advances its device position and context length there.
  * NULL / 0 for none.
  */
-/*
- * Token plus positional embedding (model.py:558) of n tokens:
- *     out[i, :] = round(token_table[token_ids[i], :] + pos_table[pos_i, :])
- * with pos_i = positions[i] (device int32) or, when positions is NULL,
- * position + i.  token_ids are int64; tables [vocab, dim] and
- * [max_positions, dim] and out [n, dim] in `dtype` (float32 or bfloat16),
- * summed in float32 and rounded once.  An id or position outside its table
- * writes a row of NaN.  n <= 65535.
- */
-int32_t mie_embed(const void* token_ids, const int32_t* positions, int32_t position, int32_t n,
-                  const void* token_table, int32_t vocab, const void* pos_table, int32_t max_positions, int32_t dim,
-                  void* out, int32_t dtype, void* stream);
-
 int64_t mie_lm_head_workspace(int32_t vocab);
 int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* weight,
                     const void* bias, int32_t vocab, int32_t dim, void* logits, void* token_out, void* workspace,
