@@ -88,24 +88,13 @@ def log(*parts):
 # ---- the measured step -----------------------------------------------------------
 
 
-def config4_setup(torch, partition_tokens):
-    from moe_engine import workloads
-
-    lens = workloads.cfg4_lens()
-    w = workloads.make_workload(lens, block_size=16, num_blocks=40000, dtype=torch.bfloat16, seed=2)
-    batch, heads, dim = len(lens), 12, 64
-    gen = torch.Generator(device="cuda").manual_seed(22)
-    k_new = torch.randn(batch, heads, 1, dim, generator=gen, device="cuda").to(torch.bfloat16)
-    v_new = torch.randn(batch, heads, 1, dim, generator=gen, device="cuda").to(torch.bfloat16)
-    positions = (w.context_lens - 1).contiguous()
-    out = torch.empty(batch, heads, dim, dtype=torch.bfloat16, device="cuda")
-    return w, k_new, v_new, positions, out
-
-
 def run_config4(torch, args):
-    from moe_engine import _native, kv_ops, paged_attention, workloads
+    from moe_engine import _native, workloads
 
-    w, k_new, v_new, positions, out = config4_setup(torch, args.partition_tokens)
+    # The step object is the one tests/test_gpu_decode.py checks against the
+    # oracle: the same workload, new rows and calls.
+    step = workloads.config4_step(out_dtype=torch.bfloat16, partition_tokens=args.partition_tokens)
+    w = step.w
     heads, dim = 12, 64
     attn_bytes = workloads.attention_bytes(w.lens, heads, dim, 16, 2)
     app_bytes = workloads.append_bytes(len(w.lens), heads, dim, 2)
@@ -113,31 +102,12 @@ def run_config4(torch, args):
         len(w.lens), heads, dim, 16, w.max_len, torch.bfloat16, args.partition_tokens
     )
 
-    k_rows, v_rows = k_new[:, :, 0], v_new[:, :, 0]
-
-    def append():
-        kv_ops.append(w.k_pool, w.v_pool, 0, k_new, v_new, w.block_tables, positions=positions)
-
-    def attend():
-        paged_attention.decode_batched(
-            w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
-            out=out, partition_tokens=args.partition_tokens, context_lens_host=w.lens,
-        )
-
-    def step_fused():
-        # The new token is each sequence's last context token: one launch
-        # stores it and attends (mie_paged_decode_append).
-        paged_attention.decode_batched(
-            w.q, w.k_pool, w.v_pool, 0, w.block_tables, w.context_lens, w.max_len,
-            out=out, partition_tokens=args.partition_tokens, context_lens_host=w.lens, k_new=k_rows, v_new=v_rows,
-        )
-
     # Timed region: the whole step.  Fused, the step is one launch, so one
     # pair of HIP events around the timed loop gives its average duration
     # (region / steps: inter-launch gaps included, no per-call event packets,
     # which cost ~1-2 us of stream time each).  Unfused, events bracket every
     # attention call to separate it from the append launch.
-    before, timed = (append, attend) if args.unfused else (None, step_fused)
+    before, timed = (step.append, step.attend) if args.unfused else (None, step.fused)
     timed_bytes = attn_bytes if args.unfused else attn_bytes + app_bytes
     for _ in range(args.warmup):
         if before:

@@ -142,3 +142,81 @@ def cfg4_lens(batch=64, low=512, high=8192, seed=2):
     """Context lengths of BASELINE config 4: U[low, high] from `seed`."""
     g = torch.Generator().manual_seed(seed)
     return torch.randint(low, high + 1, (batch,), generator=g).tolist()
+
+
+def take_last_tokens(w: Workload):
+    """Each sequence's last context token's K/V rows ([B, H, D] each), read
+    from the pool and then zeroed there: a decode step that appends them
+    (its new token is its last context token) restores the pool exactly."""
+    heads, dim = w.k_pool.shape[2], w.k_pool.shape[4]
+    bs = w.block_size
+    k_new = torch.zeros(len(w.lens), heads, dim, dtype=w.k_pool.dtype, device=w.k_pool.device)
+    v_new = torch.zeros_like(k_new)
+    for b, ctx in enumerate(w.lens):
+        if ctx == 0:
+            continue
+        blk, slot = w.tables[b][(ctx - 1) // bs], (ctx - 1) % bs
+        k_new[b] = w.k_pool[w.layer, blk, :, slot]
+        v_new[b] = w.v_pool[w.layer, blk, :, slot]
+        w.k_pool[w.layer, blk, :, slot] = 0
+        w.v_pool[w.layer, blk, :, slot] = 0
+    return k_new, v_new
+
+
+@dataclass
+class DecodeStep:
+    """One decode step of one layer over a batch: every sequence's new token
+    (its last context token, rows k_new / v_new [B, H, D]) is appended
+    through its block table and attended to together with the rest of its
+    context.  `fused()` is one mie_paged_decode_append call; `append()` then
+    `attend()` is the same step as the append launch and the decode launch.
+    bench.py times exactly these calls."""
+
+    w: Workload
+    k_new: torch.Tensor
+    v_new: torch.Tensor
+    out: torch.Tensor
+    partition_tokens: int = 0
+
+    def __post_init__(self):
+        # Position of each new token: its sequence's last slot (an empty
+        # sequence gets -1, which the append skips).
+        self.positions = (self.w.context_lens - 1).contiguous()
+
+    def fused(self):
+        from moe_engine import paged_attention
+
+        w = self.w
+        return paged_attention.decode_batched(
+            w.q, w.k_pool, w.v_pool, w.layer, w.block_tables, w.context_lens, w.max_len,
+            out=self.out, partition_tokens=self.partition_tokens, context_lens_host=w.lens,
+            k_new=self.k_new, v_new=self.v_new,
+        )
+
+    def append(self):
+        from moe_engine import kv_ops
+
+        w = self.w
+        kv_ops.append(w.k_pool, w.v_pool, w.layer, self.k_new[:, :, None], self.v_new[:, :, None],
+                      w.block_tables, positions=self.positions)
+
+    def attend(self):
+        from moe_engine import paged_attention
+
+        w = self.w
+        return paged_attention.decode_batched(
+            w.q, w.k_pool, w.v_pool, w.layer, w.block_tables, w.context_lens, w.max_len,
+            out=self.out, partition_tokens=self.partition_tokens, context_lens_host=w.lens,
+        )
+
+
+def config4_step(out_dtype=torch.bfloat16, partition_tokens=0, device="cuda"):
+    """BASELINE config 4's decode step: 64 sequences, contexts U[512, 8192]
+    (seed 2), 12 x 64, block 16, bf16, tables shuffled over a shared
+    40000-block pool; the new rows are the sequences' last tokens, taken out
+    of the pool (take_last_tokens).  Output [64, 12, 64] in out_dtype."""
+    lens = cfg4_lens()
+    w = make_workload(lens, block_size=16, num_blocks=40000, dtype=torch.bfloat16, seed=2, device=device)
+    k_new, v_new = take_last_tokens(w)
+    out = torch.empty(len(lens), 12, 64, dtype=out_dtype, device=device)
+    return DecodeStep(w, k_new, v_new, out, partition_tokens)

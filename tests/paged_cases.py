@@ -15,6 +15,7 @@ from moe_engine.workloads import (  # noqa: F401  (re-exported for the tests)
     make_workload,
     scatter_tokens,
     sequence_kv,
+    take_last_tokens,
 )
 from oracle import paged_ref as ref
 
@@ -34,21 +35,3 @@ def bf16_close(got, want, atol=2e-3):
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     return bool(np.all(np.abs(got - want) <= atol + math.ldexp(1.0, -8) * np.abs(want)))
-
-
-def take_last_tokens(w):
-    """The new rows of a fused append: each sequence's last token's K/V, read
-    from the pool and then zeroed there, so only the fused store can restore it."""
-    heads, dim = w.k_pool.shape[2], w.k_pool.shape[4]
-    bs = w.k_pool.shape[3]
-    k_new = torch.zeros(len(w.lens), heads, dim, dtype=w.k_pool.dtype, device=w.k_pool.device)
-    v_new = torch.zeros_like(k_new)
-    for b, ctx in enumerate(w.lens):
-        if ctx == 0:
-            continue
-        blk, slot = w.tables[b][(ctx - 1) // bs], (ctx - 1) % bs
-        k_new[b] = w.k_pool[w.layer, blk, :, slot]
-        v_new[b] = w.v_pool[w.layer, blk, :, slot]
-        w.k_pool[w.layer, blk, :, slot] = 0
-        w.v_pool[w.layer, blk, :, slot] = 0
-    return k_new, v_new

@@ -173,28 +173,82 @@ def test_config4_batched_64_sequences_bf16():
     check_workload(w)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_config4_timed_step(out_dtype):
+    """The step bench.py times, through the same object (workloads.config4_step):
+    one mie_paged_decode_append call over config 4 with the new rows passed in,
+    host lengths (longest-first order) and the automatic plan.  The new rows
+    were taken out of the pool, so only the launch's stores can put them back:
+    afterwards both pools are bit-identical to the workload as built, and
+    every sequence's output is the oracle's attention over its full context.
+    A second call (the bench repeats the step) gives the same bits."""
+    from moe_engine import workloads
+
+    print_case("config4 timed step", out_dtype)
+    lens = cfg4_lens()
+    built = make_workload(lens, block_size=16, num_blocks=40000, dtype=torch.bfloat16, seed=2)
+    step = workloads.config4_step(out_dtype=out_dtype)
+    w = step.w
+    assert w.lens == built.lens and w.tables == built.tables
+    assert not torch.equal(w.k_pool, built.k_pool), "the new rows must be missing before the step"
+    want = oracle_outputs(built)
+    got = step.fused().clone()
+    assert torch.equal(w.k_pool.view(torch.int16), built.k_pool.view(torch.int16))
+    assert torch.equal(w.v_pool.view(torch.int16), built.v_pool.view(torch.int16))
+    assert got.dtype == out_dtype and got.shape == (64, 12, 64)
+    if out_dtype == torch.float32:
+        np.testing.assert_allclose(got.cpu().numpy(), want, rtol=0, atol=2e-3)
+    else:
+        assert bf16_close(got.float().cpu().numpy(), want)
+    again = step.fused()
+    assert np.array_equal(ref.raw_bits(got.cpu()), ref.raw_bits(again.cpu()))
+
+
+def test_config4_unfused_step():
+    """bench.py --unfused: the append launch, then the decode launch, give
+    the pools and outputs of the fused step."""
+    from moe_engine import workloads
+
+    print_case("config4 unfused step")
+    step = workloads.config4_step(out_dtype=torch.float32)
+    k_missing, v_missing = step.w.k_pool.clone(), step.w.v_pool.clone()
+    step.append()
+    got = step.attend().clone()
+    k_after, v_after = step.w.k_pool.clone(), step.w.v_pool.clone()
+    step.w.k_pool.copy_(k_missing)
+    step.w.v_pool.copy_(v_missing)
+    fused = step.fused()
+    assert torch.equal(step.w.k_pool.view(torch.int16), k_after.view(torch.int16))
+    assert torch.equal(step.w.v_pool.view(torch.int16), v_after.view(torch.int16))
+    np.testing.assert_allclose(got.cpu().numpy(), oracle_outputs(step.w), rtol=0, atol=2e-3)
+    assert torch.equal(got, fused)
+
+
+CONFIG5_CELLS = [
+    (batch, ctx, block_size, dtype)
+    for dtype in (torch.bfloat16, torch.float32)
+    for batch in (1, 8)
+    for ctx in (32768, 131072)
+    for block_size in (16, 32)
+]
+
+
 @pytest.mark.parametrize(
-    "batch,ctx,block_size,dtype",
-    [
-        (1, 32768, 16, torch.bfloat16),
-        (1, 32768, 32, torch.float32),
-        (1, 131072, 16, torch.float32),
-        (1, 131072, 32, torch.bfloat16),
-        (8, 32768, 16, torch.float32),
-        (8, 32768, 32, torch.bfloat16),
-        (8, 131072, 32, torch.bfloat16),
-    ],
+    "batch,ctx,block_size,dtype", CONFIG5_CELLS,
+    ids=[f"{'bf16' if d == torch.bfloat16 else 'f32'}-b{b}-c{c}-bs{bs}" for b, c, bs, d in CONFIG5_CELLS],
 )
 def test_config5_long_context_split(batch, ctx, block_size, dtype):
-    """long contexts with 1 % of keys x20, split-context
-    partitions merged by the reduce launch."""
+    """BASELINE config 5, every cell bench.py times (the same workload: seed 5,
+    1 % of keys x20): split-context partitions merged by the reduce launch,
+    every sequence against the float64 oracle, through the call bench.py
+    makes (host lengths, output in the input dtype) and a float32-output
+    launch sized from max_context_len."""
     print_case("config5", batch, ctx, block_size, dtype)
     w = make_workload([ctx] * batch, block_size=block_size, dtype=dtype, seed=5, heavy_fraction=0.01)
     part, ws = _native.decode_plan(batch, 12, 64, block_size, ctx, dtype, 0)
     assert ws > 0 and part < ctx, "long contexts must take the split path"
     atol = 1e-5 if dtype == torch.float32 else 2e-3
-    batches = [0, batch - 1] if batch > 1 else None
-    check_workload(w, out_f32_atol=atol, batches=batches)
+    check_workload(w, out_f32_atol=atol)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
