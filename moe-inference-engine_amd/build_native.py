@@ -2,15 +2,18 @@
 
     python moe-inference-engine_amd/build_native.py
 
-compiles csrc/*.hip with hipcc into moe_engine/libmie_paged.so.  The library
-is written to a temporary name first and renamed, so a process that already
-mapped the old file keeps a consistent copy.
+compiles each csrc/*.hip with hipcc (in parallel, one object per source) and
+links the objects into moe_engine/libmie_paged.so.  The library is written to
+a temporary name first and renamed, so a process that already mapped the old
+file keeps a consistent copy.
 """
 
 import os
 import shlex
 import subprocess
 import sys
+import tempfile
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent
@@ -26,10 +29,10 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    "-shared",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
+NOISE = "is not a recognized feature for this target"
 
 
 def hipcc() -> str:
@@ -37,20 +40,34 @@ def hipcc() -> str:
     return str(Path(rocm) / "bin" / "hipcc")
 
 
-def build(verbose: bool = True) -> Path:
-    sources = sorted(str(p) for p in CSRC.glob("*.hip"))
-    tmp = OUTPUT.with_name(OUTPUT.name + f".tmp{os.getpid()}")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *sources, "-o", str(tmp)]
+def _run(cmd, verbose):
     if verbose:
         print("+", " ".join(shlex.quote(c) for c in cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    stderr = "\n".join(line for line in proc.stderr.splitlines() if noise not in line)
-    if proc.returncode != 0:
-        tmp.unlink(missing_ok=True)
-        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{stderr}")
-    if stderr.strip() and verbose:
-        print(stderr, file=sys.stderr)
+    stderr = "\n".join(line for line in proc.stderr.splitlines() if NOISE not in line)
+    return proc.returncode, stderr
+
+
+def build(verbose: bool = True) -> Path:
+    sources = sorted(CSRC.glob("*.hip"))
+    tmp = OUTPUT.with_name(OUTPUT.name + f".tmp{os.getpid()}")
+    jobs = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with tempfile.TemporaryDirectory(prefix="mie_build_") as objdir:
+        objs = [str(Path(objdir) / (src.stem + ".o")) for src in sources]
+        compiles = [[hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", obj]
+                    for src, obj in zip(sources, objs)]
+        with ThreadPoolExecutor(jobs) as pool:
+            results = list(pool.map(lambda c: _run(c, verbose), compiles))
+        failed = [(c[-3], rc, err) for c, (rc, err) in zip(compiles, results) if rc != 0]
+        if failed:
+            raise RuntimeError("hipcc failed:\n" + "\n".join(f"{src} ({rc}):\n{err}" for src, rc, err in failed))
+        for _, err in results:
+            if err.strip() and verbose:
+                print(err, file=sys.stderr)
+        rc, err = _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
+        if rc != 0:
+            tmp.unlink(missing_ok=True)
+            raise RuntimeError(f"hipcc link failed ({rc}):\n{err}")
     os.replace(tmp, OUTPUT)
     return OUTPUT
 
