@@ -205,8 +205,10 @@ def test_config4_timed_step(out_dtype):
 
 
 def test_config4_unfused_step():
-    """bench.py --unfused: the append launch, then the decode launch, give
-    the pools and outputs of the fused step."""
+    """bench.py --unfused: the append launch, then the decode launch, leave
+    the pools the fused step leaves, and both outputs are the oracle's (the
+    fused launch scores the new token from registers, so the two may differ
+    in the last bits)."""
     from moe_engine import workloads
 
     print_case("config4 unfused step")
@@ -220,8 +222,9 @@ def test_config4_unfused_step():
     fused = step.fused()
     assert torch.equal(step.w.k_pool.view(torch.int16), k_after.view(torch.int16))
     assert torch.equal(step.w.v_pool.view(torch.int16), v_after.view(torch.int16))
-    np.testing.assert_allclose(got.cpu().numpy(), oracle_outputs(step.w), rtol=0, atol=2e-3)
-    assert torch.equal(got, fused)
+    want = oracle_outputs(step.w)
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=0, atol=2e-3)
+    np.testing.assert_allclose(fused.cpu().numpy(), want, rtol=0, atol=2e-3)
 
 
 CONFIG5_CELLS = [
