@@ -77,7 +77,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 10
+#define MIE_ABI_VERSION 11
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -364,6 +364,37 @@ int64_t mie_lm_head_workspace(int32_t vocab);
 int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* weight,
                     const void* bias, int32_t vocab, int32_t dim, void* logits, void* token_out, void* workspace,
                     int64_t workspace_bytes, int32_t* advance, int32_t n_advance, int32_t dtype, void* stream);
+
+/*
+ * mie_paged_decode without the workspace arguments: an entry point that
+ * allocates nothing, neither inside the library nor through the caller.  It
+ * has no counterpart in the reference.  It is for callers that cannot call
+ * hipMalloc or take memory from an allocator: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation.
+ *
+ * The split-context workspace is a device array inside the library of
+ * MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE bytes, one per GPU, held until the
+ * process ends.  A decode whose plan needs more (mie_paged_decode_plan's
+ * workspace_bytes) fails with MIE_ERR_WORKSPACE before anything is launched.
+ * The first call on a device looks the array's address up
+ * (hipGetSymbolAddress) with that device current, so make it outside graph
+ * capture.  Every call on one GPU shares that GPU's array: calls that can
+ * overlap on one GPU (different streams, no ordering between them) race and
+ * must be serialised by the caller.  Nothing in the array needs clearing; each
+ * call writes every partial it reads.  Arguments, results and kernels are
+ * those of mie_paged_decode.
+ */
+#define MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE ((int64_t)16 << 20)
+int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                 const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                                 int64_t pool_stride_head, int32_t num_blocks,
+                                 const int32_t* block_tables, int64_t block_table_stride,
+                                 const int32_t* ctx_lens, const int32_t* ctx_lens_host,
+                                 int32_t ctx_len, int32_t max_ctx_len, int32_t batch,
+                                 int32_t num_heads, int32_t head_dim, int32_t block_size,
+                                 float scale, void* out, int64_t out_stride_b, int64_t out_stride_h,
+                                 int32_t out_dtype, int32_t partition_tokens, int32_t dtype,
+                                 void* stream);
 
 /*
  * One decoder block for ONE decode token (TransformerMoEBlock.forward,

@@ -45,6 +45,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 
 #include "mie_common.h"
 
@@ -1094,4 +1095,82 @@ extern "C" int32_t mie_paged_decode_append(const void* q, int64_t q_stride_b, in
                      block_tables, block_table_stride, ctx_lens, ctx_lens_host, ctx_len, max_ctx_len, batch,
                      num_heads, head_dim, block_size, scale, out, out_stride_b, out_stride_h, out_dtype, workspace,
                      workspace_bytes, partition_tokens, k_new, v_new, new_stride_b, new_stride_h, dtype, stream);
+}
+
+// ---- the allocation-free variant ---------------------------------------------
+
+// Split-context workspace of mie_paged_decode_noalloc: one copy per GPU the
+// library runs on, held until the process ends.  In host code `scratch` is a
+// stand-in for the symbol, not a device address; kernels get the address that
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices];  // per device, resolved on its first call
+
+// The scratch array's device address on the device `stream` belongs to (the
+// current device for the null stream), resolved once per device with that
+// device current.
+int32_t scratch_address(hipStream_t stream, void** out) {
+  int current = -1;
+  hipError_t e = hipGetDevice(&current);
+  if (e != hipSuccess) return mie::fail(MIE_ERR_LAUNCH, "mie_paged_decode_noalloc: hipGetDevice: %s",
+                                        hipGetErrorString(e));
+  int dev = current;
+  if (stream) {
+    hipDevice_t sd = 0;
+    e = hipStreamGetDevice(stream, &sd);
+    if (e != hipSuccess)
+      return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    dev = static_cast<int>(sd);
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_noalloc: device %d beyond the %d supported", dev,
+                     kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != current && (e = hipSetDevice(dev)) != hipSuccess)
+      return mie::fail(MIE_ERR_LAUNCH, "mie_paged_decode_noalloc: hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != current) (void)hipSetDevice(current);
+    if (e != hipSuccess || !ptr)
+      return mie::fail(MIE_ERR_LAUNCH, "mie_paged_decode_noalloc: hipGetSymbolAddress(scratch) on device %d: %s",
+                       dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MIE_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                            const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                                            int64_t pool_stride_head, int32_t num_blocks,
+                                            const int32_t* block_tables, int64_t block_table_stride,
+                                            const int32_t* ctx_lens, const int32_t* ctx_lens_host, int32_t ctx_len,
+                                            int32_t max_ctx_len, int32_t batch, int32_t num_heads,
+                                            int32_t head_dim, int32_t block_size, float scale, void* out,
+                                            int64_t out_stride_b, int64_t out_stride_h, int32_t out_dtype,
+                                            int32_t partition_tokens, int32_t dtype, void* stream) {
+  Plan p;
+  int32_t rc = plan(batch, num_heads, head_dim, block_size, max_ctx_len, dtype, partition_tokens, &p);
+  if (rc != MIE_OK) return rc;
+  if (p.ws_bytes > MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE)
+    return mie::fail(MIE_ERR_WORKSPACE,
+                     "mie_paged_decode_noalloc: this decode needs a %lld-byte split workspace, above the "
+                     "%lld bytes of the library's scratch; call mie_paged_decode with a workspace",
+                     static_cast<long long>(p.ws_bytes),
+                     static_cast<long long>(MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE));
+  void* ws = nullptr;
+  rc = scratch_address(static_cast<hipStream_t>(stream), &ws);
+  if (rc != MIE_OK) return rc;
+  return decode_impl(q, q_stride_b, q_stride_h, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks,
+                     block_tables, block_table_stride, ctx_lens, ctx_lens_host, ctx_len, max_ctx_len, batch,
+                     num_heads, head_dim, block_size, scale, out, out_stride_b, out_stride_h, out_dtype, ws,
+                     MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE, partition_tokens, nullptr, nullptr, 0, 0, dtype, stream);
 }

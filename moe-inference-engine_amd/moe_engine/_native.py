@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -78,6 +78,18 @@ _SIGNATURES = {
          _c_void_p, _i64, _i64, _i32,  # out, strides b/h, out dtype
          _c_void_p, _i64, _i32,  # workspace, bytes, partition_tokens
          _c_void_p, _c_void_p, _i64, _i64,  # new K/V rows, strides b/h
+         _i32, _c_void_p],  # dtype, stream
+    ),
+    "mie_paged_decode_noalloc": (
+        _i32,
+        [_c_void_p, _i64, _i64,  # q, strides b/h
+         _c_void_p, _c_void_p, _i64, _i64, _i32,  # pools, strides, num_blocks
+         _c_void_p, _i64,  # block tables, stride
+         _c_void_p, _c_void_p, _i32, _i32,  # ctx_lens (device), ctx_lens (host), ctx_len, max_ctx_len
+         _i32, _i32, _i32, _i32,  # batch, heads, head_dim, block_size
+         _f32,  # scale
+         _c_void_p, _i64, _i64, _i32,  # out, strides b/h, out dtype
+         _i32,  # partition_tokens
          _i32, _c_void_p],  # dtype, stream
     ),
     "mie_paged_decode_plan": (
