@@ -15,11 +15,19 @@ on the CPU the reference's paged path is gather + SDPA), and writes small
 JSON fixtures next to this file.  Only data is written: digests, token ids,
 logits slices and per-step logits checksums.
 
-Configs: the reference's TINY test model (tests/test_parity.py:11) and the
+Configs: the reference's TINY test model (tests/test_parity.py:11), and the
 BASELINE config 1 shape (12 layers, d 768, 12 heads x 64, top-2 of 8, vocab
-50257) at the reference's fixed expert width 4 * d = 3072 (model.py:489); the
-FFN-2048 variant is not expressible by the reference.
+50257) at two expert widths: the reference's fixed 4 * d = 3072
+(model.py:487-489) and config 1's 2048.  The reference's MoEFeedForward takes
+its width as an argument (model.py:288); only TransformerMoEBlock passes
+4 * d.  For the 2048 fixture this script hands TransformerMoEBlock a
+MoEFeedForward built at width 2048 (the module-level name is swapped for the
+duration of the construction), so every module is still the reference's own
+and consumes the RNG in the reference's order.  The fixture's "config" is
+this engine's ModelConfig, which names the width (ffn_dim).
 """
+
+import contextlib
 
 import hashlib
 import json
@@ -34,9 +42,27 @@ def digest(t):
     return hashlib.sha256(t.detach().contiguous().cpu().numpy().tobytes()).hexdigest()
 
 
-def run_case(name, cfg_kwargs, prompt_len, new_tokens, block_size, torch, Model, ModelConfig):
+@contextlib.contextmanager
+def expert_width(ffn_dim):
+    """Within the block, TransformerMoEBlock builds its MoEFeedForward at
+    width ffn_dim instead of 4 * hidden_dim (None: unchanged)."""
+    ref_model = sys.modules["moe_engine.model"]
+    original = ref_model.MoEFeedForward
+    if ffn_dim is not None:
+        ref_model.MoEFeedForward = lambda dim, hidden, experts, top_k, **kw: original(dim, ffn_dim, experts, top_k, **kw)
+    try:
+        yield
+    finally:
+        ref_model.MoEFeedForward = original
+
+
+def run_case(name, cfg_kwargs, prompt_len, new_tokens, block_size, torch, Model, ModelConfig, ffn_dim=None):
     torch.manual_seed(0)
-    model = Model(ModelConfig(**cfg_kwargs)).eval()
+    with expert_width(ffn_dim):
+        model = Model(ModelConfig(**cfg_kwargs)).eval()
+    if ffn_dim is not None:
+        assert all(b.moe.hidden_dim == ffn_dim and b.moe.experts[0].net[0].out_features == ffn_dim
+                   for b in model.MoEBlocks)
     state = {k: digest(v) for k, v in model.state_dict().items()}
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, cfg_kwargs["vocab_size"], (prompt_len,), generator=gen)
@@ -57,7 +83,7 @@ def run_case(name, cfg_kwargs, prompt_len, new_tokens, block_size, torch, Model,
             steps.append(model(seq[:, t : t + 1], cache)[0, -1])
     logits = torch.stack(steps).double()
     fixture = {
-        "config": cfg_kwargs,
+        "config": cfg_kwargs if ffn_dim is None else dict(cfg_kwargs, ffn_dim=ffn_dim),
         "seed": 0,
         "prompt_generator_seed": 0,
         "prompt": prompt.tolist(),
@@ -88,6 +114,7 @@ def main():
     e2e = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
                num_experts=8, top_k=2)
     run_case("config1_ffn3072", e2e, 32, 64, 16, torch, Model, ModelConfig)
+    run_case("config1", e2e, 32, 64, 16, torch, Model, ModelConfig, ffn_dim=2048)
 
 
 if __name__ == "__main__":

@@ -1,7 +1,9 @@
 """The engine against golden vectors written by the reference engine itself.
 
 tests/golden/make_reference_golden.py ran the reference's Model on the CPU
-(seed-0 random init, greedy decode, contiguous and paged caches) and stored
+(seed-0 random init, greedy decode, contiguous and paged caches; the TINY
+test model and BASELINE config 1's shape at expert widths 3072 and 2048,
+config 1's own) and stored
 per-tensor SHA-256 digests of the state dict, the token ids and logits
 slices.  Here the same construction and decode run through this engine on the
 CPU: the weights must be bit-identical (the random-init order is the
@@ -55,7 +57,10 @@ def check_logits(logits, fixture, atol):
     np.testing.assert_allclose(logits.sum(dim=1).numpy(), fixture["logits_sum"], rtol=0, atol=sum_atol)
 
 
-@pytest.mark.parametrize("name", ["tiny", "config1_ffn3072"])
+FIXTURES = ["tiny", "config1_ffn3072", "config1"]
+
+
+@pytest.mark.parametrize("name", FIXTURES)
 def test_seed0_weights_are_the_reference_weights(name):
     fixture = load(name)
     model = build(fixture)
@@ -65,7 +70,18 @@ def test_seed0_weights_are_the_reference_weights(name):
     assert not mismatched, f"{len(mismatched)} tensors differ, first {mismatched[:3]}"
 
 
-@pytest.mark.parametrize("name", ["tiny", "config1_ffn3072"])
+def test_config1_fixture_is_baseline_config1():
+    """reference_config1.json is BASELINE config 1 itself: FFN 2048, 32-token
+    prompt, 64 greedy tokens, block 16."""
+    fixture = load("config1")
+    cfg = fixture["config"]
+    assert (cfg["num_layers"], cfg["hidden_dim"], cfg["num_heads"], cfg["num_experts"], cfg["top_k"],
+            cfg["ffn_dim"], cfg["vocab_size"]) == (12, 768, 12, 8, 2, 2048, 50257)
+    assert (len(fixture["prompt"]), fixture["new_tokens"], fixture["block_size"]) == (32, 64, 16)
+    assert any(k.endswith("experts.0.net.0.weight") for k in fixture["state_dict_sha256"])
+
+
+@pytest.mark.parametrize("name", FIXTURES)
 def test_cpu_greedy_tokens_and_logits_match_reference(name):
     fixture = load(name)
     model = build(fixture)

@@ -1,33 +1,68 @@
-"""Greedy decode on the GPU through the paged-direct path against the
-reference engine's CPU tokens (tests/golden/reference_*.json).
+"""Greedy decode on the GPU against the reference engine's CPU tokens and
+logits (tests/golden/reference_*.json), through every GPU decode path: the
+paged cache with the direct HIP decode, with the HIP gather + SDPA, and the
+whole decode step replayed from a HIP graph (moe_engine.graphs).
 
 Tokens must be identical.  Logits differ from the reference CPU run only by
-GPU GEMM rounding (hipBLASLt vs the CPU BLAS); they are checked within a bound
-far below the logit scale (|logit| ~ 28 at d 768), with identical argmax.
+GPU rounding (hipBLASLt and the HIP GEMVs against the CPU BLAS); they are
+checked within a bound far below the logit scale (|logit| ~ 28 at d 768),
+with identical argmax at every step.
 """
 
 import pytest
 import torch
 
 from conftest import print_case
-from test_golden import build, check_logits, load, step_logits
+from moe_engine.graphs import GraphedDecoder, generate_graphed
+from test_golden import FIXTURES, build, check_logits, load, step_logits
 
 pytestmark = pytest.mark.gpu
 
+ATOL = {"tiny": 1e-4, "config1_ffn3072": 2e-2, "config1": 2e-2}
 
-@pytest.mark.parametrize("name,atol", [("tiny", 1e-4), ("config1_ffn3072", 2e-2)])
+
+def paged_cache(model, fixture, mode):
+    bs = fixture["block_size"]
+    return model.new_block_allocator(-(-model.max_seq_length // bs), bs, attention_mode=mode).new_cache()
+
+
+@pytest.mark.parametrize("name", FIXTURES)
 @pytest.mark.parametrize("mode", ["direct", "gather"])
-def test_gpu_paged_tokens_match_reference_cpu(name, atol, mode):
+def test_gpu_paged_tokens_match_reference_cpu(name, mode):
     print_case("golden", name, mode)
     fixture = load(name)
     model = build(fixture).to("cuda")
     prompt = torch.tensor(fixture["prompt"], device="cuda")
-    bs = fixture["block_size"]
-    allocator = model.new_block_allocator(-(-model.max_seq_length // bs), bs, attention_mode=mode)
-    cache = allocator.new_cache()
+    cache = paged_cache(model, fixture, mode)
     tokens = model.generate(prompt, fixture["new_tokens"], temperature=0, cache=cache)[0].tolist()
     cache.free()
     assert tokens == fixture["tokens"]["paged_gather"]
-    cache = allocator.new_cache()
-    check_logits(step_logits(model, fixture["tokens"]["contiguous"], len(prompt), cache), fixture, atol)
+    check_logits(step_logits(model, fixture["tokens"]["contiguous"], len(prompt), cache), fixture, ATOL[name])
+    cache.free()
+
+
+@pytest.mark.parametrize("name", FIXTURES)
+def test_gpu_graphed_decode_matches_reference_cpu(name):
+    """generate_graphed's tokens, and the logits every replayed step leaves,
+    against the reference's: the graph is checked against the reference
+    itself, not only against the eager HIP path."""
+    print_case("golden graph", name)
+    fixture = load(name)
+    model = build(fixture).to("cuda")
+    prompt = torch.tensor(fixture["prompt"], device="cuda")
+    want = fixture["tokens"]["paged_gather"]
+    cache = paged_cache(model, fixture, "direct")
+    assert generate_graphed(model, prompt, fixture["new_tokens"], cache)[0].tolist() == want
+    cache.free()
+    with torch.no_grad():
+        rows = [model(prompt[None], cache)[0, -1]]
+        decoder = GraphedDecoder(model, cache)
+        decoder.prime(rows[0].argmax().reshape(1, 1))
+        picks = []
+        for _ in range(len(prompt), len(want) - 1):
+            picks.append(int(decoder.step()))
+            rows.append(decoder.logits[0].clone())
+    assert decoder.replays == len(want) - len(prompt) - 2  # the first step runs eagerly, then captures
+    assert picks == want[len(prompt) + 1:]
+    check_logits(torch.stack(rows).double().cpu(), fixture, ATOL[name])
     cache.free()
