@@ -419,6 +419,14 @@ int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_st
  * initialises the plan again with a larger workspace.  The plan holds
  * pointers only: the caller keeps every buffer alive while the plan is used,
  * and one plan serves calls in stream order.
+ *
+ * mie_block_plan_init makes every host check of the five launches (built
+ * width, head_dim and dtype - the MoE half is float32 only -, shapes,
+ * strides, alignment, null pointers) and fails with their status, so an
+ * initialised plan never stops between launches.  The decode reads at most
+ * block_table_len table entries (block_table_len >= 1).  mie_block_decode
+ * checks x (non-NULL, 16-byte aligned) and rejects a position at or past
+ * block_table_len * block_size, both before launching.
  */
 int64_t mie_block_plan_bytes(void);
 int32_t mie_block_plan_init(void* plan, int64_t plan_bytes, int32_t dim, int32_t num_heads, int32_t head_dim,

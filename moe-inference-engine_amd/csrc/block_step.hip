@@ -11,7 +11,8 @@
 // in caller-owned host memory, and each token is one call with the input row,
 // the position and the stream.  The launches and their arguments are exactly
 // those of the five entry points, so the results are bit-identical to calling
-// them in turn.
+// them in turn.  mie_block_plan_init makes every host check those entry points
+// make, so a call that passes its own checks launches all five.
 #include <string.h>
 
 #include "mie_common.h"
@@ -66,6 +67,24 @@ extern "C" int32_t mie_block_plan_init(
                      num_heads, head_dim, block_size);
   if (!q || !attn || !h || !out)
     return mie::fail(MIE_ERR_INVALID, "mie_block_plan_init: null scratch or output row");
+  if (block_table_len <= 0)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_plan_init: block table of %d entries", block_table_len);
+  // Every check the five launches would make, made now, so that a plan that
+  // initialises never fails half-way through a block.  x is the per-call
+  // input: a stand-in that passes the checks here, checked in mie_block_decode.
+  const void* x_stand_in = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+  int32_t rc = mie::qkv_append_check(x_stand_in, attn_ln_weight, attn_ln_bias, w_in, dim, k_pool, v_pool,
+                                     pool_stride_block, pool_stride_head, num_blocks, block_table, block_table_len,
+                                     nullptr, 0, q, num_heads, head_dim, block_size, dtype);
+  if (rc != MIE_OK) return rc;
+  rc = mie::paged_decode_check(q, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, block_table,
+                               num_heads, head_dim, block_size, attn, dtype);
+  if (rc != MIE_OK) return rc;
+  rc = mie::linear_residual_check(attn, w_out, h, dim, dim, dtype);
+  if (rc != MIE_OK) return rc;
+  rc = mie::moe_decode_block_check(h, moe_ln_weight, moe_ln_bias, router_weight, w1, b1, w2, b2, num_experts, top_k,
+                                   dim, hidden, router_logits, expert_ids, route_weights, hidden_act, out, dtype);
+  if (rc != MIE_OK) return rc;
   BlockPlan p{};
   p.magic = kPlanMagic;
   p.dtype = dtype;
@@ -118,7 +137,11 @@ extern "C" int32_t mie_block_decode(const void* plan, const void* x, int32_t pos
   BlockPlan p;
   memcpy(&p, plan, sizeof(p));
   if (p.magic != kPlanMagic) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: plan not initialised");
-  if (!x || position < 0) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: x %p position %d", x, position);
+  if (!x || reinterpret_cast<uintptr_t>(x) % 16 != 0 || position < 0)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_decode: x %p (16-byte aligned) position %d", x, position);
+  if (static_cast<int64_t>(position) >= static_cast<int64_t>(p.block_table_len) * p.block_size)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_decode: position %d lies past the %d-entry block table", position,
+                     p.block_table_len);
   // The decode's split-context workspace is checked before anything is
   // launched, so a call that cannot finish changes nothing.
   const int32_t ctx = position + 1;
@@ -134,9 +157,9 @@ extern "C" int32_t mie_block_decode(const void* plan, const void* x, int32_t pos
   if (rc != MIE_OK) return rc;
   const int64_t row = static_cast<int64_t>(p.num_heads) * p.head_dim;
   rc = mie_paged_decode(p.q, row, p.head_dim, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head,
-                        p.num_blocks, p.block_table, 0, nullptr, nullptr, ctx, ctx, 1, p.num_heads, p.head_dim,
-                        p.block_size, p.scale, p.attn, row, p.head_dim, p.dtype, ws_need ? p.workspace : nullptr,
-                        ws_need, 0, p.dtype, stream);
+                        p.num_blocks, p.block_table, p.block_table_len, nullptr, nullptr, ctx, ctx, 1, p.num_heads,
+                        p.head_dim, p.block_size, p.scale, p.attn, row, p.head_dim, p.dtype,
+                        ws_need ? p.workspace : nullptr, ws_need, 0, p.dtype, stream);
   if (rc != MIE_OK) return rc;
   rc = mie_linear_residual(p.attn, p.w_out, p.b_out, x, p.h, p.dim, p.dim, p.dtype, stream);
   if (rc != MIE_OK) return rc;

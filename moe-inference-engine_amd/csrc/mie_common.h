@@ -152,3 +152,26 @@ namespace mie {
 int32_t launch_argmax_pairs(const ArgmaxPair* pairs, int32_t n, int32_t limit, int64_t* out, int32_t* advance,
                             int32_t n_advance, hipStream_t stream);
 }  // namespace mie
+
+namespace mie {
+// Host-only argument checks of the entry points mie_block_plan_init stores a
+// plan for: each returns what its entry point would return for these
+// arguments before launching anything (MIE_OK when it would launch).
+// paged_decode_check checks one sequence of one token (batch 1, ctx 1); the
+// split workspace is checked per call.
+int32_t qkv_append_check(const void* x, const void* ln_weight, const void* ln_bias, const void* w_in, int32_t dim,
+                         const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_head,
+                         int32_t num_blocks, const int32_t* block_table, int32_t block_table_len,
+                         const int32_t* position_dev, int32_t position, const void* q_out, int32_t num_heads,
+                         int32_t head_dim, int32_t block_size, int32_t dtype);
+int32_t linear_residual_check(const void* x, const void* weight, const void* out, int32_t rows, int32_t cols,
+                              int32_t dtype);
+int32_t paged_decode_check(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                           int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                           int32_t num_heads, int32_t head_dim, int32_t block_size, void* out, int32_t dtype);
+int32_t moe_decode_block_check(const void* x, const void* ln_weight, const void* ln_bias, const void* router_weight,
+                               const void* w1, const void* b1, const void* w2, const void* b2, int32_t num_experts,
+                               int32_t top_k, int32_t dim, int32_t hidden, const void* router_logits,
+                               const void* expert_ids, const void* route_weights, const void* hidden_act,
+                               const void* out, int32_t dtype);
+}  // namespace mie

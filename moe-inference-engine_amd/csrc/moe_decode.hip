@@ -512,17 +512,33 @@ extern "C" int32_t mie_moe_decode(const void* x, const void* router_weight, cons
   return launch_experts(a, static_cast<hipStream_t>(stream));
 }
 
-extern "C" int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
-                                        const void* router_weight, const void* w1, const void* b1, const void* w2,
-                                        const void* b2, int32_t num_experts, int32_t top_k, int32_t dim,
-                                        int32_t hidden, void* router_logits, void* expert_ids, void* route_weights,
-                                        void* hidden_act, void* out, int32_t dtype, void* stream) {
+namespace mie {
+
+int32_t moe_decode_block_check(const void* x, const void* ln_weight, const void* ln_bias, const void* router_weight,
+                               const void* w1, const void* b1, const void* w2, const void* b2, int32_t num_experts,
+                               int32_t top_k, int32_t dim, int32_t hidden, const void* router_logits,
+                               const void* expert_ids, const void* route_weights, const void* hidden_act,
+                               const void* out, int32_t dtype) {
   int32_t rc = check_route_args("mie_moe_decode_block", x, router_weight, num_experts, top_k, dim, router_logits,
                                 expert_ids, route_weights, dtype);
   if (rc != MIE_OK) return rc;
   rc = check_expert_args("mie_moe_decode_block", hidden, dim, w1, b1, w2, b2, hidden_act, out);
   if (rc != MIE_OK) return rc;
   if (!ln_weight && ln_bias) return mie::fail(MIE_ERR_INVALID, "mie_moe_decode_block: a norm bias needs a weight");
+  return MIE_OK;
+}
+
+}  // namespace mie
+
+extern "C" int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+                                        const void* router_weight, const void* w1, const void* b1, const void* w2,
+                                        const void* b2, int32_t num_experts, int32_t top_k, int32_t dim,
+                                        int32_t hidden, void* router_logits, void* expert_ids, void* route_weights,
+                                        void* hidden_act, void* out, int32_t dtype, void* stream) {
+  const int32_t rc = mie::moe_decode_block_check(x, ln_weight, ln_bias, router_weight, w1, b1, w2, b2, num_experts,
+                                                 top_k, dim, hidden, router_logits, expert_ids, route_weights,
+                                                 hidden_act, out, dtype);
+  if (rc != MIE_OK) return rc;
   MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids, route_weights);
   a.ln_w = static_cast<const float*>(ln_weight);
   a.ln_b = static_cast<const float*>(ln_bias);

@@ -929,7 +929,8 @@ int32_t decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
                     int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, void* out,
                     int64_t out_stride_b, int64_t out_stride_h, int32_t out_dtype, void* workspace,
                     int64_t workspace_bytes, int32_t partition_tokens, const void* k_new, const void* v_new,
-                    int64_t new_stride_b, int64_t new_stride_h, int32_t dtype, void* stream) {
+                    int64_t new_stride_b, int64_t new_stride_h, int32_t dtype, void* stream,
+                    bool check_only = false) {
   Plan p;
   int32_t rc = plan(batch, num_heads, head_dim, block_size, max_ctx_len, dtype, partition_tokens, &p);
   if (rc != MIE_OK) return rc;
@@ -973,6 +974,7 @@ int32_t decode_impl(const void* q, int64_t q_stride_b, int64_t q_stride_h, const
     return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_append: misaligned new rows");
   if (k_new && !ctx_lens && ctx_len < 1)
     return mie::fail(MIE_ERR_INVALID, "mie_paged_decode_append: ctx_len %d leaves no slot for the new token", ctx_len);
+  if (check_only) return MIE_OK;
 
   DecodeArgs a{};
   a.q = static_cast<const char*>(q);
@@ -1096,6 +1098,19 @@ extern "C" int32_t mie_paged_decode_append(const void* q, int64_t q_stride_b, in
                      num_heads, head_dim, block_size, scale, out, out_stride_b, out_stride_h, out_dtype, workspace,
                      workspace_bytes, partition_tokens, k_new, v_new, new_stride_b, new_stride_h, dtype, stream);
 }
+
+namespace mie {
+
+int32_t paged_decode_check(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                           int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                           int32_t num_heads, int32_t head_dim, int32_t block_size, void* out, int32_t dtype) {
+  const int64_t row = static_cast<int64_t>(num_heads) * head_dim;
+  return decode_impl(q, row, head_dim, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, block_table,
+                     0, nullptr, nullptr, 1, 1, 1, num_heads, head_dim, block_size, 1.0f, out, row, head_dim, dtype,
+                     nullptr, 0, 0, nullptr, nullptr, 0, 0, dtype, nullptr, /*check_only=*/true);
+}
+
+}  // namespace mie
 
 // ---- the allocation-free variant ---------------------------------------------
 

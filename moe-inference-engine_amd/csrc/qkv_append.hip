@@ -358,12 +358,13 @@ extern "C" int32_t mie_qkv_append_supported(int32_t dim, int32_t dtype) {
   return 0;
 }
 
-extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
-                                  const void* w_in, const void* b_in, int32_t dim, void* k_pool, void* v_pool,
-                                  int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
-                                  const int32_t* block_table, int32_t block_table_len, const int32_t* position_dev,
-                                  int32_t position, void* q_out, int32_t num_heads, int32_t head_dim,
-                                  int32_t block_size, int32_t dtype, void* stream) {
+namespace mie {
+
+int32_t qkv_append_check(const void* x, const void* ln_weight, const void* ln_bias, const void* w_in, int32_t dim,
+                         const void* k_pool, const void* v_pool, int64_t pool_stride_block, int64_t pool_stride_head,
+                         int32_t num_blocks, const int32_t* block_table, int32_t block_table_len,
+                         const int32_t* position_dev, int32_t position, const void* q_out, int32_t num_heads,
+                         int32_t head_dim, int32_t block_size, int32_t dtype) {
   if (!mie_qkv_append_supported(dim, dtype))
     return mie::fail(MIE_ERR_UNSUPPORTED, "mie_qkv_append: dim %d with dtype %d is not built", dim, dtype);
   if (num_heads <= 0 || head_dim <= 0 || num_heads * head_dim != dim)
@@ -382,6 +383,32 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
     return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: pool strides (%lld, %lld) overlap",
                      static_cast<long long>(pool_stride_block), static_cast<long long>(pool_stride_head));
   if (!position_dev && position < 0) return mie::fail(MIE_ERR_INVALID, "mie_qkv_append: position %d", position);
+  return MIE_OK;
+}
+
+int32_t linear_residual_check(const void* x, const void* weight, const void* out, int32_t rows, int32_t cols,
+                              int32_t dtype) {
+  if (!mie_qkv_append_supported(cols, dtype))
+    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_linear_residual: width %d with dtype %d is not built", cols, dtype);
+  if (rows <= 0) return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: rows %d", rows);
+  if (!x || !weight || !out) return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: null pointer");
+  if (!aligned16(weight) || !aligned16(x))
+    return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: x and the weight must be 16-byte aligned");
+  return MIE_OK;
+}
+
+}  // namespace mie
+
+extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+                                  const void* w_in, const void* b_in, int32_t dim, void* k_pool, void* v_pool,
+                                  int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                                  const int32_t* block_table, int32_t block_table_len, const int32_t* position_dev,
+                                  int32_t position, void* q_out, int32_t num_heads, int32_t head_dim,
+                                  int32_t block_size, int32_t dtype, void* stream) {
+  const int32_t rc = mie::qkv_append_check(x, ln_weight, ln_bias, w_in, dim, k_pool, v_pool, pool_stride_block,
+                                           pool_stride_head, num_blocks, block_table, block_table_len, position_dev,
+                                           position, q_out, num_heads, head_dim, block_size, dtype);
+  if (rc != MIE_OK) return rc;
   QkvArgs a{};
   a.rows = 3 * dim;
   a.x = x;
@@ -410,12 +437,8 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
 
 extern "C" int32_t mie_linear_residual(const void* x, const void* weight, const void* bias, const void* residual,
                                        void* out, int32_t rows, int32_t cols, int32_t dtype, void* stream) {
-  if (!mie_qkv_append_supported(cols, dtype))
-    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_linear_residual: width %d with dtype %d is not built", cols, dtype);
-  if (rows <= 0) return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: rows %d", rows);
-  if (!x || !weight || !out) return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: null pointer");
-  if (!aligned16(weight) || !aligned16(x))
-    return mie::fail(MIE_ERR_INVALID, "mie_linear_residual: x and the weight must be 16-byte aligned");
+  const int32_t rc = mie::linear_residual_check(x, weight, out, rows, cols, dtype);
+  if (rc != MIE_OK) return rc;
   QkvArgs a{};
   a.rows = rows;
   a.residual = residual;

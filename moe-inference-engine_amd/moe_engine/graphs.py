@@ -80,14 +80,14 @@ class GraphedDecoder:
         c.graph_partition_tokens = self.partition_tokens if on else 0
 
     def _forward_body(self):
-        """The captured step: embeddings and blocks (Model.hidden_states),
+        """The captured step: embeddings and blocks (Model._hidden_states),
         then mie_lm_head - final norm, LM head and greedy pick, which writes
         the token the next step reads and advances the device position and
         context length.  The pick's merge is one workgroup with nothing to
         clear (torch.argmax over a row this wide reduces across workgroups
         behind a memset, which a graph must not hold)."""
         model = self.model
-        x = model.hidden_states(self.token, self.cache)
+        x = model._hidden_states(self.token, self.cache)
         projection.lm_head(x[0, -1], model.final_norm, model.output_projection, out=self._logits,
                            token_out=self.token, workspace=self._head_ws, advance=self.counters)
         return self._logits

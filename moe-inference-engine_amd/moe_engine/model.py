@@ -26,6 +26,7 @@ a seeded model has the reference's weights.
 
 import ctypes
 import math
+import weakref
 from dataclasses import dataclass
 from typing import Optional
 
@@ -38,6 +39,51 @@ from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention, p
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
 MOE_MODES = ("auto", "direct", "reference")
+
+# A block's one-token launch plan (TransformerMoEBlock._decode_one_token) holds
+# raw device addresses of parameters, buffers and expert storages.  Every
+# operation that can put a new tensor in their place inside the modules below -
+# device / dtype conversion (_apply), assignment of a parameter, buffer or
+# submodule (which load_state_dict(assign=True) and the expert repacking go
+# through) - advances this epoch, and a plan built under an earlier epoch is
+# rebuilt before its next use.  Writing through .data or in place keeps the
+# addresses, so it needs nothing.
+_TENSOR_EPOCH = [0]
+
+
+def _tensors_replaced() -> None:
+    _TENSOR_EPOCH[0] += 1
+
+
+class _TracksReplacement:
+    """Mixin for the modules a launch plan reads from: conversion or
+    assignment of a tensor or submodule advances _TENSOR_EPOCH."""
+
+    def _apply(self, fn, recurse=True):
+        result = super()._apply(fn, recurse=recurse)
+        _tensors_replaced()
+        return result
+
+    def __setattr__(self, name, value):
+        super().__setattr__(name, value)
+        if isinstance(value, (torch.Tensor, nn.Module)):
+            _tensors_replaced()
+
+    def register_buffer(self, name, tensor, persistent=True):
+        super().register_buffer(name, tensor, persistent)
+        _tensors_replaced()
+
+    def register_parameter(self, name, param):
+        super().register_parameter(name, param)
+        _tensors_replaced()
+
+
+class Linear(_TracksReplacement, nn.Linear):
+    """nn.Linear whose tensor replacements invalidate launch plans."""
+
+
+class LayerNorm(_TracksReplacement, nn.LayerNorm):
+    """nn.LayerNorm whose tensor replacements invalidate launch plans."""
 
 
 @dataclass
@@ -301,7 +347,7 @@ class PagedKVCache:
         self._write_index_key = None
 
 
-class CachedAttention(nn.Module):
+class CachedAttention(_TracksReplacement, nn.Module):
     """Causal self-attention over an external cache (model.py:211-269)."""
 
     def __init__(self, dim: int, num_heads: int):
@@ -310,7 +356,7 @@ class CachedAttention(nn.Module):
         self.head_dim = dim // num_heads
         self.in_proj_weight = nn.Parameter(torch.empty(3 * dim, dim))
         self.in_proj_bias = nn.Parameter(torch.empty(3 * dim))
-        self.out_proj = nn.Linear(dim, dim)
+        self.out_proj = Linear(dim, dim)
         nn.init.xavier_uniform_(self.in_proj_weight)
         nn.init.zeros_(self.in_proj_bias)
 
@@ -398,16 +444,16 @@ class CachedAttention(nn.Module):
         return self.out_proj(out)
 
 
-class Expert(nn.Module):
+class Expert(_TracksReplacement, nn.Module):
     def __init__(self, dim, hidden_dim):
         super().__init__()
-        self.net = nn.Sequential(nn.Linear(dim, hidden_dim), nn.GELU(), nn.Linear(hidden_dim, dim))
+        self.net = nn.Sequential(Linear(dim, hidden_dim), nn.GELU(), Linear(hidden_dim, dim))
 
     def forward(self, x):
         return self.net(x)
 
 
-class MoEFeedForward(nn.Module):
+class MoEFeedForward(_TracksReplacement, nn.Module):
     """Top-k mixture of experts (model.py:285-481).
 
     Mode 'reference' runs the reference's PyTorch path (model.py:443-461)
@@ -438,7 +484,7 @@ class MoEFeedForward(nn.Module):
         self.top_k = top_k
         self.num_experts = num_experts
         self.experts = nn.ModuleList(Expert(dim, hidden_dim) for _ in range(num_experts))
-        self.router = nn.Linear(dim, num_experts, bias=False)
+        self.router = Linear(dim, num_experts, bias=False)
         # Fixed per-layer decode workspaces; non-persistent, so checkpoints and
         # state-dict keys are unchanged (model.py:301-321).
         for name, shape, dtype in (
@@ -640,16 +686,17 @@ class TransformerMoEBlock(nn.Module):
         super().__init__()
         self.attention = CachedAttention(config.hidden_dim, config.num_heads)
         self.moe = MoEFeedForward(config.hidden_dim, config.expert_hidden_dim, config.num_experts, config.top_k)
-        self.attn_norm = nn.LayerNorm(config.hidden_dim)
-        self.moe_norm = nn.LayerNorm(config.hidden_dim)
-        self._one_token = None  # (key, launcher or None): see _decode_one_token
+        self.attn_norm = LayerNorm(config.hidden_dim)
+        self.moe_norm = LayerNorm(config.hidden_dim)
+        self._one_token = None  # (key, cache weakref, launcher or None): see _decode_one_token
         self.register_load_state_dict_post_hook(TransformerMoEBlock._drop_plan_after_load)
 
     def drop_decode_plan(self) -> None:
         """Forget the one-token launch plan; the next decode token builds a
-        new one.  .to() / .float() / ... and load_state_dict call this
-        themselves; code that replaces a parameter of the block any other way
-        calls it too."""
+        new one.  Conversions (.to(), .float(), ...), loads and assignments of
+        tensors or submodules anywhere in the block invalidate the plan by
+        themselves (_TENSOR_EPOCH); code that swaps a tensor's storage some
+        other way (param.data = ...) calls this."""
         self._one_token = None
 
     @staticmethod
@@ -683,14 +730,14 @@ class TransformerMoEBlock(nn.Module):
 
     def _one_token_key(self, x, cache, layer_idx):
         """What a plan is built for besides the block's own tensors: the
-        cache (its pools, table and attention mode), the allocator's fuse_qkv
-        switch, the MoE mode, the norms' eps, and x's dtype, device and width.
-        The block's parameters and expert storage are covered by dropping the
-        plan whenever they can be replaced (_apply, load_state_dict,
-        drop_decode_plan), so each token compares this short key only."""
+        cache (by identity; the plan also keeps a weak reference to it), its
+        attention mode, the allocator's fuse_qkv switch, the MoE mode, the
+        norms' eps, x's dtype, device and width, and the tensor epoch, which
+        covers every replacement of a parameter, buffer or expert storage the
+        plan points at.  Each token compares this short key only."""
         m = self._modules
-        return (layer_idx, cache, cache.attention_mode, cache.allocator.fuse_qkv, m["moe"].mode,
-                m["attn_norm"].eps, m["moe_norm"].eps, x.dtype, x.device, x.shape[-1])
+        return (layer_idx, id(cache), cache.attention_mode, cache.allocator.fuse_qkv, m["moe"].mode,
+                m["attn_norm"].eps, m["moe_norm"].eps, x.dtype, x.device, x.shape[-1], _TENSOR_EPOCH[0])
 
     def _decode_one_token(self, x, cache, layer_idx, position):
         """The block for one eager decode token when both fused halves apply:
@@ -702,13 +749,16 @@ class TransformerMoEBlock(nn.Module):
             return None
         key = self._one_token_key(x, cache, layer_idx)
         plan = self._one_token
-        if plan is None or plan[0] != key:
+        # The weak reference rules out a new cache that reuses a dead one's id;
+        # the plan itself holds no reference to the cache or its pools, so a
+        # finished sequence's pools can be freed.
+        if plan is None or plan[0] != key or plan[1]() is not cache:
             launcher = None
             if self.attention.fused_decode_supported(x, self.attn_norm, cache) and self.moe.fused_block_supported(
                     x, self.moe_norm):
                 launcher = self._build_one_token(x, cache, layer_idx)
-            plan = self._one_token = (key, launcher)
-        return None if plan[1] is None else plan[1](x, cache, position)
+            plan = self._one_token = (key, weakref.ref(cache), launcher)
+        return None if plan[2] is None else plan[2](x, cache, position)
 
     def _build_one_token(self, x, cache, layer_idx):
         """A launch plan of the block's five launches (mie_block_plan_init):
@@ -722,6 +772,9 @@ class TransformerMoEBlock(nn.Module):
         dim = x.shape[-1]
         dtype, device = x.dtype, x.device
         off = layer_idx * layer_bytes
+        # Addresses only: the launcher must not keep the cache or its pools alive.
+        k_layer, v_layer = alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off
+        table = cache.block_table_device.data_ptr()
         an, mn = self.attn_norm, self.moe_norm
         s = moe._expert_storage
         out = moe._direct_out.view(1, 1, dim)
@@ -739,8 +792,7 @@ class TransformerMoEBlock(nn.Module):
                 plan, len(plan), dim, heads, head_dim, block_size, code,
                 ptr(an.weight), ptr(an.bias), float(an.eps), att.in_proj_weight.data_ptr(), ptr(att.in_proj_bias),
                 att.out_proj.weight.data_ptr(), ptr(att.out_proj.bias),
-                alloc.k_pool.data_ptr() + off, alloc.v_pool.data_ptr() + off, sblk, shead, num_blocks,
-                cache.block_table_device.data_ptr(), num_blocks, 1.0 / math.sqrt(head_dim),
+                k_layer, v_layer, sblk, shead, num_blocks, table, num_blocks, 1.0 / math.sqrt(head_dim),
                 q.data_ptr(), attn.data_ptr(), h.data_ptr(), ptr(ws), 0 if ws is None else ws.numel(),
                 ptr(mn.weight), ptr(mn.bias), float(mn.eps), moe.router.weight.data_ptr(),
                 s["w1"].data_ptr(), s["b1"].data_ptr(), s["w2"].data_ptr(), s["b2"].data_ptr(),
@@ -779,9 +831,9 @@ class Model(nn.Module):
         self.max_seq_length = config.max_seq_length
         self.token_embedding = nn.Embedding(config.vocab_size, config.hidden_dim)
         self.positional_embedding = nn.Embedding(config.max_seq_length, config.hidden_dim)
-        self.output_projection = nn.Linear(config.hidden_dim, config.vocab_size)
+        self.output_projection = Linear(config.hidden_dim, config.vocab_size)
         self.MoEBlocks = nn.ModuleList(TransformerMoEBlock(config) for _ in range(config.num_layers))
-        self.final_norm = nn.LayerNorm(config.hidden_dim)
+        self.final_norm = LayerNorm(config.hidden_dim)
         self.output_projection.weight = self.token_embedding.weight  # tied
 
     def new_cache(self, batch_size: int = 1) -> KVCache:
@@ -799,7 +851,7 @@ class Model(nn.Module):
         return BlockAllocator(self.config, num_blocks, block_size, weight.device, weight.dtype, attention_mode)
 
     def forward(self, token_ids, cache):
-        x = self.hidden_states(token_ids, cache)
+        x = self._hidden_states(token_ids, cache)
         if x.shape[0] == 1 and x.shape[1] == 1 and not torch.is_grad_enabled() and self._head_on_device(x):
             # One decode token at inference: final norm and LM head in one
             # launch (no autograd graph; with gradients on, the modules run).
@@ -813,7 +865,18 @@ class Model(nn.Module):
 
     def hidden_states(self, token_ids, cache):
         """The forward pass up to the final norm (model.py:543-562): the
-        embeddings and every block, advancing cache.position."""
+        embeddings and every block, advancing cache.position.  The result is
+        the caller's (as the reference's is), never a buffer a later step
+        overwrites."""
+        x = self._hidden_states(token_ids, cache)
+        if x.shape[:2] == (1, 1) and x.data_ptr() == self.MoEBlocks[-1].moe._direct_out.data_ptr():
+            x = x.clone()  # one-token decode leaves the last block's output in its MoE buffer
+        return x
+
+    def _hidden_states(self, token_ids, cache):
+        """hidden_states without the copy: for one decode token the result
+        may be the last block's MoE output buffer, which the next token
+        overwrites (Model.forward and the captured step consume it at once)."""
         batch, seq_len = token_ids.shape
         position = cache.position
         assert position + seq_len <= self.max_seq_length, "KV cache is full"

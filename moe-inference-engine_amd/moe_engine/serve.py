@@ -194,9 +194,11 @@ def enable_decode_graph() -> None:
     graph_generator = GraphedGenerator(model, pool.new_cache())
 
 
-def main(argv=None) -> None:
+def configure(args) -> dict:
+    """Set the server's model, device, cache switch and pool from parsed
+    command-line arguments (scripts/serve.py:139-160); returns the model's
+    provenance."""
     global model, cache_mode, allocator, device, graph_generator
-    args = build_parser().parse_args(argv)
     device = ("cuda" if torch.cuda.is_available() else "cpu") if args.device == "auto" else args.device
     if device == "cuda" and not torch.cuda.is_available():
         raise SystemExit("a GPU was requested but none is available")
@@ -211,6 +213,12 @@ def main(argv=None) -> None:
     graph_generator = None
     if args.decode_graph:
         enable_decode_graph()
+    return meta
+
+
+def main(argv=None) -> None:
+    args = build_parser().parse_args(argv)
+    meta = configure(args)
     print(f"Serving {meta['source']} on {device} with {cache_mode} KV cache "
           f"({args.paged_attention} attention), {args.moe} MoE, tokenizer {enc.name}")
     import uvicorn

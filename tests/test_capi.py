@@ -138,3 +138,53 @@ def test_block_plan_checks_fail_before_launch():
     assert rc == 1 and b"null scratch" in lib.mie_last_error()
     rc = lib.mie_block_decode(ctypes.create_string_buffer(size), 1 << 20, 5, None)
     assert rc == 1 and b"not initialised" in lib.mie_last_error()
+
+
+def _valid_plan_args(**over):
+    """mie_block_plan_init arguments after (plan, plan_bytes) that pass every
+    host check: float32, d 64 = 2 heads x 32, block 16, 8 blocks, 4 experts,
+    top-2, hidden 128.  Pointers are aligned stand-ins that the host checks
+    never dereference."""
+    names = ("dim heads head_dim block_size dtype attn_ln_w attn_ln_b attn_eps w_in b_in w_out b_out k_pool v_pool "
+             "sblk shead num_blocks table table_len scale q attn h ws ws_bytes moe_ln_w moe_ln_b moe_eps router w1 "
+             "b1 w2 b2 experts top_k hidden logits ids route_w hidden_act out").split()
+    addr = iter(range(1 << 20, 1 << 30, 1 << 16))
+    args = {name: next(addr) for name in names}
+    args.update(dim=64, heads=2, head_dim=32, block_size=16, dtype=0, attn_eps=1e-5, moe_eps=1e-5,
+                sblk=2 * 16 * 32, shead=16 * 32, num_blocks=8, table_len=8, scale=1.0, ws=0, ws_bytes=0,
+                experts=4, top_k=2, hidden=128)
+    args.update(over)
+    assert len(args) == 41
+    return [args[n] for n in names]
+
+
+@pytest.mark.parametrize("change,code,message", [
+    (dict(dtype=1), 2, b"float32 only"),            # bf16 passes the attention half, the MoE half refuses it
+    (dict(head_dim=48, heads=1, dim=48, sblk=16 * 48, shead=16 * 48), 2, b""),  # a head_dim the decode lacks
+    (dict(table_len=0), 1, b"block table"),
+    (dict(w1=(1 << 20) + 4), 1, b"aligned"),
+    (dict(router=0), 1, b"null pointer"),
+    (dict(experts=65), 1, b"experts"),
+    (dict(sblk=16 * 32), 1, b"overlap"),
+])
+def test_block_plan_init_makes_every_launch_check(change, code, message):
+    """A plan that one of the five launches would refuse is refused when it is
+    initialised, so mie_block_decode never stops between launches."""
+    lib = _native.lib()
+    plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
+    assert lib.mie_block_plan_init(plan, len(plan), *_valid_plan_args()) == 0
+    rc = lib.mie_block_plan_init(plan, len(plan), *_valid_plan_args(**change))
+    assert rc == code, lib.mie_last_error()
+    assert message in lib.mie_last_error()
+
+
+def test_block_decode_refuses_a_position_past_the_table_before_launching():
+    """The new token's slot must lie inside the plan's block table (8 entries
+    of 16 tokens here), and x must be aligned; both fail on the host."""
+    lib = _native.lib()
+    plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
+    assert lib.mie_block_plan_init(plan, len(plan), *_valid_plan_args()) == 0
+    rc = lib.mie_block_decode(plan, 1 << 20, 8 * 16, None)
+    assert rc == 1 and b"past the 8-entry block table" in lib.mie_last_error()
+    rc = lib.mie_block_decode(plan, (1 << 20) + 4, 3, None)
+    assert rc == 1 and b"aligned" in lib.mie_last_error()

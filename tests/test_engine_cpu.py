@@ -366,3 +366,32 @@ def test_decode_plans_are_dropped_when_parameters_can_change():
         plant()
         change()
         assert all(b._one_token is None for b in blocks)
+
+
+def test_submodule_changes_advance_the_plan_epoch():
+    """Launch plans hold tensor addresses; every conversion, load or
+    assignment that can replace a tensor inside a block's modules advances
+    the epoch that is part of each plan's key, including changes made on a
+    submodule (the block itself is not told)."""
+    from moe_engine import model as model_mod
+
+    model = Model(ModelConfig(**TINY)).eval()
+    block = model.MoEBlocks[0]
+    for change in (
+        lambda: block.moe.float(),
+        lambda: block.moe.load_state_dict(block.moe.state_dict()),
+        lambda: block.attention.to("cpu"),
+        lambda: block.attention.load_state_dict({k: v.clone() for k, v in block.attention.state_dict().items()},
+                                                assign=True),
+        lambda: block.moe.router.float(),
+        lambda: block.moe.experts[1].net[0].float(),
+        lambda: block.attn_norm.float(),
+        lambda: setattr(block.attention.out_proj, "weight", torch.nn.Parameter(torch.zeros(32, 32))),
+        lambda: setattr(block.moe_norm, "bias", torch.nn.Parameter(torch.zeros(32))),
+    ):
+        before = model_mod._TENSOR_EPOCH[0]
+        change()
+        assert model_mod._TENSOR_EPOCH[0] > before
+    # State-dict names and module types the reference's callers check are unchanged.
+    assert isinstance(block.attn_norm, torch.nn.LayerNorm) and isinstance(block.moe.router, torch.nn.Linear)
+    assert "MoEBlocks.0.attention.out_proj.weight" in model.state_dict()

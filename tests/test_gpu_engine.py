@@ -183,7 +183,7 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
         assert torch.equal(run(factory, True), run(factory, False))
 
     check(alloc_a.new_cache)
-    assert all(b._one_token is not None and b._one_token[1] is not None for b in model.MoEBlocks)
+    assert all(b._one_token is not None and b._one_token[2] is not None for b in model.MoEBlocks)
     check(alloc_b.new_cache)
     check(alloc_a.new_cache)
     # New parameter tensors at new addresses.
@@ -193,7 +193,7 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
     # The PyTorch MoE path (no plan), then back.
     model.set_moe_mode("reference")
     check(alloc_a.new_cache)
-    assert all(b._one_token[1] is None for b in model.MoEBlocks)
+    assert all(b._one_token[2] is None for b in model.MoEBlocks)
     model.set_moe_mode("auto")
     check(alloc_a.new_cache)
     # A conversion (.float() is one even when nothing changes) drops the plans.
@@ -205,10 +205,73 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
     out_proj.weight = torch.nn.Parameter(out_proj.weight.detach() * 0.25)
     model.MoEBlocks[1].drop_decode_plan()
     check(alloc_a.new_cache)
+    # Submodule-level conversions, loads and assignments, with no
+    # drop_decode_plan: each one replaces tensors the plan points at.
+    block = model.MoEBlocks[0]
+    for change in (
+        lambda: block.moe.float(),
+        lambda: block.moe.load_state_dict({k: v.clone() * 0.5 for k, v in block.moe.state_dict().items()}),
+        lambda: block.attention.to("cuda"),
+        lambda: block.attention.load_state_dict(
+            {k: v.clone() * 0.5 for k, v in block.attention.state_dict().items()}, assign=True),
+        lambda: setattr(block.attn_norm, "weight", torch.nn.Parameter(block.attn_norm.weight.detach() + 0.5)),
+        lambda: setattr(block.moe.router, "weight", torch.nn.Parameter(block.moe.router.weight.detach() * -1)),
+    ):
+        change()
+        check(alloc_a.new_cache)
     # The reference's projection + append sequence for the attention half.
     alloc_a.fuse_qkv = False
     check(alloc_a.new_cache)
-    assert all(b._one_token[1] is None for b in model.MoEBlocks)
+    assert all(b._one_token[2] is None for b in model.MoEBlocks)
+
+
+def test_block_plans_do_not_keep_finished_caches_alive():
+    """A plan refers to its cache weakly and holds only addresses: once a
+    sequence's cache and allocator are dropped, their pools are freed even
+    though every block still holds the plan built for them."""
+    import gc
+    import weakref
+
+    print_case("plan does not hold the pools")
+    torch.manual_seed(0)
+    model = Model(ModelConfig(**TINY)).to("cuda").eval()
+    ids = torch.randint(0, TINY["vocab_size"], (1, 8), device="cuda")
+    alloc = model.new_block_allocator(num_blocks=16, block_size=4, attention_mode="direct")
+    cache = alloc.new_cache()
+    stepwise_logits(model, ids, cache, 4)
+    assert all(b._one_token is not None and b._one_token[2] is not None for b in model.MoEBlocks)
+    pool = weakref.ref(alloc.k_pool)
+    del cache, alloc
+    gc.collect()
+    assert pool() is None, "a block's launch plan kept a finished cache's pools alive"
+    # A new cache (possibly at the dead one's id) builds a new plan and decodes as the per-call path does.
+    alloc = model.new_block_allocator(num_blocks=16, block_size=4, attention_mode="direct")
+    got = stepwise_logits(model, ids, alloc.new_cache(), 4)
+    for b in model.MoEBlocks:
+        b.drop_decode_plan()
+        b._decode_one_token = lambda *args, **kwargs: None
+    try:
+        want = stepwise_logits(model, ids, alloc.new_cache(), 4)
+    finally:
+        for b in model.MoEBlocks:
+            del b._decode_one_token
+    assert torch.equal(got, want)
+
+
+def test_hidden_states_is_the_callers_tensor():
+    """For one decode token the last block leaves its output in a per-layer
+    buffer; Model.hidden_states returns a copy, so a result kept across steps
+    does not change (as the reference's does not)."""
+    print_case("hidden_states copy")
+    torch.manual_seed(0)
+    model = Model(ModelConfig(**TINY)).to("cuda").eval()
+    cache = model.new_block_allocator(num_blocks=16, block_size=4, attention_mode="direct").new_cache()
+    with torch.no_grad():
+        model.hidden_states(torch.tensor([[1, 2, 3]], device="cuda"), cache)
+        first = model.hidden_states(torch.tensor([[4]], device="cuda"), cache)
+        kept = first.clone()
+        model.hidden_states(torch.tensor([[5]], device="cuda"), cache)
+    assert torch.equal(first, kept)
 
 
 def test_block_plan_grows_its_workspace_for_split_contexts():
@@ -242,5 +305,5 @@ def test_block_plan_grows_its_workspace_for_split_contexts():
 
     assert torch.equal(run(True), run(False))
     for b in model.MoEBlocks:
-        launcher = b._one_token[1]
+        launcher = b._one_token[2]
         assert launcher is not None and launcher.buffers[-1]["ws"] is not None
