@@ -37,8 +37,9 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
-SECONDARY_NAMES = ("config2_single_layer", "config3_append_gather", "config5_long_context", "fused_moe_decode",
-                   "config1_e2e_decode")
+SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
+                   "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync")
+PROBES = ROOT / "moe-inference-engine_amd" / "moe_engine" / "libmie_probes.so"
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
 
@@ -187,7 +188,7 @@ def run_config4(torch, args):
 # ---- CPU baseline (the oracle's gather + SDPA path, on the host cores) -------------
 
 
-def cpu_model() -> str:
+def cpu_model_name() -> str:
     """The host CPU's model name from /proc/cpuinfo ("unknown" elsewhere)."""
     try:
         with open("/proc/cpuinfo") as f:
@@ -226,7 +227,7 @@ def cpu_baseline(torch, w, budget_s):
         "sample": (
             f"sequences {sample} of config 4 ({sum(lens)} tokens, bf16), {passes} passes of "
             f"per-sequence gather + torch scaled_dot_product_attention in {elapsed:.1f} s; "
-            f"host {os.cpu_count()} logical CPUs ({cpu_model()}), torch threads {threads}"
+            f"host {os.cpu_count()} logical CPUs ({cpu_model_name()}), torch threads {threads}"
         ),
         "ms_per_pass": round(elapsed / passes * 1e3, 2),
     }
@@ -443,19 +444,193 @@ def secondary_config5(torch):
     return res
 
 
-def secondary_e2e(torch, rounds=5, new_tokens=64):
-    """BASELINE config 1 on the GPU (random init from seed 0, fp32, block 16,
-    32-token prompt): per-token greedy decode latency of the contiguous,
-    paged-gather, paged-direct and paged-direct-graph (decode steps replayed
-    from a HIP graph) systems in interleaved rounds with paired Student-t
-    intervals (moe_engine.harness.ab_compare)."""
+def probes_lib():
+    """libmie_probes.so (csrc/probes): measurement kernels only."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(PROBES))
+    c = ctypes
+    lib.mie_probe_read_chunks.argtypes = [c.c_int32, c.c_int32, c.c_void_p, c.c_int64, c.c_void_p, c.c_int32,
+                                          c.c_int32, c.c_void_p, c.c_void_p]
+    lib.mie_probe_read_chunks.restype = c.c_int32
+    lib.mie_probe_noop.argtypes = [c.c_int32, c.c_void_p]
+    lib.mie_probe_noop.restype = c.c_int32
+    lib.mie_probe_grid_barrier.argtypes = [c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_void_p, c.c_void_p,
+                                           c.c_void_p, c.c_void_p, c.c_int64, c.c_void_p]
+    lib.mie_probe_grid_barrier.restype = c.c_int32
+    return lib
+
+
+def secondary_grid_sync(torch, iters=2000):
+    """What a grid-wide wait inside one launch costs, against a kernel
+    boundary in a graph (launch_floor): a cooperative launch of 256 or 512
+    workgroups meeting at a device counter `iters` times, in three memory
+    disciplines (csrc/probes/grid_sync.hip): device-scope relaxed data
+    (mode 1: no L2 writeback), one agent release/acquire per workgroup
+    (mode 2), and __threadfence in every thread (mode 0).  Best of five
+    launches, microseconds per barrier, with the count of stale reads seen
+    by the checks."""
+    lib = probes_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for groups in (256, 512):
+        counter = torch.zeros(1, dtype=torch.int32, device="cuda")
+        flags = torch.zeros(2, dtype=torch.int32, device="cuda")
+        vec = torch.zeros(2 * groups * 256, dtype=torch.float32, device="cuda")
+        for mode, name in ((1, "device_scope_data"), (2, "release_acquire_per_group"), (0, "threadfence_all")):
+            best, bad = None, 0
+            for _ in range(5):
+                counter.zero_()
+                flags.zero_()
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                rc = lib.mie_probe_grid_barrier(mode, groups, iters, 256, counter.data_ptr(), vec.data_ptr(),
+                                                flags[0:1].data_ptr(), flags[1:2].data_ptr(), 1 << 20, stream)
+                stop.record()
+                torch.cuda.synchronize()
+                if rc:
+                    raise RuntimeError(f"mie_probe_grid_barrier returned {rc}")
+                err, wrong = flags.tolist()
+                if err:
+                    raise RuntimeError("a grid barrier wait hit its spin limit")
+                bad += wrong
+                us = start.elapsed_time(stop) * 1e3 / iters
+                best = us if best is None else min(best, us)
+            res[f"g{groups}_{name}"] = {"us_per_barrier": round(best, 3), "stale_reads": bad}
+    return res
+
+
+def secondary_launch_floor(torch):
+    """The floor a launch-bound call cannot go under on this box: device time
+    per call of 64 calls replayed from one HIP graph, each call one or two
+    launches of an empty kernel (256 workgroups) - the same way the config 2,
+    3 and 5 figures are timed."""
+    lib = probes_lib()
+
+    def noop():
+        if lib.mie_probe_noop(256, torch.cuda.current_stream().cuda_stream):
+            raise RuntimeError("mie_probe_noop failed")
+
+    one = graph_replay_us(torch, [noop] * 64)
+    two = graph_replay_us(torch, [lambda: (noop(), noop())] * 64)
+    return {"one_launch_us": round(one, 3), "two_launch_us": round(two, 3),
+            "note": "empty kernel, 256 workgroups x 256 threads; 64 calls per graph, device time per call"}
+
+
+def secondary_read_ceilings(torch):
+    """Read ceilings of the decode's access pattern: 768 MiB per call (about
+    config 4's 785 MB) in 2 KiB chunks - one bf16 (block, head) tile - at
+    random chunk ids of a 4 GiB buffer and in order, read into registers with
+    non-temporal loads (the decode kernels' way) or staged through LDS with
+    global_load_lds, with 1-8 chunks in flight per wave (csrc/probes)."""
+    lib = probes_lib()
+    chunks = (4 << 30) // 2048
+    n = (768 << 20) // 2048
+    buf = torch.empty(chunks * 2048, dtype=torch.uint8, device="cuda")
+    gen = torch.Generator().manual_seed(0)
+    orders = {"random": torch.randperm(chunks, generator=gen)[:n].to(torch.int32).cuda(),
+              "in_order": torch.arange(n, dtype=torch.int32, device="cuda")}
+    groups = 2048
+    out = torch.empty(groups * 256, dtype=torch.int32, device="cuda")
+    res = {}
+    for order, ids in orders.items():
+        for kind, name, depths in ((0, "registers", (1, 2, 4, 8)), (1, "global_load_lds", (1, 2, 4))):
+            for depth in depths:
+                def call(kind=kind, depth=depth, ids=ids):
+                    rc = lib.mie_probe_read_chunks(kind, depth, buf.data_ptr(), chunks, ids.data_ptr(), n, groups,
+                                                   out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+                    if rc:
+                        raise RuntimeError(f"mie_probe_read_chunks returned {rc}")
+
+                us = timed_us(torch, call, iters=20, warmup=3)
+                res[f"{order}_{name}_depth{depth}"] = {"us": round(us, 1), "gbs": round(n * 2048 / us / 1e3, 1)}
+    for order in orders:
+        for name in ("registers", "global_load_lds"):
+            res[f"best_{order}_{name}_gbs"] = max(v["gbs"] for k, v in res.items()
+                                                   if isinstance(v, dict) and k.startswith(f"{order}_{name}_"))
+    del buf
+    return res
+
+
+def add_floor_fractions(secondary):
+    """Latency-bound figures as fractions of the launch floor (floor / time:
+    1.0 would be a call that costs no more than its empty launches) next to
+    their fractions of HBM peak."""
+    floor = secondary.get("launch_floor")
+    if not floor or "error" in floor:
+        return
+    one, two = floor["one_launch_us"], floor["two_launch_us"]
+    c2 = secondary.get("config2_single_layer")
+    if c2 and "warm_us" in c2:
+        c2["launch_floor_us"] = two
+        c2["floor_over_time"] = round(two / c2["warm_us"], 3)
+        c2["hbm_fraction"] = round(c2["warm_gbs"] / PEAK_HBM_GBS, 3)
+    c3 = secondary.get("config3_append_gather")
+    if c3:
+        for key, cell in c3.items():
+            if isinstance(cell, dict) and "gather_device_us_per_layer" in cell:
+                cell["launch_floor_us"] = one
+                cell["gather_floor_over_time"] = round(one / cell["gather_device_us_per_layer"], 3)
+                cell["gather_hbm_fraction"] = round(cell["gather_gbs"] / PEAK_HBM_GBS, 3)
+    c5 = secondary.get("config5_long_context")
+    if c5:
+        for key, cell in c5.items():
+            if isinstance(cell, dict) and "_b1_c32768_" in key:
+                cell["launch_floor_us"] = two  # partitions + the merge launch
+                cell["floor_over_time"] = round(two / cell["us"], 3)
+                cell["hbm_fraction"] = round(cell["gbs"] / PEAK_HBM_GBS, 3)
+
+
+def secondary_e2e(torch, rounds=5, new_tokens=64, cpu_rounds=2):
+    """BASELINE config 1 (random init from seed 0, fp32, block 16, 32-token
+    prompt, 64 greedy tokens).
+
+    GPU: per-token greedy decode latency of the reference's systems
+    (contiguous, paged-gather, paged-direct), the graph-replayed step
+    (paged-direct-graph), and contiguous-direct(-graph): the contiguous
+    layout run by the same fused kernels, so paged-direct minus it is the cost
+    of paging alone - interleaved rounds with paired Student-t intervals
+    (moe_engine.harness.ab_compare, benchmarks/ab_compare.py:75-144).
+
+    CPU (the reference CPU path, on this host's cores): contiguous and
+    paged-gather per-token decode latency, prefill excluded, median over the
+    decode steps of `cpu_rounds` interleaved rounds (benchmarks/bench.py:
+    217-231).
+
+    Parity: the reference's report (scripts/check_parity.py:64-93) of the GPU
+    paged-direct path against the CPU path, and the GPU tokens against the
+    reference engine's own tokens for this configuration
+    (tests/golden/reference_config1.json, written by the reference's code)."""
     from moe_engine import harness
 
     model = harness.make_model(harness.CONFIG1, seed=0, device="cuda")
     gen = torch.Generator().manual_seed(0)
     prompt = torch.randint(0, harness.CONFIG1["vocab_size"], (32,), generator=gen).cuda()
-    systems = harness.SYSTEMS + (harness.GRAPH_SYSTEM,)
-    return harness.ab_compare(model, prompt, systems, rounds=rounds, new_tokens=new_tokens)
+    systems = harness.SYSTEMS + (harness.GRAPH_SYSTEM, harness.CONTIGUOUS_DIRECT, harness.CONTIGUOUS_DIRECT_GRAPH)
+    report = harness.ab_compare(model, prompt, systems, rounds=rounds, new_tokens=new_tokens)
+
+    log("config 1 on the CPU")
+    cpu_model = harness.make_model(harness.CONFIG1, seed=0, device="cpu")
+    start = time.perf_counter()
+    cpu = harness.ab_compare(cpu_model, prompt.cpu(), ("contiguous", "paged-gather"), rounds=cpu_rounds,
+                             new_tokens=new_tokens)
+    cpu["wall_s"] = round(time.perf_counter() - start, 1)
+    cpu["torch_threads"] = torch.get_num_threads()
+    cpu["os_cpu_count"] = os.cpu_count()
+    cpu["cpu_model"] = cpu_model_name()
+    cpu["tokens_equal_gpu"] = cpu["tokens_identical"] and cpu.pop("tokens") == report.pop("tokens")
+    report["cpu"] = cpu
+
+    log("config 1 parity report")
+    parity = harness.parity_report(model, cpu_model, prompt, new_tokens=new_tokens)
+    fixture = ROOT / "tests" / "golden" / "reference_config1.json"
+    if fixture.exists():
+        golden = json.loads(fixture.read_text())
+        if golden["prompt"] == prompt.tolist() and golden["new_tokens"] == new_tokens:
+            parity["tokens_equal_reference_engine"] = parity["tokens"] == golden["tokens"]["paged_gather"]
+    parity.pop("tokens")
+    report["parity"] = parity
+    return report
 
 
 def main():
@@ -496,11 +671,14 @@ def main():
     if not args.no_secondary:
         chosen = [n for n in args.secondary.split(",") if n] or list(SECONDARY_NAMES)
         for name, fn in (
+            ("launch_floor", secondary_launch_floor),
             ("config2_single_layer", secondary_config2),
             ("config3_append_gather", secondary_config3),
             ("config5_long_context", secondary_config5),
             ("fused_moe_decode", secondary_moe),
             ("config1_e2e_decode", secondary_e2e),
+            ("read_ceilings", secondary_read_ceilings),
+            ("grid_sync", secondary_grid_sync),
         ):
             if name not in chosen:
                 continue
@@ -510,6 +688,7 @@ def main():
             except Exception as exc:  # a secondary figure never hides the main line
                 secondary[name] = {"error": f"{type(exc).__name__}: {exc}"}
             torch.cuda.empty_cache()
+        add_floor_fractions(secondary)
 
     line = {
         "metric": METRIC,
@@ -554,6 +733,23 @@ def per_token_decode_ms(e2e):
         return None
     out = {system: s["decode_median_ms"] for system, s in e2e["summary"].items()}
     out["tokens_identical"] = e2e.get("tokens_identical")
+    paired = e2e.get("paired_deltas", {})
+    for name in ("paged-direct_minus_contiguous-direct", "paged-direct-graph_minus_contiguous-direct-graph"):
+        if name in paired:
+            out[f"paging_cost_{name.split('_minus_')[0]}_ms"] = {
+                "mean_delta_ms": paired[name]["mean_delta_ms"], "ci95_ms": paired[name]["ci95_ms"]}
+    cpu = e2e.get("cpu")
+    if cpu and "summary" in cpu:
+        for system, s in cpu["summary"].items():
+            out[f"cpu_{system}"] = s["decode_median_ms"]
+        out["cpu_threads"] = cpu.get("torch_threads")
+        out["cpu_model"] = cpu.get("cpu_model")
+        out["cpu_tokens_identical_to_gpu"] = cpu.get("tokens_equal_gpu")
+    parity = e2e.get("parity")
+    if parity:
+        out["parity"] = {k: parity[k] for k in ("engine_cache", "max_abs_logit_diff", "max_rel_logit_diff",
+                                                "greedy_tokens_compared", "first_greedy_mismatch",
+                                                "tokens_equal_reference_engine") if k in parity}
     out["workload"] = ("BASELINE config 1: 12 layers, d 768, 12 x 64 heads, top-2 of 8, FFN 2048, vocab 50257, "
                        "fp32, random init seed 0, 32-token prompt, 64 greedy tokens, block 16")
     return out

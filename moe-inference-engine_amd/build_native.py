@@ -5,7 +5,9 @@
 compiles each csrc/*.hip with hipcc (in parallel, one object per source) and
 links the objects into moe_engine/libmie_paged.so.  The library is written to
 a temporary name first and renamed, so a process that already mapped the old
-file keeps a consistent copy.
+file keeps a consistent copy.  The measurement probes bench.py runs
+(csrc/probes/*.hip: read ceilings, launch floor) go into their own
+moe_engine/libmie_probes.so, apart from the product library.
 """
 
 import os
@@ -21,6 +23,7 @@ REPO_ROOT = PKG_ROOT.parent
 CSRC = PKG_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 OUTPUT = PKG_ROOT / "moe_engine" / "libmie_paged.so"
+PROBE_OUTPUT = PKG_ROOT / "moe_engine" / "libmie_probes.so"
 ARCH = os.environ.get("MIE_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
@@ -49,8 +52,13 @@ def _run(cmd, verbose):
 
 
 def build(verbose: bool = True) -> Path:
-    sources = sorted(CSRC.glob("*.hip"))
-    tmp = OUTPUT.with_name(OUTPUT.name + f".tmp{os.getpid()}")
+    _link(sorted(CSRC.glob("*.hip")), OUTPUT, verbose)
+    _link(sorted((CSRC / "probes").glob("*.hip")), PROBE_OUTPUT, verbose)
+    return OUTPUT
+
+
+def _link(sources, output: Path, verbose: bool) -> None:
+    tmp = output.with_name(output.name + f".tmp{os.getpid()}")
     jobs = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with tempfile.TemporaryDirectory(prefix="mie_build_") as objdir:
         objs = [str(Path(objdir) / (src.stem + ".o")) for src in sources]
@@ -68,8 +76,7 @@ def build(verbose: bool = True) -> Path:
         if rc != 0:
             tmp.unlink(missing_ok=True)
             raise RuntimeError(f"hipcc link failed ({rc}):\n{err}")
-    os.replace(tmp, OUTPUT)
-    return OUTPUT
+    os.replace(tmp, output)
 
 
 if __name__ == "__main__":

@@ -13,9 +13,19 @@ the real checkpoint and tokenizer are not available here:
                    (benchmarks/ab_compare.py:49-198)
 
 System names are the reference's: "contiguous", "paged-gather",
-"paged-direct", plus "paged-direct-graph": paged-direct with each decode step
-replayed from one captured HIP graph (moe_engine.graphs), captured once in the
-warm-up and reused for every later round.  Run as a module for a JSON report:
+"paged-direct", plus
+  "paged-direct-graph"       paged-direct with each decode step replayed from
+                             one captured HIP graph (moe_engine.graphs),
+                             captured once in the warm-up and reused for every
+                             later round;
+  "contiguous-direct"        the contiguous cache's layout run by the same
+                             fused kernels as paged-direct (a one-block pool,
+                             contiguous_direct_cache), so that paged-direct
+                             minus it is the cost of paging alone;
+  "contiguous-direct-graph"  the same, replayed from a graph.
+The reference's "contiguous" system runs PyTorch attention (and, on a GPU,
+this engine's fused MoE half), so paged-direct minus contiguous also counts
+the fused attention kernels.  Run as a module for a JSON report:
 
     python -m moe_engine.harness ab --rounds 5 --new-tokens 64
 """
@@ -34,6 +44,9 @@ from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig
 
 SYSTEMS = ("contiguous", "paged-gather", "paged-direct")
 GRAPH_SYSTEM = "paged-direct-graph"
+CONTIGUOUS_DIRECT = "contiguous-direct"
+CONTIGUOUS_DIRECT_GRAPH = "contiguous-direct-graph"
+ALL_SYSTEMS = SYSTEMS + (GRAPH_SYSTEM, CONTIGUOUS_DIRECT, CONTIGUOUS_DIRECT_GRAPH)
 
 # the miniMoE-shaped decoder.
 CONFIG1 = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768, num_heads=12,
@@ -62,11 +75,27 @@ def make_model(config=None, seed=0, device="cuda", dtype=torch.float32):
     return Model(ModelConfig(**(config or CONFIG1))).to(device, dtype).eval()
 
 
+def contiguous_direct_cache(model):
+    """The contiguous cache (KVCache, model.py:30-58) in the form the fused
+    kernels take: one pool block of max_seq_length tokens.  The pools are
+    [layers, 1, heads, max_seq_length, head_dim] - KVCache's k / v tensors
+    for batch 1, element for element - and the block table is [0], so token t
+    sits at offset t * head_dim of its head's row, as in KVCache.  The
+    append, the decode and the graph step run unchanged on it."""
+    return model.new_block_allocator(1, model.max_seq_length, attention_mode="direct").new_cache()
+
+
+def is_graph_system(system) -> bool:
+    return system.endswith("-graph")
+
+
 def make_cache(model, system, block_size=16):
     """A fresh cache for `system`; paged pools hold one max-length sequence
     (scripts/serve.py:147-155)."""
     if system == "contiguous":
         return model.new_cache()
+    if system in (CONTIGUOUS_DIRECT, CONTIGUOUS_DIRECT_GRAPH):
+        return contiguous_direct_cache(model)
     num_blocks = -(-model.max_seq_length // block_size)
     mode = "direct" if system == GRAPH_SYSTEM else system[len("paged-"):]
     return model.new_block_allocator(num_blocks, block_size, attention_mode=mode).new_cache()
@@ -179,16 +208,17 @@ def paired_t_summary(deltas):
 def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, block_size=16):
     """Interleaved rounds of every system, rotating which starts each round."""
     systems = list(systems)
-    graph_state = {}
+    graph_states = {}
 
     def run(system):
-        if system == GRAPH_SYSTEM:
-            if "cache" not in graph_state:
-                graph_state["cache"] = make_cache(model, system, block_size)
+        if is_graph_system(system):
+            state = graph_states.setdefault(system, {})
+            if "cache" not in state:
+                state["cache"] = make_cache(model, system, block_size)
             try:
-                return run_round_graphed(model, graph_state, prompt_ids, new_tokens)
+                return run_round_graphed(model, state, prompt_ids, new_tokens)
             finally:
-                release(graph_state["cache"])
+                release(state["cache"])
         cache = make_cache(model, system, block_size)
         try:
             return run_round(model, cache, prompt_ids, new_tokens)
@@ -221,7 +251,8 @@ def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, bloc
 
     paired = {}
     for a, b in (("paged-direct", "contiguous"), ("paged-direct", "paged-gather"), ("paged-gather", "contiguous"),
-                 (GRAPH_SYSTEM, "paged-direct"), (GRAPH_SYSTEM, "contiguous")):
+                 (GRAPH_SYSTEM, "paged-direct"), (GRAPH_SYSTEM, "contiguous"),
+                 ("paged-direct", CONTIGUOUS_DIRECT), (GRAPH_SYSTEM, CONTIGUOUS_DIRECT_GRAPH)):
         if a in systems and b in systems:
             paired[f"{a}_minus_{b}"] = paired_t_summary([x - y for x, y in zip(mean_steps_ms(a), mean_steps_ms(b))])
     tokens = [results[s]["tokens"] for s in systems]
@@ -229,9 +260,58 @@ def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, bloc
         "summary": summary,
         "paired_deltas": paired,
         "tokens_identical": all(t == tokens[0] for t in tokens),
+        "tokens": tokens[0],
         "rounds": rounds,
         "new_tokens": new_tokens,
         "prompt_tokens": int(prompt_ids.numel()),
+    }
+
+
+def stepwise_logits(model, seq, cache, prompt_len):
+    """Logits [T, vocab] for every position of `seq` ([1, T] ids): the prompt
+    as one prefill, then one decode step per later token (teacher forcing)."""
+    with torch.no_grad():
+        rows = [model(seq[:, :prompt_len], cache)[0]]
+        for t in range(prompt_len, seq.shape[1]):
+            rows.append(model(seq[:, t:t + 1], cache)[0])
+    return torch.cat(rows).float()
+
+
+def parity_report(model, cpu_model, prompt_ids, new_tokens=64, block_size=16, system="paged-direct"):
+    """The reference's parity report (scripts/check_parity.py:64-93) for
+    `system` on `model`'s device against the CPU contiguous path of the same
+    weights (`cpu_model`): greedy tokens of both, and the logits at every
+    position of the CPU's greedy sequence - the prefill and each decode step,
+    with the same token fed to both - compared as the reference does
+    (relative difference over |reference logit| clamped to at least 1)."""
+    prompt_cpu = prompt_ids.cpu()
+    with torch.no_grad():
+        want = cpu_model.generate(prompt_cpu, new_tokens, temperature=0, cache=cpu_model.new_cache())
+        cache = make_cache(model, system, block_size)
+        got = model.generate(prompt_ids, new_tokens, temperature=0, cache=cache)
+        release(cache)
+        ref_logits = stepwise_logits(cpu_model, want, cpu_model.new_cache(), len(prompt_cpu))
+        cache = make_cache(model, system, block_size)
+        logits = stepwise_logits(model, want.to(prompt_ids.device), cache, len(prompt_cpu)).cpu()
+        release(cache)
+    abs_diff = (ref_logits - logits).abs()
+    rel_diff = abs_diff / ref_logits.abs().clamp(min=1.0)
+    want, got = want[0].tolist(), got[0].tolist()
+    first = next((i for i, (a, b) in enumerate(zip(want, got)) if a != b), None)
+    if first is None and len(want) != len(got):
+        first = min(len(want), len(got))
+    return {
+        "engine_cache": system,
+        "device": str(prompt_ids.device),
+        "reference_path": "CPU, contiguous cache, same seed-0 weights",
+        "dtype": str(next(model.parameters()).dtype),
+        "prompt_tokens": len(prompt_cpu),
+        "positions_compared": int(logits.shape[0]),
+        "max_abs_logit_diff": abs_diff.max().item(),
+        "max_rel_logit_diff": rel_diff.max().item(),
+        "greedy_tokens_compared": len(want) - len(prompt_cpu),
+        "first_greedy_mismatch": first,
+        "tokens": got,
     }
 
 
@@ -266,7 +346,7 @@ def main(argv=None):
     parser.add_argument("--new-tokens", type=int, default=64)
     parser.add_argument("--prompt-tokens", type=int, default=32)
     parser.add_argument("--contexts", default="16,64,256,1024")
-    parser.add_argument("--systems", default=",".join(SYSTEMS))
+    parser.add_argument("--systems", default=",".join(SYSTEMS), help="any of " + ", ".join(ALL_SYSTEMS))
     parser.add_argument("--device", default="cuda")
     args = parser.parse_args(argv)
     contexts = [int(c) for c in args.contexts.split(",")]
