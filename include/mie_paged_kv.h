@@ -21,9 +21,14 @@
  *   mie_lm_head       <- final_norm + output_projection (model.py:564-565) and,
  *                        optionally, the greedy argmax (:603) for one token
  *   mie_embed         <- token_embedding(ids) + positional_embedding(pos)  src/moe_engine/model.py:558
+ *   mie_attn_out_acc  <- paged_attention.decode then out_proj for one decode
+ *                        token (model.py:263 then :268), per head, summed into
+ *                        a fixed-point accumulator row: one launch
+ *   mie_moe_decode_block_acc <- the block's x + out_proj(a) (model.py:447) and
+ *                        x + moe(moe_norm(x)) (:448-449) after mie_attn_out_acc
  *   mie_block_plan_init, mie_block_decode <- one TransformerMoEBlock.forward for one
- *                        decode token (model.py:446-449 with :226-269): the five
- *                        launches above from a stored plan, one call per token
+ *                        decode token (model.py:446-449 with :226-269): four or
+ *                        five launches above from a stored plan, one call per token
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -77,7 +82,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 11
+#define MIE_ABI_VERSION 12
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -397,12 +402,62 @@ int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_st
                                  void* stream);
 
 /*
+ * Decode attention of ONE token fused with the attention's output projection
+ * (paged_attention.decode, paged_attention.py:113-154, then out_proj,
+ * model.py:268), one launch.  For each head h the launch computes
+ *
+ *   a_h = softmax(scale * q_h . K_h^T) . V_h   over tokens [0, ctx)   (as mie_paged_decode)
+ *   y_h = W_out[:, h*D : (h+1)*D] . a_h        (W_out [dim, dim] row-major, dim = H * D)
+ *
+ * and adds round(y_h[i] * 2^32) into acc[i] (int64, dim + 1 entries) with
+ * integer atomics, so acc[i] = sum_h round(y_h[i] * 2^32) is exact and the
+ * same whatever order the workgroups run in.  A y_h[i] of magnitude 2^31 or
+ * more (or NaN) is not added: acc[dim] is set instead.  acc must hold zeros
+ * beforehand (mie_moe_decode_block_acc clears it after use).  ctx is *ctx_dev
+ * when ctx_dev is non-NULL (device int32), else `ctx`; either is clamped to
+ * max_ctx, and max_ctx spans at most 1024 blocks.  q [H * D], the pools (one
+ * layer, element strides, as mie_paged_decode) and W_out are float32 and
+ * 16-byte aligned; head_dim 32, 64 or 128; block_table holds block_table_len
+ * entries (ids outside the pool are skipped, as in the decode).
+ */
+int32_t mie_attn_out_acc(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                         int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                         int32_t block_table_len, const int32_t* ctx_dev, int32_t ctx, int32_t max_ctx,
+                         int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, const void* w_out,
+                         void* acc, int32_t dtype, void* stream);
+
+/*
+ * The rest of a decoder block after mie_attn_out_acc (model.py:447-449):
+ *
+ *   h_out = x + round(acc * 2^-32 + b_out)          (NaN everywhere when acc[dim] != 0)
+ *   out   = h_out + MoE(LayerNorm(h_out))           (as mie_moe_decode_block)
+ *
+ * and acc cleared to zeros for the next token.  Two launches: h_out is formed
+ * in the W1 launch (every workgroup forms it in registers, one stores it), the
+ * W2 launch adds it and clears acc.  Arguments and limits as
+ * mie_moe_decode_block; acc (int64 [dim + 1]), h_out and b_out (may be NULL)
+ * 16-byte aligned; h_out must not alias x.
+ */
+int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_out, void* h_out,
+                                 const void* ln_weight, const void* ln_bias, float ln_eps, const void* router_weight,
+                                 const void* w1, const void* b1, const void* w2, const void* b2, int32_t num_experts,
+                                 int32_t top_k, int32_t dim, int32_t hidden, void* router_logits, void* expert_ids,
+                                 void* route_weights, void* hidden_act, void* out, int32_t dtype, void* stream);
+
+/*
  * One decoder block for ONE decode token (TransformerMoEBlock.forward,
  * model.py:446-449, with the attention half model.py:226-269) from a launch
  * plan stored in caller-owned host memory of mie_block_plan_bytes() bytes.
- * mie_block_decode(plan, x, position, stream) issues, on `stream`:
+ * mie_block_decode(plan, x, counters, position, stream) issues, on `stream`:
  *
+ * with an accumulator (`acc` non-NULL, used when mie_attn_out_acc is built for
+ * the shape - float32, head_dim 32, 64 or 128 - and ignored otherwise) and
+ * position + 1 <= 2048, four launches:
  *   mie_qkv_append(x, attn norm, in_proj, pools, block_table, position) -> q
+ *   mie_attn_out_acc(q, pools, block_table, ctx = position + 1, out_proj) -> acc
+ *   mie_moe_decode_block_acc(x, acc, out_proj bias, moe norm, router, experts) -> h, out
+ * otherwise five:
+ *   mie_qkv_append(...)                                                   -> q
  *   mie_paged_decode(q, pools, block_table, ctx = position + 1)           -> attn
  *   mie_linear_residual(attn, out_proj, residual x)                        -> h
  *   mie_moe_decode_block(h, moe norm, router, experts)                     -> out
@@ -411,22 +466,29 @@ int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_st
  * mie_block_plan_init: the block's weights and norms, the layer's pools
  * (element strides) and block table, the rows q, attn and h ([num_heads *
  * head_dim], [num_heads * head_dim], [dim], written by the call), the MoE
- * scratch and the output row.  The results are those of calling the entry
- * points in turn.  `workspace` (may be NULL) serves the decode's split
- * context; a position whose decode needs more than workspace_bytes (see
- * mie_paged_decode_plan at batch 1 and max_ctx_len = position + 1) fails
- * with MIE_ERR_WORKSPACE before anything is launched, and the caller
- * initialises the plan again with a larger workspace.  The plan holds
- * pointers only: the caller keeps every buffer alive while the plan is used,
- * and one plan serves calls in stream order.
+ * scratch, the output row and the accumulator (int64 [dim + 1], zeros when
+ * the plan is made; each four-launch call leaves it zeroed again).  The
+ * results are those of calling the entry points in turn.
  *
- * mie_block_plan_init makes every host check of the five launches (built
- * width, head_dim and dtype - the MoE half is float32 only -, shapes,
- * strides, alignment, null pointers) and fails with their status, so an
- * initialised plan never stops between launches.  The decode reads at most
+ * `counters` (device int32[2], or NULL): the position and the context length
+ * are then read on the device (counters[0], counters[1]), so a captured graph
+ * can advance them, and `position` is the largest position a call may see: it
+ * sizes the launches and picks the form.  `workspace` (may be NULL) serves
+ * the five-launch form's split context; a call whose decode needs more than
+ * workspace_bytes (see mie_paged_decode_plan at batch 1 and max_ctx_len =
+ * position + 1) fails with MIE_ERR_WORKSPACE before anything is launched, and
+ * the caller initialises the plan again with a larger workspace.  The plan
+ * holds pointers only: the caller keeps every buffer alive while the plan is
+ * used, and one plan serves calls in stream order.
+ *
+ * mie_block_plan_init makes every host check of the launches (built width,
+ * head_dim and dtype - the MoE half is float32 only -, shapes, strides,
+ * alignment, null pointers) and fails with their status, so an initialised
+ * plan never stops between launches.  The decode reads at most
  * block_table_len table entries (block_table_len >= 1).  mie_block_decode
- * checks x (non-NULL, 16-byte aligned) and rejects a position at or past
- * block_table_len * block_size, both before launching.
+ * checks x (non-NULL, 16-byte aligned, not one of the plan's rows) and
+ * rejects a position at or past block_table_len * block_size, both before
+ * launching.
  */
 int64_t mie_block_plan_bytes(void);
 int32_t mie_block_plan_init(void* plan, int64_t plan_bytes, int32_t dim, int32_t num_heads, int32_t head_dim,
@@ -440,8 +502,8 @@ int32_t mie_block_plan_init(void* plan, int64_t plan_bytes, int32_t dim, int32_t
                             const void* router_weight, const void* w1, const void* b1, const void* w2,
                             const void* b2, int32_t num_experts, int32_t top_k, int32_t hidden,
                             void* router_logits, void* expert_ids, void* route_weights, void* hidden_act,
-                            void* out);
-int32_t mie_block_decode(const void* plan, const void* x, int32_t position, void* stream);
+                            void* out, void* acc);
+int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,343 @@
+// Decode attention of one token fused with the attention's output projection.
+//
+// The reference's attention half of a decoder block for one decode token
+// (src/moe_engine/model.py:226-269 and :447) is, after the QKV projection and
+// the cache write:
+//
+//   a_h  = softmax(scale * q_h . K_h^T) . V_h          for each head h
+//   o    = out_proj(a) = W_out a + b_out               (W_out [dim, dim], a = [a_0 .. a_{H-1}])
+//   h    = x + o
+//
+// Done as two launches (a decode kernel writing a, then a GEMV over all of a)
+// the projection waits for every head.  Here one launch computes, for each
+// head h and each block of output rows r, the head's attention and that head's
+// share of the rows:
+//
+//   y_hr[i] = sum_{d < D} W_out[i, h*D + d] * a_h[d]     i in rows block r
+//
+// and adds y_hr[i] into acc[i] with a 64-bit integer atomic on a fixed-point
+// value round(y_hr[i] * 2^32).  Integer addition is exact and associative, so
+// acc[i] = sum_h round(y_hr[i] * 2^32) comes out bit-identical whatever order
+// the workgroups finish in - deterministic, with no cross-workgroup handoff
+// (which on MI355X needs an L2 writeback per publishing workgroup) and no
+// second launch.  The consumer (the MoE W1 launch of the same block,
+// mie_moe_decode_block_acc) forms h = x + (float(acc) * 2^-32 + b_out), and
+// its W2 launch clears acc for the next token.  A value of 2^31 or more in magnitude
+// (or not a number) cannot be held: such a partial sets acc[dim] instead, and
+// the consumer then writes NaN.
+//
+// Work decomposition: grid (8 * R * ceil(H / 8)) workgroups of 4 waves.  The
+// hardware dispatches workgroup i to XCD i mod 8, so workgroup (8 j + x) is
+// head x + 8 (j / R), rows block j % R: the R workgroups of a head share one
+// XCD's L2, and the head's K/V, which each of them reads, comes from HBM once.
+// Inside a workgroup the 4 waves split the context (token t goes to wave
+// (t / TPL) mod 4) and merge their softmax states in LDS; then each wave
+// computes TPL rows per wave load of its share of the row block.  Everything
+// that does not depend on the attention - q, the block table, this
+// workgroup's W_out slice - is read in the first memory round; the K/V tiles
+// in the second (one round per 32 tokens per wave).
+//
+// float32 pools, head_dim 32, 64 or 128, contexts up to kMaxTable blocks.  A
+// context block whose id lies outside the pool is never read; the head's
+// attention is then NaN (as the decode kernels write), which sets acc[dim].
+#include <math.h>
+
+#include "mie_common.h"
+
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWaves = 4;
+constexpr int kMaxTable = mie::kAttnOutMaxBlocks;  // block-table entries held in LDS
+constexpr int kBatch = 8;         // wave loads of K (and of V) per memory round
+// Wave loads of W_out rows per wave: 3 gives 48 rows per workgroup at
+// head_dim 64 (R = 16 workgroups per head at dim 768, 192 in all).  Measured
+// on MI355X (config 1, kernel trace): 6 loads (R = 8) 7.0 us per launch, 3
+// with plain K/V loads 5.6 us, 2 with plain loads 5.7 us.
+constexpr int kRowSteps = 3;
+constexpr float kFix = 4294967296.0f;  // 2^32
+constexpr float kFixLimit = 2147483648.0f;  // |y| < 2^31
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct AttnOutArgs {
+  const float* q;  // [H * D]
+  const float* k;  // one layer's pools
+  const float* v;
+  int64_t sblk, shead;  // element strides
+  int32_t num_blocks;
+  const int32_t* bt;
+  int32_t bt_len;
+  const int32_t* ctx_dev;  // device context length (or NULL: ctx)
+  int32_t ctx;
+  int32_t max_ctx;  // contexts are clamped to this (host bound for ctx_dev)
+  int32_t nblk_max;  // ceil(max_ctx / block_size) <= kMaxTable
+  int32_t H;
+  mie::FastDiv bs;
+  float qk_scale;  // scale * log2(e)
+  const float* w;  // W_out [dim, dim] row-major
+  int32_t dim;
+  int32_t R;  // row blocks per head
+  int32_t rows_per_block;
+  unsigned long long* acc;  // [dim + 1]
+};
+
+template <int D>
+struct Shape {
+  static constexpr int LPT = D / 4;   // lanes per row, 16 bytes each
+  static constexpr int TPL = 64 / LPT;  // rows per wave load
+};
+
+__device__ __forceinline__ float dot4(f32x4_t a, f32x4_t b, float s) {
+  s = fmaf(a.x, b.x, s);
+  s = fmaf(a.y, b.y, s);
+  s = fmaf(a.z, b.z, s);
+  return fmaf(a.w, b.w, s);
+}
+
+// Log-sum-exp merge of (m, l, o) with (m2, l2, o2) in the log2 domain; a state
+// with m = -inf holds no token.
+__device__ __forceinline__ void merge_state(float& m, float& l, f32x4_t& o, float m2, float l2, f32x4_t o2) {
+  const float mm = fmaxf(m, m2);
+  const float c1 = m == -INFINITY ? 0.f : mie::fast_exp2(m - mm);
+  const float c2 = m2 == -INFINITY ? 0.f : mie::fast_exp2(m2 - mm);
+  l = l * c1 + l2 * c2;
+  o = o * c1 + o2 * c2;
+  m = mm;
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
+  constexpr int LPT = Shape<D>::LPT;
+  constexpr int TPL = Shape<D>::TPL;
+  __shared__ int32_t s_bt[kMaxTable];
+  __shared__ float s_ml[kWaves][2];
+  __shared__ __align__(16) float s_o[kWaves][D];
+  __shared__ __align__(16) float s_attn[D];
+
+  const int xcd = blockIdx.x & 7;
+  const int j = blockIdx.x >> 3;
+  const int h = xcd + 8 * (j / a.R);
+  const int rblk = j % a.R;
+  if (h >= a.H) return;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane / LPT;          // row within a wave load
+  const int c4 = (lane % LPT) * 4;   // this lane's 4 columns of a row
+
+  // Round 1, all independent: this workgroup's W_out rows, q, the block
+  // table up to the host's bound (nblk_max entries, at most 1024 = 4 per
+  // thread), and the live length.
+  f32x4_t wv[kRowSteps];
+  const int row0 = rblk * a.rows_per_block;
+  const int row_end = min(a.dim, row0 + a.rows_per_block);
+#pragma unroll
+  for (int s = 0; s < kRowSteps; ++s) {
+    int row = row0 + (s * kWaves + wave) * TPL + g;
+    row = row < row_end ? row : row0;  // in bounds; the product is dropped below
+    wv[s] = __builtin_nontemporal_load(
+        reinterpret_cast<const f32x4_t*>(a.w + static_cast<int64_t>(row) * a.dim + h * D + c4));
+  }
+  const f32x4_t qv = *reinterpret_cast<const f32x4_t*>(a.q + h * D + c4);
+  constexpr int kTablePerThread = kMaxTable / 256;
+  int tb[kTablePerThread];
+#pragma unroll
+  for (int u = 0; u < kTablePerThread; ++u) {
+    const int i = u * 256 + static_cast<int>(threadIdx.x);
+    const int ic = i < a.bt_len ? i : 0;  // bt_len >= 1
+    tb[u] = u * 256 < a.nblk_max ? a.bt[ic] : 0;
+  }
+  int ctx = a.ctx_dev ? *a.ctx_dev : a.ctx;
+  ctx = ctx < 0 ? 0 : (ctx > a.max_ctx ? a.max_ctx : ctx);
+  const int nblk = static_cast<int>(a.bs.div(static_cast<uint32_t>(ctx + a.bs.d - 1)));  // <= nblk_max
+  int bad = 0;
+#pragma unroll
+  for (int u = 0; u < kTablePerThread; ++u) {
+    const int i = u * 256 + static_cast<int>(threadIdx.x);
+    if (i < nblk) {
+      const int blk = i < a.bt_len ? tb[u] : -1;
+      s_bt[i] = blk;
+      bad |= blk < 0 || blk >= a.num_blocks;
+    }
+  }
+  // A context block outside the pool (never read) makes the head's attention NaN.
+  const bool any_bad = __syncthreads_or(bad) != 0;
+
+  // Round 2..: this wave's tokens t = (step * 4 + wave) * TPL + g, kBatch wave
+  // loads of K and V per round; online softmax per TPL-row group.
+  const float* kh = a.k + static_cast<int64_t>(h) * a.shead + c4;
+  const float* vh = a.v + static_cast<int64_t>(h) * a.shead + c4;
+  float m = -INFINITY, l = 0.f;
+  f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+  const int steps = (ctx + kWaves * TPL - 1) / (kWaves * TPL);
+  for (int s0 = 0; s0 < steps; s0 += kBatch) {
+    f32x4_t kv[kBatch], vv[kBatch];
+    bool valid[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int t = ((s0 + b) * kWaves + wave) * TPL + g;
+      valid[b] = t < ctx;
+      const int tc = valid[b] ? t : 0;  // rows past the context re-read token 0, masked below
+      const uint32_t lb = a.bs.div(static_cast<uint32_t>(tc));
+      int blk = s_bt[lb];
+      blk = blk >= 0 && blk < a.num_blocks ? blk : 0;  // never dereferenced outside the pool (any_bad is set)
+      const int64_t off = static_cast<int64_t>(blk) * a.sblk + static_cast<int64_t>(tc - lb * a.bs.d) * D;
+      // Plain (temporal) loads: the R workgroups of this head run on one XCD
+      // and read the same K/V, so all but the first hit its L2.
+      kv[b] = *reinterpret_cast<const f32x4_t*>(kh + off);
+      vv[b] = *reinterpret_cast<const f32x4_t*>(vh + off);
+    }
+    float sc[kBatch];
+    float mb = m;
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      sc[b] = mie::group_sum<LPT>(dot4(qv, kv[b], 0.f)) * a.qk_scale;
+      sc[b] = valid[b] ? sc[b] : -INFINITY;
+      mb = fmaxf(mb, sc[b]);
+    }
+    if (mb != -INFINITY) {
+      const float alpha = m == -INFINITY ? 0.f : mie::fast_exp2(m - mb);
+      l *= alpha;
+      o *= alpha;
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        const float p = valid[b] ? mie::fast_exp2(sc[b] - mb) : 0.f;
+        l += p;
+        o += p * vv[b];
+      }
+      m = mb;
+    }
+  }
+  // Merge the TPL row groups of the wave (lanes g * LPT + c hold the same
+  // columns for every g), then the four waves through LDS.
+#pragma unroll
+  for (int off = LPT; off < 64; off <<= 1) {
+    const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
+    f32x4_t o2;
+    o2.x = __shfl_xor(o.x, off);
+    o2.y = __shfl_xor(o.y, off);
+    o2.z = __shfl_xor(o.z, off);
+    o2.w = __shfl_xor(o.w, off);
+    merge_state(m, l, o, m2, l2, o2);
+  }
+  if (lane < LPT) {
+    *reinterpret_cast<f32x4_t*>(&s_o[wave][c4]) = o;
+    if (lane == 0) {
+      s_ml[wave][0] = m;
+      s_ml[wave][1] = l;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < LPT) {
+    float mm = s_ml[0][0], ll = s_ml[0][1];
+    f32x4_t oo = *reinterpret_cast<const f32x4_t*>(&s_o[0][c4]);
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w)
+      merge_state(mm, ll, oo, s_ml[w][0], s_ml[w][1], *reinterpret_cast<const f32x4_t*>(&s_o[w][c4]));
+    // No key at all: scaled_dot_product_attention's zeros.  A context block
+    // outside the pool gives NaN, as the decode kernels write.
+    f32x4_t r = ll > 0.f ? oo / ll : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (any_bad) r = f32x4_t{NAN, NAN, NAN, NAN};
+    *reinterpret_cast<f32x4_t*>(&s_attn[c4]) = r;
+  }
+  __syncthreads();
+
+  // This head's share of the rows: y = W_out[row, h*D : (h+1)*D] . a_h.
+  const f32x4_t av = *reinterpret_cast<const f32x4_t*>(&s_attn[c4]);
+#pragma unroll
+  for (int s = 0; s < kRowSteps; ++s) {
+    const int row = row0 + (s * kWaves + wave) * TPL + g;
+    const float y = mie::group_sum<LPT>(dot4(wv[s], av, 0.f));
+    if (lane % LPT == 0 && row < row_end) {
+      if (fabsf(y) < kFixLimit) {
+        const long long fx = llrintf(y * kFix);
+        atomicAdd(a.acc + row, static_cast<unsigned long long>(fx));
+      } else {
+        atomicOr(a.acc + a.dim, 1ull);  // not representable (or NaN): the consumer writes NaN
+      }
+    }
+  }
+}
+
+}  // namespace
+
+namespace mie {
+
+int32_t attn_out_check(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                       int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                       int32_t block_table_len, int32_t max_ctx, int32_t num_heads, int32_t head_dim,
+                       int32_t block_size, const void* w_out, const void* acc, int32_t dtype) {
+  if (dtype != MIE_DTYPE_F32) return mie::fail(MIE_ERR_UNSUPPORTED, "mie_attn_out_acc: float32 only");
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128)
+    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_attn_out_acc: head_dim %d (32, 64 or 128)", head_dim);
+  if (num_heads <= 0 || num_heads > 4096 || block_size <= 0 || num_blocks <= 0 || block_table_len <= 0)
+    return mie::fail(MIE_ERR_INVALID, "mie_attn_out_acc: heads %d, block_size %d, blocks %d, table %d", num_heads,
+                     block_size, num_blocks, block_table_len);
+  if (max_ctx < 0 || (static_cast<int64_t>(max_ctx) + block_size - 1) / block_size > kMaxTable)
+    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_attn_out_acc: contexts up to %d blocks (max_ctx %d, block %d)",
+                     kMaxTable, max_ctx, block_size);
+  if (!q || !k_pool || !v_pool || !block_table || !w_out || !acc)
+    return mie::fail(MIE_ERR_INVALID, "mie_attn_out_acc: null pointer");
+  if (pool_stride_head < static_cast<int64_t>(block_size) * head_dim ||
+      pool_stride_block < static_cast<int64_t>(num_heads) * pool_stride_head || pool_stride_head % 4 ||
+      pool_stride_block % 4)
+    return mie::fail(MIE_ERR_INVALID, "mie_attn_out_acc: pool strides overlap or are not multiples of 4");
+  auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  if (!a16(q) || !a16(k_pool) || !a16(v_pool) || !a16(w_out) || reinterpret_cast<uintptr_t>(acc) % 8)
+    return mie::fail(MIE_ERR_INVALID, "mie_attn_out_acc: q, the pools and W_out must be 16-byte aligned, acc 8");
+  return MIE_OK;
+}
+
+int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                        int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                        int32_t block_table_len, const int32_t* ctx_dev, int32_t ctx, int32_t max_ctx,
+                        int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, const void* w_out,
+                        void* acc, hipStream_t stream) {
+  AttnOutArgs a{};
+  a.q = static_cast<const float*>(q);
+  a.k = static_cast<const float*>(k_pool);
+  a.v = static_cast<const float*>(v_pool);
+  a.sblk = pool_stride_block;
+  a.shead = pool_stride_head;
+  a.num_blocks = num_blocks;
+  a.bt = block_table;
+  a.bt_len = block_table_len;
+  a.ctx_dev = ctx_dev;
+  a.ctx = ctx;
+  a.max_ctx = max_ctx;
+  a.nblk_max = static_cast<int32_t>((static_cast<int64_t>(max_ctx) + block_size - 1) / block_size);
+  a.H = num_heads;
+  a.bs = mie::FastDiv::make(static_cast<uint32_t>(block_size));
+  a.qk_scale = scale * kLog2e;
+  a.w = static_cast<const float*>(w_out);
+  a.dim = num_heads * head_dim;
+  a.acc = static_cast<unsigned long long*>(acc);
+  const int tpl = 64 / (head_dim / 4);
+  a.rows_per_block = kWaves * tpl * kRowSteps;
+  a.R = (a.dim + a.rows_per_block - 1) / a.rows_per_block;
+  const dim3 grid(8 * a.R * ((num_heads + 7) / 8));
+  switch (head_dim) {
+    case 32: attn_out_kernel<32><<<grid, 256, 0, stream>>>(a); break;
+    case 64: attn_out_kernel<64><<<grid, 256, 0, stream>>>(a); break;
+    default: attn_out_kernel<128><<<grid, 256, 0, stream>>>(a); break;
+  }
+  return mie::check_launch("attn_out_kernel");
+}
+
+}  // namespace mie
+
+extern "C" int32_t mie_attn_out_acc(const void* q, const void* k_pool, const void* v_pool,
+                                    int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                                    const int32_t* block_table, int32_t block_table_len, const int32_t* ctx_dev,
+                                    int32_t ctx, int32_t max_ctx, int32_t num_heads, int32_t head_dim,
+                                    int32_t block_size, float scale, const void* w_out, void* acc, int32_t dtype,
+                                    void* stream) {
+  int32_t rc = mie::attn_out_check(q, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, block_table,
+                                   block_table_len, max_ctx, num_heads, head_dim, block_size, w_out, acc, dtype);
+  if (rc != MIE_OK) return rc;
+  if (!ctx_dev && (ctx < 0 || ctx > max_ctx))
+    return mie::fail(MIE_ERR_INVALID, "mie_attn_out_acc: ctx %d outside [0, max_ctx=%d]", ctx, max_ctx);
+  return mie::attn_out_launch(q, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, block_table,
+                              block_table_len, ctx_dev, ctx, max_ctx, num_heads, head_dim, block_size, scale, w_out,
+                              acc, static_cast<hipStream_t>(stream));
+}

@@ -1,18 +1,24 @@
 // One decoder block for one decode token from a stored launch plan.
 //
 // The block of the reference (src/moe_engine/model.py:446-449, attention half
-// :226-269) for a single new token is five launches of this library: the QKV
-// projection into the pool (mie_qkv_append), the paged decode attention
-// (mie_paged_decode), out_proj with the residual add (mie_linear_residual) and
-// the MoE half (mie_moe_decode_block, two launches).  Issued one by one from
-// Python, each costs a foreign call of two dozen arguments; the eager decode
-// step is then bound by the host.  Here the arguments that do not change from
-// token to token (weights, pools, table, scratch rows, shapes) are stored once
-// in caller-owned host memory, and each token is one call with the input row,
-// the position and the stream.  The launches and their arguments are exactly
-// those of the five entry points, so the results are bit-identical to calling
-// them in turn.  mie_block_plan_init makes every host check those entry points
-// make, so a call that passes its own checks launches all five.
+// :226-269) for a single new token is, with a plan that holds an accumulator
+// row and a context of at most kFusedMaxCtx tokens, four launches of this
+// library: the QKV projection into the pool (mie_qkv_append), the attention
+// fused with the output projection (mie_attn_out_acc: per-head shares summed
+// in fixed point into the accumulator), and the MoE half forming the residual
+// sum itself (mie_moe_decode_block_acc, two launches).  Otherwise it is five:
+// mie_qkv_append, the paged decode attention (mie_paged_decode), out_proj
+// with the residual add (mie_linear_residual) and the MoE half
+// (mie_moe_decode_block).  Issued one by one from Python, each costs a
+// foreign call of two dozen arguments; the eager decode step is then bound by
+// the host.  Here the arguments that do not change from token to token
+// (weights, pools, table, scratch rows, shapes) are stored once in
+// caller-owned host memory, and each token is one call with the input row,
+// the position (or a device counter pair, for a captured graph) and the
+// stream.  The launches and their arguments are exactly those of the entry
+// points named, so the results are bit-identical to calling them in turn.
+// mie_block_plan_init makes every host check those entry points make, so a
+// call that passes its own checks launches the whole block.
 #include <string.h>
 
 #include "mie_common.h"
@@ -44,7 +50,15 @@ struct BlockPlan {
   const void *router, *w1, *b1, *w2, *b2;
   int32_t num_experts, top_k, hidden;
   void *router_logits, *expert_ids, *route_weights, *hidden_act, *out;
+  // fused attention + output projection (mie_attn_out_acc): fixed-point sums
+  // [dim + 1], or NULL for the five-launch form only
+  void* acc;
 };
+
+// Contexts the four-launch form serves: each of a head's workgroups reads the
+// head's whole context, so past this length the partitioned decode (every CU
+// on one head's context) plus the separate projection launch is faster.
+constexpr int32_t kFusedMaxCtx = 2048;
 
 }  // namespace
 
@@ -58,7 +72,7 @@ extern "C" int32_t mie_block_plan_init(
     void* q, void* attn, void* h, void* workspace, int64_t workspace_bytes, const void* moe_ln_weight,
     const void* moe_ln_bias, float moe_ln_eps, const void* router_weight, const void* w1, const void* b1,
     const void* w2, const void* b2, int32_t num_experts, int32_t top_k, int32_t hidden, void* router_logits,
-    void* expert_ids, void* route_weights, void* hidden_act, void* out) {
+    void* expert_ids, void* route_weights, void* hidden_act, void* out, void* acc) {
   if (!plan || plan_bytes < static_cast<int64_t>(sizeof(BlockPlan)))
     return mie::fail(MIE_ERR_INVALID, "mie_block_plan_init: plan needs %lld bytes",
                      static_cast<long long>(sizeof(BlockPlan)));
@@ -85,6 +99,22 @@ extern "C" int32_t mie_block_plan_init(
   rc = mie::moe_decode_block_check(h, moe_ln_weight, moe_ln_bias, router_weight, w1, b1, w2, b2, num_experts, top_k,
                                    dim, hidden, router_logits, expert_ids, route_weights, hidden_act, out, dtype);
   if (rc != MIE_OK) return rc;
+  if (acc) {
+    rc = mie::attn_out_check(q, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, block_table,
+                             block_table_len, 1, num_heads, head_dim, block_size, w_out, acc, dtype);
+    if (rc == MIE_ERR_UNSUPPORTED) {
+      acc = nullptr;  // a shape the fused attention is not built for: the five-launch form serves every call
+      mie::clear_error();
+    } else if (rc != MIE_OK) {
+      return rc;
+    }
+  }
+  if (acc) {
+    rc = mie::moe_decode_block_acc_check(x_stand_in, acc, b_out, h, moe_ln_weight, moe_ln_bias, router_weight, w1,
+                                         b1, w2, b2, num_experts, top_k, dim, hidden, router_logits, expert_ids,
+                                         route_weights, hidden_act, out, dtype);
+    if (rc != MIE_OK) return rc;
+  }
   BlockPlan p{};
   p.magic = kPlanMagic;
   p.dtype = dtype;
@@ -128,11 +158,13 @@ extern "C" int32_t mie_block_plan_init(
   p.route_weights = route_weights;
   p.hidden_act = hidden_act;
   p.out = out;
+  p.acc = acc;
   memcpy(plan, &p, sizeof(p));
   return MIE_OK;
 }
 
-extern "C" int32_t mie_block_decode(const void* plan, const void* x, int32_t position, void* stream) {
+extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position,
+                                    void* stream) {
   if (!plan) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: null plan");
   BlockPlan p;
   memcpy(&p, plan, sizeof(p));
@@ -142,23 +174,49 @@ extern "C" int32_t mie_block_decode(const void* plan, const void* x, int32_t pos
   if (static_cast<int64_t>(position) >= static_cast<int64_t>(p.block_table_len) * p.block_size)
     return mie::fail(MIE_ERR_INVALID, "mie_block_decode: position %d lies past the %d-entry block table", position,
                      p.block_table_len);
+  if (x == p.h || x == p.q || x == p.attn)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_decode: x aliases one of the plan's intermediate rows");
+  // With counters the position and context length are read on the device
+  // (counters[0], counters[1]) and `position` bounds them: it sizes the
+  // launch and chooses the form.
+  const int32_t* pos_dev = counters;
+  const int32_t* ctx_dev = counters ? counters + 1 : nullptr;
+  const int32_t max_ctx = position + 1;
+  const bool fused = p.acc && max_ctx <= kFusedMaxCtx &&
+                     (static_cast<int64_t>(max_ctx) + p.block_size - 1) / p.block_size <= mie::kAttnOutMaxBlocks;
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int32_t rc;
+  if (fused) {
+    // Four launches: QKV into the pool, attention with the output projection
+    // summed into acc, then the MoE half forming x + out_proj(a) itself.
+    rc = mie_qkv_append(x, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool, p.v_pool,
+                        p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table, p.block_table_len,
+                        pos_dev, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
+    if (rc != MIE_OK) return rc;
+    rc = mie::attn_out_launch(p.q, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head, p.num_blocks,
+                              p.block_table, p.block_table_len, ctx_dev, max_ctx, max_ctx, p.num_heads, p.head_dim,
+                              p.block_size, p.scale, p.w_out, p.acc, st);
+    if (rc != MIE_OK) return rc;
+    return mie_moe_decode_block_acc(x, p.acc, p.b_out, p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1,
+                                    p.b1, p.w2, p.b2, p.num_experts, p.top_k, p.dim, p.hidden, p.router_logits,
+                                    p.expert_ids, p.route_weights, p.hidden_act, p.out, p.dtype, stream);
+  }
   // The decode's split-context workspace is checked before anything is
   // launched, so a call that cannot finish changes nothing.
-  const int32_t ctx = position + 1;
   int64_t ws_need = 0;
-  int32_t rc = mie_paged_decode_plan(1, p.num_heads, p.head_dim, p.block_size, ctx, p.dtype, 0, nullptr, &ws_need);
+  rc = mie_paged_decode_plan(1, p.num_heads, p.head_dim, p.block_size, max_ctx, p.dtype, 0, nullptr, &ws_need);
   if (rc != MIE_OK) return rc;
   if (ws_need > p.workspace_bytes)
     return mie::fail(MIE_ERR_WORKSPACE, "mie_block_decode: position %d needs a %lld-byte workspace, plan has %lld",
                      position, static_cast<long long>(ws_need), static_cast<long long>(p.workspace_bytes));
   rc = mie_qkv_append(x, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool, p.v_pool,
                       p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table, p.block_table_len,
-                      nullptr, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
+                      pos_dev, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
   if (rc != MIE_OK) return rc;
   const int64_t row = static_cast<int64_t>(p.num_heads) * p.head_dim;
   rc = mie_paged_decode(p.q, row, p.head_dim, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head,
-                        p.num_blocks, p.block_table, p.block_table_len, nullptr, nullptr, ctx, ctx, 1, p.num_heads,
-                        p.head_dim, p.block_size, p.scale, p.attn, row, p.head_dim, p.dtype,
+                        p.num_blocks, p.block_table, p.block_table_len, ctx_dev, nullptr, max_ctx, max_ctx, 1,
+                        p.num_heads, p.head_dim, p.block_size, p.scale, p.attn, row, p.head_dim, p.dtype,
                         ws_need ? p.workspace : nullptr, ws_need, 0, p.dtype, stream);
   if (rc != MIE_OK) return rc;
   rc = mie_linear_residual(p.attn, p.w_out, p.b_out, x, p.h, p.dim, p.dim, p.dtype, stream);

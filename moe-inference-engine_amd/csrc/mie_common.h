@@ -175,3 +175,27 @@ int32_t moe_decode_block_check(const void* x, const void* ln_weight, const void*
                                const void* expert_ids, const void* route_weights, const void* hidden_act,
                                const void* out, int32_t dtype);
 }  // namespace mie
+
+namespace mie {
+// Block-table entries the fused attention + output projection holds in LDS:
+// it serves contexts of at most this many blocks.
+constexpr int32_t kAttnOutMaxBlocks = 1024;
+// Host checks and launch of the fused attention + output projection
+// (attn_out.hip, mie_attn_out_acc) and the MoE half that consumes its
+// fixed-point sums (mie_moe_decode_block_acc).
+int32_t attn_out_check(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                       int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                       int32_t block_table_len, int32_t max_ctx, int32_t num_heads, int32_t head_dim,
+                       int32_t block_size, const void* w_out, const void* acc, int32_t dtype);
+int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
+                        int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
+                        int32_t block_table_len, const int32_t* ctx_dev, int32_t ctx, int32_t max_ctx,
+                        int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, const void* w_out,
+                        void* acc, hipStream_t stream);
+int32_t moe_decode_block_acc_check(const void* x, const void* acc, const void* b_out, const void* h_out,
+                                   const void* ln_weight, const void* ln_bias, const void* router_weight,
+                                   const void* w1, const void* b1, const void* w2, const void* b2,
+                                   int32_t num_experts, int32_t top_k, int32_t dim, int32_t hidden,
+                                   const void* router_logits, const void* expert_ids, const void* route_weights,
+                                   const void* hidden_act, const void* out, int32_t dtype);
+}  // namespace mie

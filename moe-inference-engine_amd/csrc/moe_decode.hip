@@ -47,6 +47,7 @@ template <int K>
 constexpr int kW2Chunks = K <= 2 ? 8 : (16 / K > 0 ? 16 / K : 1);
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef long long i64x2_t __attribute__((ext_vector_type(2)));
 
 struct MoeArgs {
   const float* x;       // [dim]
@@ -60,6 +61,14 @@ struct MoeArgs {
   const float* ln_b;      // block form: norm bias [dim] or NULL
   float ln_eps;
   const float* residual;  // block form: x, added to the output
+  // Accumulator form (after mie_attn_out_acc): the block's input to the MoE
+  // half is h = x + (acc * 2^-32 + b_out), formed in the W1 launch (h_out
+  // written by workgroup (0, 0)); the W2 launch adds h_out as the residual
+  // and clears acc for the next token.
+  const unsigned long long* acc;  // [dim + 1]; acc[dim] != 0: a partial was not representable
+  const float* b_out;             // [dim] or NULL
+  float* h_out;                   // [dim]
+  unsigned long long* acc_clear;  // W2: acc to clear, or NULL
   float* logits;   // [E]
   int32_t* ids;    // [top_k], largest logit first
   float* weights;  // [top_k], same order
@@ -86,10 +95,16 @@ __device__ __forceinline__ float wave_dot(const float* __restrict__ row, const f
 }
 
 // (v, i) against (ov, oi): the larger logit wins, the lower expert id on
-// ties - a total order, so any reduction tree gives the same pick.  Compares
-// and selects, no branches.
+// ties, and NaN counts as larger than every number (torch.topk's order) - a
+// total order, so any reduction tree gives the same pick, and a NaN logit is
+// picked like any other, so the pick is always an expert that is not yet
+// taken (a taken expert holds -inf and an id past 63).  Compares and selects,
+// no branches.
 __device__ __forceinline__ void topk_take(float& v, int& i, float ov, int oi) {
-  const bool b = (ov > v) | ((ov == v) & (oi < i));
+  const bool v_nan = v != v, o_nan = ov != ov;
+  const bool lower = oi < i;
+  // ov > v and ov == v are false when either is NaN.
+  const bool b = (o_nan & (!v_nan | lower)) | (ov > v) | ((ov == v) & lower);
   v = b ? ov : v;
   i = b ? oi : i;
 }
@@ -189,7 +204,7 @@ __device__ __forceinline__ float wave_sum4(float r0, float r1, float r2, float r
 // behind the kernel's one barrier, every wave takes the top-k itself, then
 // computes 4 rows of slot blockIdx.y's expert.  hidden % 4 == 0, so a wave's
 // rows are all valid or all past the end.
-template <int NCH, bool NORM>
+template <int NCH, bool NORM, bool ACC = false>
 __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   __shared__ float s_logits[kMaxExperts];
   const int k = blockIdx.y;
@@ -210,6 +225,52 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
     gb[c] = NORM && valid && a.ln_b ? load4(a.ln_b + i) : zero;
     q0[c] = valid && e0 < a.E ? load4(a.router + static_cast<int64_t>(e0) * dim + i) : zero;
     q1[c] = valid && e1 < a.E ? load4(a.router + static_cast<int64_t>(e1) * dim + i) : zero;
+  }
+  // Accumulator form: the fixed-point sums, the output projection's bias and
+  // the flag, loaded with the rest (unconditionally: lanes past dim re-read
+  // element 0 and drop it), so they add no memory round.
+  constexpr int NA = ACC ? NCH : 1;
+  i64x2_t acc_lo[NA], acc_hi[NA];
+  f32x4_t bo[NA];
+  long long acc_flag = 0;
+  if constexpr (ACC) {
+    const float* bsrc = a.b_out ? a.b_out : a.x;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int i = c * 256 + lane * 4;
+      const int ic = i < dim ? i : 0;
+      bo[c] = load4(bsrc + ic);
+      acc_lo[c] = *reinterpret_cast<const i64x2_t*>(a.acc + ic);
+      acc_hi[c] = *reinterpret_cast<const i64x2_t*>(a.acc + ic + 2);
+    }
+    acc_flag = *reinterpret_cast<const long long*>(a.acc + dim);
+    // Keep the scheduler from sinking any of these loads below the first use
+    // of the ones before them (which would cost a memory round).
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (ACC) {
+    // h = x + (acc * 2^-32 + b_out): the attention output projection summed
+    // over heads in fixed point (int64 -> float is one rounding, the power of
+    // two scale is exact), its bias, then the residual - the rounding points
+    // of x + out_proj(a).
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int i = c * 256 + lane * 4;
+      f32x4_t o = {static_cast<float>(acc_lo[c].x), static_cast<float>(acc_lo[c].y),
+                   static_cast<float>(acc_hi[c].x), static_cast<float>(acc_hi[c].y)};
+      o *= 2.3283064365386963e-10f;  // 2^-32
+      if (a.b_out) o += bo[c];
+      f32x4_t hv = y[c] + o;
+      if (acc_flag != 0) hv = f32x4_t{NAN, NAN, NAN, NAN};
+      y[c] = i < dim ? hv : zero;
+    }
+    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int i = c * 256 + lane * 4;
+        if (i < dim) *reinterpret_cast<f32x4_t*>(a.h_out + i) = y[c];
+      }
+    }
   }
 
   // 2. The block's LayerNorm (float32, biased variance), per wave.
@@ -338,6 +399,12 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
     bias[s] = a.b2[static_cast<int64_t>(e[s]) * a.dim + j];
   }
   const float res = RESID ? a.residual[j] : 0.f;
+  if (a.acc_clear && lane == 0) {
+    // The attention's fixed-point sums were consumed by the W1 launch: ready
+    // for the next token.
+    a.acc_clear[j] = 0ull;
+    if (j == 0) a.acc_clear[a.dim] = 0ull;
+  }
   float acc[K];
 #pragma unroll
   for (int s = 0; s < K; ++s) acc[s] = 0.f;
@@ -458,7 +525,13 @@ int32_t check_expert_args(const char* who, int32_t hidden, int32_t dim, const vo
 template <int NCH>
 void launch_w1(const MoeArgs& a, hipStream_t st) {
   const dim3 grid((a.hidden + 15) / 16, a.top_k);
-  if (a.ln_w) {
+  if (a.acc) {
+    if (a.ln_w) {
+      moe_w1_gelu_kernel<NCH, true, true><<<grid, 256, 0, st>>>(a);
+    } else {
+      moe_w1_gelu_kernel<NCH, false, true><<<grid, 256, 0, st>>>(a);
+    }
+  } else if (a.ln_w) {
     moe_w1_gelu_kernel<NCH, true><<<grid, 256, 0, st>>>(a);
   } else {
     moe_w1_gelu_kernel<NCH, false><<<grid, 256, 0, st>>>(a);
@@ -528,6 +601,25 @@ int32_t moe_decode_block_check(const void* x, const void* ln_weight, const void*
   return MIE_OK;
 }
 
+int32_t moe_decode_block_acc_check(const void* x, const void* acc, const void* b_out, const void* h_out,
+                                   const void* ln_weight, const void* ln_bias, const void* router_weight,
+                                   const void* w1, const void* b1, const void* w2, const void* b2,
+                                   int32_t num_experts, int32_t top_k, int32_t dim, int32_t hidden,
+                                   const void* router_logits, const void* expert_ids, const void* route_weights,
+                                   const void* hidden_act, const void* out, int32_t dtype) {
+  const int32_t rc = moe_decode_block_check(x, ln_weight, ln_bias, router_weight, w1, b1, w2, b2, num_experts,
+                                            top_k, dim, hidden, router_logits, expert_ids, route_weights,
+                                            hidden_act, out, dtype);
+  if (rc != MIE_OK) return rc;
+  if (!acc || !h_out || reinterpret_cast<uintptr_t>(acc) % 16 || !aligned16(h_out) || !aligned16(b_out))
+    return mie::fail(MIE_ERR_INVALID, "mie_moe_decode_block_acc: acc and h_out (and b_out) must be non-NULL and "
+                                      "16-byte aligned");
+  if (h_out == x)
+    return mie::fail(MIE_ERR_INVALID, "mie_moe_decode_block_acc: h_out must not alias x (the W1 launch reads x "
+                                      "while it writes h_out)");
+  return MIE_OK;
+}
+
 }  // namespace mie
 
 extern "C" int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
@@ -544,6 +636,37 @@ extern "C" int32_t mie_moe_decode_block(const void* x, const void* ln_weight, co
   a.ln_b = static_cast<const float*>(ln_bias);
   a.ln_eps = ln_eps;
   a.residual = static_cast<const float*>(x);
+  a.w1 = static_cast<const float*>(w1);
+  a.b1 = static_cast<const float*>(b1);
+  a.w2 = static_cast<const float*>(w2);
+  a.b2 = static_cast<const float*>(b2);
+  a.h = static_cast<float*>(hidden_act);
+  a.out = static_cast<float*>(out);
+  return launch_experts(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_out, void* h_out,
+                                            const void* ln_weight, const void* ln_bias, float ln_eps,
+                                            const void* router_weight, const void* w1, const void* b1,
+                                            const void* w2, const void* b2, int32_t num_experts, int32_t top_k,
+                                            int32_t dim, int32_t hidden, void* router_logits, void* expert_ids,
+                                            void* route_weights, void* hidden_act, void* out, int32_t dtype,
+                                            void* stream) {
+  int32_t rc = mie::moe_decode_block_acc_check(x, acc, b_out, h_out, ln_weight, ln_bias, router_weight, w1, b1, w2,
+                                               b2, num_experts, top_k, dim, hidden, router_logits, expert_ids,
+                                               route_weights, hidden_act, out, dtype);
+  if (rc != MIE_OK) return rc;
+  MoeArgs a = make_args(h_out, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids,
+                        route_weights);
+  a.x = static_cast<const float*>(x);  // the W1 launch reads x and forms h_out
+  a.acc = static_cast<const unsigned long long*>(acc);
+  a.b_out = static_cast<const float*>(b_out);
+  a.h_out = static_cast<float*>(h_out);
+  a.acc_clear = static_cast<unsigned long long*>(const_cast<void*>(acc));
+  a.ln_w = static_cast<const float*>(ln_weight);
+  a.ln_b = static_cast<const float*>(ln_bias);
+  a.ln_eps = ln_eps;
+  a.residual = static_cast<const float*>(h_out);
   a.w1 = static_cast<const float*>(w1);
   a.b1 = static_cast<const float*>(b1);
   a.w2 = static_cast<const float*>(w2);

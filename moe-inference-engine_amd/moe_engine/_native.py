@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -141,9 +141,26 @@ _SIGNATURES = {
          _c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64,  # q, attn, h rows, workspace, its bytes
          _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # moe norm, router, experts
          _i32, _i32, _i32,  # experts, top_k, hidden
-         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p],  # router logits, ids, weights, hidden, out
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # router logits, ids, weights, hidden, out
+         _c_void_p],  # accumulator (int64 [dim + 1]) or NULL
     ),
-    "mie_block_decode": (_i32, [_c_void_p, _c_void_p, _i32, _c_void_p]),
+    "mie_block_decode": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plan, x, counters, pos, stream
+    "mie_attn_out_acc": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,  # q, pools, strides, num_blocks
+         _c_void_p, _i32, _c_void_p, _i32, _i32,  # block table, length, ctx (device), ctx, max_ctx
+         _i32, _i32, _i32, _f32,  # heads, head_dim, block_size, scale
+         _c_void_p, _c_void_p, _i32, _c_void_p],  # W_out, accumulator, dtype, stream
+    ),
+    "mie_moe_decode_block_acc": (
+        _i32,
+        [_c_void_p, _c_void_p, _c_void_p, _c_void_p,  # x, accumulator, out_proj bias, h_out
+         _c_void_p, _c_void_p, _f32,  # norm weight, norm bias, eps
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # router, canonical w1, b1, w2, b2
+         _i32, _i32, _i32, _i32,  # experts, top_k, dim, hidden
+         _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,  # logits, ids, weights, hidden, out
+         _i32, _c_void_p],  # dtype, stream
+    ),
     "mie_lm_head": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _f32, _c_void_p, _c_void_p,  # x, norm weight, norm bias, eps, W, bias

@@ -78,6 +78,10 @@ class GraphedDecoder:
         c.graph_pos = self.pos if on else None
         c.graph_ctx = self.ctx if on else None
         c.graph_partition_tokens = self.partition_tokens if on else 0
+        # The largest position a replay can reach: the model's context or the
+        # pool's capacity, whichever is smaller.
+        capacity = c.allocator.num_blocks * c.allocator.block_size
+        c.graph_max_position = min(self.model.max_seq_length, capacity) - 1 if on else None
 
     def _forward_body(self):
         """The captured step: embeddings and blocks (Model._hidden_states),

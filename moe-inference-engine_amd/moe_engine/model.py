@@ -213,12 +213,15 @@ class PagedKVCache:
         )
         self._write_index_key = None  # (position, seq_len) of cached CPU indices
         # Graph mode (moe_engine.graphs): device int32 [1] tensors holding the
-        # position of the token being decoded and the context length; the
-        # kernels read them instead of host ints, and blocks are reserved by
-        # the caller before each replay.  None in ordinary use.
+        # position of the token being decoded and the context length (adjacent
+        # in memory: [position, length]); the kernels read them instead of host
+        # ints, and blocks are reserved by the caller before each replay.
+        # graph_max_position bounds the positions a replay can reach.  None in
+        # ordinary use.
         self.graph_pos = None
         self.graph_ctx = None
         self.graph_partition_tokens = 0
+        self.graph_max_position = None
 
     def _reserve(self, num_tokens: int) -> None:
         """Hold enough blocks for `num_tokens`, all or nothing (model.py:125-143)."""
@@ -711,11 +714,12 @@ class TransformerMoEBlock(nn.Module):
         return super()._apply(fn, recurse=recurse)
 
     def forward(self, x, cache, layer_idx, position):
-        # One-token eager decode with both fused halves runs from a cached
-        # launch plan; otherwise each half takes its fused path where it
-        # applies (same results to float32 rounding), else the reference's
-        # block (model.py:446-449).
-        if position > 0 and x.shape[1] == 1 and getattr(cache, "graph_pos", None) is None:
+        # One-token decode with both fused halves runs from a cached launch
+        # plan (eagerly, or recorded into a graph with device positions);
+        # otherwise each half takes its fused path where it applies (same
+        # results to float32 rounding), else the reference's block
+        # (model.py:446-449).
+        if position > 0 and x.shape[1] == 1:
             out = self._decode_one_token(x, cache, layer_idx, position)
             if out is not None:
                 return out
@@ -740,13 +744,20 @@ class TransformerMoEBlock(nn.Module):
                 m["attn_norm"].eps, m["moe_norm"].eps, x.dtype, x.device, x.shape[-1], _TENSOR_EPOCH[0])
 
     def _decode_one_token(self, x, cache, layer_idx, position):
-        """The block for one eager decode token when both fused halves apply:
-        the same five launches as fused_decode + fused_block_decode, with the
-        checks and the static launch arguments computed once per plan key
-        rather than per token.  Returns None when the fused halves do not
-        both apply."""
+        """The block for one decode token when both fused halves apply, from
+        a launch plan (mie_block_decode): four launches for contexts the fused
+        attention + output projection serves, else the five of fused_decode +
+        fused_block_decode; the checks and the static launch arguments are
+        computed once per plan key rather than per token.  In graph mode
+        (cache.graph_pos set) the launches read the device position and
+        length.  Returns None when the fused halves do not both apply."""
         if getattr(cache, "allocator", None) is None or x.dim() != 3 or x.shape[0] != 1 or not x.is_contiguous():
             return None
+        graph_pos = getattr(cache, "graph_pos", None)
+        if graph_pos is not None and (
+                cache.graph_ctx is None or cache.graph_max_position is None
+                or cache.graph_ctx.data_ptr() != graph_pos.data_ptr() + 4):
+            return None  # the plan reads [position, length] as one device pair
         key = self._one_token_key(x, cache, layer_idx)
         plan = self._one_token
         # The weak reference rules out a new cache that reuses a dead one's id;
@@ -760,9 +771,12 @@ class TransformerMoEBlock(nn.Module):
             plan = self._one_token = (key, weakref.ref(cache), launcher)
         return None if plan[2] is None else plan[2](x, cache, position)
 
+
     def _build_one_token(self, x, cache, layer_idx):
-        """A launch plan of the block's five launches (mie_block_plan_init):
-        each token is then one call, mie_block_decode(plan, x, position)."""
+        """A launch plan of the block's launches (mie_block_plan_init): each
+        token is then one call, mie_block_decode(plan, x, counters, position).
+        The plan holds an accumulator row for the fused attention + output
+        projection (zeros; each call leaves it zeroed)."""
         alloc = cache.allocator
         att, moe = self.attention, self.moe
         lib = _native.lib()
@@ -783,6 +797,7 @@ class TransformerMoEBlock(nn.Module):
         q = torch.empty((1, heads, 1, head_dim), dtype=dtype, device=device)
         attn = torch.empty_like(q)
         h = torch.empty((1, 1, dim), dtype=dtype, device=device)
+        acc = torch.zeros(dim + 1, dtype=torch.int64, device=device)
         plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
         held = {}  # the split-context workspace the plan points at
 
@@ -798,29 +813,35 @@ class TransformerMoEBlock(nn.Module):
                 s["w1"].data_ptr(), s["b1"].data_ptr(), s["w2"].data_ptr(), s["b2"].data_ptr(),
                 moe.router.weight.shape[0], moe._expert_ids.numel(), s["w1"].shape[1],
                 moe._router_logits.data_ptr(), moe._expert_ids.data_ptr(), moe._route_weights.data_ptr(),
-                moe._expert_hidden.data_ptr(), moe._direct_out.data_ptr(),
+                moe._expert_hidden.data_ptr(), moe._direct_out.data_ptr(), acc.data_ptr(),
             ), "mie_block_plan_init")
 
         init(None)
         run = lib.mie_block_decode
 
         def launch(x, cache, position):
-            cache._reserve(position + 1)
+            if cache.graph_pos is None:
+                cache._reserve(position + 1)
+                counters, bound = None, position
+            else:
+                # Blocks were reserved before the replay; the launches read the
+                # device [position, length] pair, bounded by the capacity.
+                counters, bound = cache.graph_pos.data_ptr(), cache.graph_max_position
             stream = stream_of(x)
-            rc = run(plan, x.data_ptr(), position, stream)
+            rc = run(plan, x.data_ptr(), counters, bound, stream)
             if rc == _native.ERR_WORKSPACE:
                 # A longer context splits into partitions: the plan is set up
                 # again with a workspace at least twice the last one (nothing
                 # was launched).
-                _, need = decode_plan(1, heads, head_dim, block_size, position + 1, dtype, 0)
+                _, need = decode_plan(1, heads, head_dim, block_size, bound + 1, dtype, 0)
                 old = held["ws"]
                 init(torch.empty(max(need, 0 if old is None else 2 * old.numel()), dtype=torch.uint8, device=device))
-                rc = run(plan, x.data_ptr(), position, stream)
+                rc = run(plan, x.data_ptr(), counters, bound, stream)
             if rc:
                 check(rc, "mie_block_decode")
             return out
 
-        launch.buffers = (q, attn, h, plan, held)  # kept alive with the plan
+        launch.buffers = (q, attn, h, acc, plan, held)  # kept alive with the plan
         return launch
 
 

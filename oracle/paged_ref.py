@@ -142,6 +142,26 @@ def qkv_project_fp64(x, in_proj_weight, in_proj_bias, heads, norm_weight=None, n
     return q, k, v
 
 
+# ---- the attention half of a block for one decode token (model.py:263-268, :447)
+
+
+def attention_half_fp64(q, k, v, out_proj_weight, out_proj_bias, x, scale=None):
+    """x + out_proj(attention) for one token, in float64.
+
+    q [H, D]; k, v [H, C, D]; out_proj_weight [dim, dim] with dim = H * D;
+    out_proj_bias [dim] or None; x [dim] (the block's input, the residual).
+    The per-head attention outputs are concatenated head by head - the
+    [1, H, 1, D] -> [1, 1, dim] reshape of CachedAttention.forward
+    (model.py:267) - and projected (model.py:268), then added to x
+    (model.py:447).  Returns (out_proj output, x + it).
+    """
+    a = attention_fp64(q, k, v, scale).reshape(-1)
+    o = to_f64(out_proj_weight) @ a
+    if out_proj_bias is not None:
+        o = o + to_f64(out_proj_bias)
+    return o, to_f64(x).reshape(-1) + o
+
+
 def gather_sdpa(q, k_pool, v_pool, layer, block_table, context_len):
     """The reference's gather decode path on the CPU: PagedKVCache.read
     (model.py:186-201) then scaled_dot_product_attention (model.py:265-266).

@@ -129,14 +129,14 @@ def test_block_plan_checks_fail_before_launch():
     size = lib.mie_block_plan_bytes()
     assert 64 <= size <= 4096
     small = ctypes.create_string_buffer(size - 1)
-    args = [0] * 41  # dim .. out after (plan, plan_bytes); zeros are never dereferenced
+    args = [0] * 42  # dim .. acc after (plan, plan_bytes); zeros are never dereferenced
     args[0:5] = [64, 2, 32, 16, 0]  # dim, heads, head_dim, block_size, dtype
     rc = lib.mie_block_plan_init(small, len(small), *args)
     assert rc == 1 and b"plan needs" in lib.mie_last_error()
     plan = ctypes.create_string_buffer(size)
     rc = lib.mie_block_plan_init(plan, len(plan), *args)
     assert rc == 1 and b"null scratch" in lib.mie_last_error()
-    rc = lib.mie_block_decode(ctypes.create_string_buffer(size), 1 << 20, 5, None)
+    rc = lib.mie_block_decode(ctypes.create_string_buffer(size), 1 << 20, None, 5, None)
     assert rc == 1 and b"not initialised" in lib.mie_last_error()
 
 
@@ -147,14 +147,14 @@ def _valid_plan_args(**over):
     never dereference."""
     names = ("dim heads head_dim block_size dtype attn_ln_w attn_ln_b attn_eps w_in b_in w_out b_out k_pool v_pool "
              "sblk shead num_blocks table table_len scale q attn h ws ws_bytes moe_ln_w moe_ln_b moe_eps router w1 "
-             "b1 w2 b2 experts top_k hidden logits ids route_w hidden_act out").split()
+             "b1 w2 b2 experts top_k hidden logits ids route_w hidden_act out acc").split()
     addr = iter(range(1 << 20, 1 << 30, 1 << 16))
     args = {name: next(addr) for name in names}
     args.update(dim=64, heads=2, head_dim=32, block_size=16, dtype=0, attn_eps=1e-5, moe_eps=1e-5,
                 sblk=2 * 16 * 32, shead=16 * 32, num_blocks=8, table_len=8, scale=1.0, ws=0, ws_bytes=0,
                 experts=4, top_k=2, hidden=128)
     args.update(over)
-    assert len(args) == 41
+    assert len(args) == 42
     return [args[n] for n in names]
 
 
@@ -166,6 +166,7 @@ def _valid_plan_args(**over):
     (dict(router=0), 1, b"null pointer"),
     (dict(experts=65), 1, b"experts"),
     (dict(sblk=16 * 32), 1, b"overlap"),
+    (dict(acc=(1 << 20) + 8), 1, b"aligned"),   # the accumulator row of the four-launch form
 ])
 def test_block_plan_init_makes_every_launch_check(change, code, message):
     """A plan that one of the five launches would refuse is refused when it is
@@ -184,7 +185,33 @@ def test_block_decode_refuses_a_position_past_the_table_before_launching():
     lib = _native.lib()
     plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
     assert lib.mie_block_plan_init(plan, len(plan), *_valid_plan_args()) == 0
-    rc = lib.mie_block_decode(plan, 1 << 20, 8 * 16, None)
+    rc = lib.mie_block_decode(plan, 1 << 20, None, 8 * 16, None)
     assert rc == 1 and b"past the 8-entry block table" in lib.mie_last_error()
-    rc = lib.mie_block_decode(plan, (1 << 20) + 4, 3, None)
+    rc = lib.mie_block_decode(plan, (1 << 20) + 4, None, 3, None)
     assert rc == 1 and b"aligned" in lib.mie_last_error()
+
+
+def test_block_plan_ignores_the_accumulator_for_shapes_the_fused_attention_lacks():
+    """head_dim 96 has the five-launch form only: a plan given an accumulator
+    still initialises (and would run five launches)."""
+    lib = _native.lib()
+    plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
+    args = _valid_plan_args(dim=192, heads=2, head_dim=96, sblk=2 * 16 * 96, shead=16 * 96)
+    assert lib.mie_block_plan_init(plan, len(plan), *args) == 0, lib.mie_last_error()
+
+
+@pytest.mark.parametrize("change,code,message", [
+    (dict(dtype=1), 2, b"float32 only"),
+    (dict(head_dim=96), 2, b"head_dim 96"),
+    (dict(max_ctx=1025 * 16), 2, b"contexts up to 1024 blocks"),
+    (dict(acc=(1 << 20) + 4), 1, b"aligned"),
+    (dict(ctx=17, max_ctx=16), 1, b"outside"),
+])
+def test_attn_out_checks_fail_before_launch(change, code, message):
+    lib = _native.lib()
+    args = dict(q=1 << 20, k=2 << 20, v=3 << 20, sblk=2 * 16 * 64, shead=16 * 64, num_blocks=8, table=4 << 20,
+                table_len=8, ctx_dev=None, ctx=5, max_ctx=64, heads=2, head_dim=64, block_size=16, scale=0.125,
+                w=5 << 20, acc=6 << 20, dtype=0)
+    args.update(change)
+    rc = lib.mie_attn_out_acc(*args.values(), None)
+    assert rc == code and message in lib.mie_last_error(), lib.mie_last_error()

@@ -149,9 +149,9 @@ def test_config1_greedy_tokens_identical_across_paths():
 
 def test_cached_one_token_plan_follows_cache_and_weight_changes():
     """The eager one-token decode runs each block from a cached launch plan
-    (TransformerMoEBlock._decode_one_token).  Every decode below must equal,
-    bit for bit, the same step with the plan disabled (the per-call fused path)
-    after changing what the plan depends on: a second cache on another
+    (TransformerMoEBlock._decode_one_token).  Every decode below must equal
+    the same step with the plan disabled (the per-call fused path), to float32
+    rounding, after changing what the plan depends on: a second cache on another
     allocator, reloaded weights (new tensors, assign=True), the MoE mode, a
     module conversion, a parameter replaced by hand (with drop_decode_plan),
     and the allocator's fuse_qkv switch."""
@@ -179,8 +179,11 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
     alloc_b = model.new_block_allocator(num_blocks=24, block_size=8, attention_mode="direct")
 
     def check(factory):
-        # The plan issues the per-call path's launches with the same arguments.
-        assert torch.equal(run(factory, True), run(factory, False))
+        # The plan runs the four-launch block (attention fused with out_proj,
+        # heads summed in fixed point): float32 rounding away from the
+        # per-call five launches, far below what stale weights or a stale
+        # cache would change.
+        torch.testing.assert_close(run(factory, True), run(factory, False), rtol=1e-5, atol=1e-5)
 
     check(alloc_a.new_cache)
     assert all(b._one_token is not None and b._one_token[2] is not None for b in model.MoEBlocks)
@@ -255,7 +258,7 @@ def test_block_plans_do_not_keep_finished_caches_alive():
     finally:
         for b in model.MoEBlocks:
             del b._decode_one_token
-    assert torch.equal(got, want)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
 
 
 def test_hidden_states_is_the_callers_tensor():
@@ -275,18 +278,18 @@ def test_hidden_states_is_the_callers_tensor():
 
 
 def test_block_plan_grows_its_workspace_for_split_contexts():
-    """Past 1024 cached tokens with few heads, the decode splits the context
-    into partitions and needs a workspace: the block's launch plan
-    (mie_block_decode) refuses such a position before launching anything,
-    and the block sets the plan up again with a workspace.  Logits equal the
-    per-call fused path's bit for bit at every step, and a plan holds a
-    workspace after."""
+    """Past 2048 cached tokens the plan takes the five-launch block, and with
+    few heads the decode splits the context into partitions and needs a
+    workspace: the block's launch plan (mie_block_decode) refuses such a
+    position before launching anything, and the block sets the plan up again
+    with a workspace.  Logits equal the per-call fused path's bit for bit at
+    every step (the same five launches), and a plan holds a workspace after."""
     print_case("block plan workspace growth")
     torch.manual_seed(1)
-    cfg = dict(max_seq_length=1200, vocab_size=96, num_layers=2, hidden_dim=64, num_heads=2, num_experts=4, top_k=2)
+    cfg = dict(max_seq_length=2200, vocab_size=96, num_layers=2, hidden_dim=64, num_heads=2, num_experts=4, top_k=2)
     model = Model(ModelConfig(**cfg)).to("cuda").eval()
-    ids = torch.randint(0, cfg["vocab_size"], (1, 1030), device="cuda")
-    alloc = model.new_block_allocator(num_blocks=80, block_size=16, attention_mode="direct")
+    ids = torch.randint(0, cfg["vocab_size"], (1, 2070), device="cuda")
+    alloc = model.new_block_allocator(num_blocks=140, block_size=16, attention_mode="direct")
 
     def run(use_plan):
         blocks = list(model.MoEBlocks)
@@ -296,7 +299,7 @@ def test_block_plan_grows_its_workspace_for_split_contexts():
                 b._decode_one_token = lambda *args, **kwargs: None
         try:
             cache = alloc.new_cache()
-            out = stepwise_logits(model, ids, cache, 1020)
+            out = stepwise_logits(model, ids, cache, 2055)
             cache.free()
             return out
         finally:

@@ -5,12 +5,13 @@ Each test replays the captured step many times across block boundaries, with
 eager work of the same model (another sequence in the same block pool) and a
 device synchronization between replays, and checks every replay: its logits
 against the eager step's for the same token and position, and the greedy
-tokens against Model.generate (reference model.py:567-621).  The graph's
-decode launch is sized for the pool's capacity: at block size 16 (1280
-positions) it splits the context into 64-token partitions merged by a second
-launch, at block size 4 (320 positions) it is the one-launch workgroup form.
-The eager launch is sized for the exact length, so float32 logits agree to
-rounding, not bit for bit.
+tokens against Model.generate (reference model.py:567-621).  Each block of
+the captured step runs its launch plan with the device [position, length]
+pair, sized for the model's capacity: up to 2048 positions that is the
+four-launch block (attention fused with out_proj); at 2200 positions it is the
+five-launch block, whose decode splits the context into partitions merged by
+a second launch.  The eager launches are sized for the exact length, so
+float32 logits agree to rounding, not always bit for bit.
 """
 
 import pytest
@@ -27,16 +28,17 @@ E2E = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768,
            num_experts=8, top_k=2, ffn_dim=2048)
 
 
-def tiny_model(dtype=torch.float32):
+def tiny_model(dtype=torch.float32, max_seq_length=None):
     torch.manual_seed(0)
-    return Model(ModelConfig(**TINY)).to("cuda", dtype).eval()
+    cfg = TINY if max_seq_length is None else dict(TINY, max_seq_length=max_seq_length)
+    return Model(ModelConfig(**cfg)).to("cuda", dtype).eval()
 
 
-@pytest.mark.parametrize("block_size", [4, 16])
-def test_every_replay_matches_eager_step(block_size):
-    print_case("graph replay vs eager", block_size)
-    model = tiny_model()
-    allocator = model.new_block_allocator(num_blocks=80, block_size=block_size, attention_mode="direct")
+@pytest.mark.parametrize("block_size,max_seq_length,num_blocks", [(4, 128, 80), (16, 128, 80), (16, 2200, 140)])
+def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks):
+    print_case("graph replay vs eager", block_size, max_seq_length, num_blocks)
+    model = tiny_model(max_seq_length=max_seq_length)
+    allocator = model.new_block_allocator(num_blocks=num_blocks, block_size=block_size, attention_mode="direct")
     graphed, eager = allocator.new_cache(), allocator.new_cache()
     prompt = torch.randint(0, TINY["vocab_size"], (1, 9), device="cuda")
     with torch.no_grad():

@@ -324,3 +324,44 @@ def test_qkv_pin_rejects_planted_mistakes(broken):
     want = torch_qkv64(x, w, b, heads, nw, nb)
     got = broken(x, w, b, heads, nw, nb)
     assert not all(np.allclose(g, t, rtol=0, atol=1e-6) for g, t in zip(got, want))
+
+
+# ---- attention half: attention, head concatenation, out_proj, residual -------
+
+
+def test_attention_half_matches_torch_multihead_layout():
+    """attention_half_fp64 against torch in float64: SDPA over [1, H, C, D],
+    the [1, H, 1, D] -> [1, 1, dim] transpose/reshape CachedAttention.forward
+    does (model.py:267), F.linear with out_proj, plus x."""
+    g = torch.Generator().manual_seed(11)
+    H, C, D = 3, 9, 8
+    q, k, v = torch.randn(H, D, generator=g), torch.randn(H, C, D, generator=g), torch.randn(H, C, D, generator=g)
+    w, b, x = torch.randn(H * D, H * D, generator=g), torch.randn(H * D, generator=g), torch.randn(H * D, generator=g)
+    a = F.scaled_dot_product_attention(q.double()[None, :, None], k.double()[None], v.double()[None])
+    o = F.linear(a.transpose(1, 2).reshape(1, 1, H * D), w.double(), b.double())[0, 0]
+    got_o, got_h = ref.attention_half_fp64(q, k, v, w, b, x)
+    np.testing.assert_allclose(got_o, o.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(got_h, (x.double() + o).numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_attention_half_known_answer():
+    """One key per head: the attention is each head's value row, so with
+    W = I the output is the concatenated values, head 0 first."""
+    H, D = 2, 3
+    q = torch.ones(H, D)
+    k = torch.ones(H, 1, D)
+    v = torch.arange(H * D, dtype=torch.float64).reshape(H, 1, D)
+    o, h = ref.attention_half_fp64(q, k, v, torch.eye(H * D), None, torch.full((H * D,), 10.0))
+    np.testing.assert_array_equal(o, np.arange(H * D))
+    np.testing.assert_array_equal(h, 10 + np.arange(H * D))
+
+
+def test_attention_half_pin_rejects_a_transposed_projection():
+    g = torch.Generator().manual_seed(12)
+    H, C, D = 2, 5, 4
+    q, k, v = torch.randn(H, D, generator=g), torch.randn(H, C, D, generator=g), torch.randn(H, C, D, generator=g)
+    w, x = torch.randn(H * D, H * D, generator=g), torch.zeros(H * D)
+    a = torch.from_numpy(ref.attention_fp64(q, k, v).reshape(-1))
+    o, _ = ref.attention_half_fp64(q, k, v, w, None, x)
+    assert not np.allclose(o, (w.double().T @ a).numpy())  # a transposed operand would fail the pin
+    np.testing.assert_allclose(o, (w.double() @ a).numpy(), rtol=1e-12)
