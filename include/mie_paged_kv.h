@@ -452,7 +452,7 @@ int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_o
  *
  * with an accumulator (`acc` non-NULL, used when mie_attn_out_acc is built for
  * the shape - float32, head_dim 32, 64 or 128 - and ignored otherwise) and
- * position + 1 <= 2048, four launches:
+ * position + 1 <= 1024, four launches:
  *   mie_qkv_append(x, attn norm, in_proj, pools, block_table, position) -> q
  *   mie_attn_out_acc(q, pools, block_table, ctx = position + 1, out_proj) -> acc
  *   mie_moe_decode_block_acc(x, acc, out_proj bias, moe norm, router, experts) -> h, out

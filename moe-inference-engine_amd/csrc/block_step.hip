@@ -58,7 +58,11 @@ struct BlockPlan {
 // Contexts the four-launch form serves: each of a head's workgroups reads the
 // head's whole context, so past this length the partitioned decode (every CU
 // on one head's context) plus the separate projection launch is faster.
-constexpr int32_t kFusedMaxCtx = 2048;
+// Measured at config 1's shape (eager decode step, ms, four / five launches):
+// 64 tokens 0.338 / 0.361, 256 0.351 / 0.384, 512 0.371 / 0.407, 1024
+// 0.425 / 0.473, 1536 0.475 / 0.419, 2040 0.526 / 0.419 - past 1024 the
+// five-launch decode takes its partition form.
+constexpr int32_t kFusedMaxCtx = 1024;
 
 }  // namespace
 

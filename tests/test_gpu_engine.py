@@ -277,8 +277,32 @@ def test_hidden_states_is_the_callers_tensor():
     assert torch.equal(first, kept)
 
 
+def test_block_plan_switches_forms_at_1024_tokens():
+    """A sequence that crosses 1024 cached tokens moves from the four-launch
+    block (attention fused with out_proj) to the five-launch one mid-sequence;
+    every step's logits stay within float32 rounding of the per-call path."""
+    print_case("block plan form switch")
+    torch.manual_seed(2)
+    cfg = dict(max_seq_length=1100, vocab_size=96, num_layers=2, hidden_dim=64, num_heads=4, num_experts=4, top_k=2)
+    model = Model(ModelConfig(**cfg)).to("cuda").eval()
+    ids = torch.randint(0, cfg["vocab_size"], (1, 1040), device="cuda")
+    alloc = model.new_block_allocator(num_blocks=70, block_size=16, attention_mode="direct")
+    cache = alloc.new_cache()
+    got = stepwise_logits(model, ids, cache, 1015)
+    cache.free()
+    for b in model.MoEBlocks:
+        b.drop_decode_plan()
+        b._decode_one_token = lambda *args, **kwargs: None
+    try:
+        want = stepwise_logits(model, ids, alloc.new_cache(), 1015)
+    finally:
+        for b in model.MoEBlocks:
+            del b._decode_one_token
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-5)
+
+
 def test_block_plan_grows_its_workspace_for_split_contexts():
-    """Past 2048 cached tokens the plan takes the five-launch block, and with
+    """Past 1024 cached tokens the plan takes the five-launch block, and with
     few heads the decode splits the context into partitions and needs a
     workspace: the block's launch plan (mie_block_decode) refuses such a
     position before launching anything, and the block sets the plan up again

@@ -7,7 +7,7 @@ device synchronization between replays, and checks every replay: its logits
 against the eager step's for the same token and position, and the greedy
 tokens against Model.generate (reference model.py:567-621).  Each block of
 the captured step runs its launch plan with the device [position, length]
-pair, sized for the model's capacity: up to 2048 positions that is the
+pair, sized for the model's capacity: up to 1024 positions that is the
 four-launch block (attention fused with out_proj); at 2200 positions it is the
 five-launch block, whose decode splits the context into partitions merged by
 a second launch.  The eager launches are sized for the exact length, so
