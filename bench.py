@@ -38,7 +38,7 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
-                   "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync")
+                   "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync", "l2_reuse")
 PROBES = ROOT / "moe-inference-engine_amd" / "moe_engine" / "libmie_probes.so"
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
@@ -458,7 +458,49 @@ def probes_lib():
     lib.mie_probe_grid_barrier.argtypes = [c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_void_p, c.c_void_p,
                                            c.c_void_p, c.c_void_p, c.c_int64, c.c_void_p]
     lib.mie_probe_grid_barrier.restype = c.c_int32
+    lib.mie_probe_read_regions.argtypes = [c.c_void_p, c.c_int64, c.c_int32, c.c_int32, c.c_int32, c.c_void_p,
+                                           c.c_void_p]
+    lib.mie_probe_read_regions.restype = c.c_int32
     return lib
+
+
+def secondary_l2_reuse(torch, reps=5):
+    """Whether one launch finds what the previous launch read in L2: 256
+    workgroups each read 48 KiB (12 MiB, 1.5 MiB per XCD) after a 1 GiB read
+    has flushed the caches, then again.  Workgroup w reads region (w + shift)
+    mod 256; read first with shift 8 (the same XCD, another workgroup), 1 (a
+    neighbouring XCD) or not at all, the second read (shift 0) then hits the
+    XCD's L2, the last-level cache only, or HBM.  Best of `reps`, microseconds
+    per launch from events around it (launch overhead included)."""
+    lib = probes_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    groups, per = 256, 48 * 1024
+    buf = torch.zeros(groups * per, dtype=torch.uint8, device="cuda")
+    flush = torch.zeros(1 << 30, dtype=torch.uint8, device="cuda")
+    out = torch.empty(max(groups, (1 << 30) // per) * 256, dtype=torch.int32, device="cuda")
+
+    def read(t, shift, n=groups):
+        if lib.mie_probe_read_regions(t.data_ptr(), t.numel(), n, per, shift, out.data_ptr(), stream):
+            raise RuntimeError("mie_probe_read_regions failed")
+
+    res = {}
+    for name, shift in (("hbm", None), ("other_xcd_l2_last_level_cache", 1), ("same_xcd_l2", 8)):
+        best = None
+        for _ in range(reps):
+            read(flush, 0, (1 << 30) // per)
+            if shift is not None:
+                read(buf, shift)
+            torch.cuda.synchronize()
+            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            read(buf, 0)
+            stop.record()
+            torch.cuda.synchronize()
+            us = start.elapsed_time(stop) * 1e3
+            best = us if best is None else min(best, us)
+        res[f"{name}_us"] = round(best, 2)
+    del buf, flush
+    return res
 
 
 def secondary_grid_sync(torch, iters=2000):
@@ -679,6 +721,7 @@ def main():
             ("config1_e2e_decode", secondary_e2e),
             ("read_ceilings", secondary_read_ceilings),
             ("grid_sync", secondary_grid_sync),
+            ("l2_reuse", secondary_l2_reuse),
         ):
             if name not in chosen:
                 continue

@@ -116,3 +116,32 @@ extern "C" int32_t mie_probe_noop(int32_t groups, void* stream) {
   noop_kernel<<<groups, 256, 0, static_cast<hipStream_t>(stream)>>>();
   return hipGetLastError() == hipSuccess ? 0 : 2;
 }
+
+// L2 reuse across kernel boundaries: workgroup w reads region (w + shift) mod
+// gridDim.x of `buf` (per_group_bytes each, 16-byte loads, folded into `out`).
+// Read once with shift s and again with shift 0: the second launch hits the
+// L2 of its own XCD when s is a multiple of 8 (the dispatcher places
+// workgroup i on XCD i mod 8), only the last-level cache otherwise.
+namespace {
+__global__ __launch_bounds__(256) void read_region_kernel(const u32x4* __restrict__ buf, int32_t per_group_vec,
+                                                          int32_t shift, uint32_t* __restrict__ out) {
+  const int region = (static_cast<int>(blockIdx.x) + shift) % static_cast<int>(gridDim.x);
+  const u32x4* p = buf + static_cast<int64_t>(region) * per_group_vec;
+  uint32_t acc = 0;
+  for (int i = threadIdx.x; i < per_group_vec; i += 256) {
+    const u32x4 v = p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  out[blockIdx.x * 256 + threadIdx.x] = acc;
+}
+}  // namespace
+
+extern "C" int32_t mie_probe_read_regions(const void* buf, int64_t buf_bytes, int32_t groups, int32_t per_group_bytes,
+                                          int32_t shift, uint32_t* out, void* stream) {
+  if (!buf || !out || groups <= 0 || per_group_bytes <= 0 || per_group_bytes % 16 || shift < 0 ||
+      static_cast<int64_t>(groups) * per_group_bytes > buf_bytes)
+    return 1;
+  read_region_kernel<<<groups, 256, 0, static_cast<hipStream_t>(stream)>>>(static_cast<const u32x4*>(buf),
+                                                                         per_group_bytes / 16, shift, out);
+  return hipGetLastError() == hipSuccess ? 0 : 2;
+}
