@@ -38,7 +38,8 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
-                   "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync", "l2_reuse")
+                   "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync", "l2_reuse",
+                   "decode_timeline")
 PROBES = ROOT / "moe-inference-engine_amd" / "moe_engine" / "libmie_probes.so"
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
@@ -464,6 +465,88 @@ def probes_lib():
     return lib
 
 
+def secondary_decode_timeline(torch, launches=3):
+    """Where config 4's decode time goes: the fused step launched from the
+    probe library's copy of the decode kernels, built with per-workgroup
+    timestamps (MIE_DECODE_TIMELINE: start and end on the 100 MHz real-time
+    clock, XCD and hardware id per workgroup).  Per launch: the kernel span,
+    how many workgroups each CU ran and when each CU finished, and each
+    workgroup's read rate (its sequence's K and V bytes for one head over
+    its duration)."""
+    import ctypes
+
+    from moe_engine import _native, workloads
+
+    probe = ctypes.CDLL(str(PROBES))
+    fn = probe.mie_paged_decode_append
+    fn.restype, fn.argtypes = _native._SIGNATURES["mie_paged_decode_append"]
+    probe.mie_probe_decode_timeline.argtypes = [ctypes.c_void_p]
+    probe.mie_probe_decode_timeline.restype = ctypes.c_int32
+
+    class ProbeDecode:  # the probe's decode, every other entry point the product's
+        def __init__(self, product):
+            self._product = product
+            self.mie_paged_decode_append = fn
+
+        def __getattr__(self, name):
+            return getattr(self._product, name)
+
+    step = workloads.config4_step()
+    w = step.w
+    heads, head_dim = w.k_pool.shape[2], w.k_pool.shape[4]
+    n_wg = heads * len(w.lens)
+    buf = torch.zeros(n_wg * 4, dtype=torch.int64, device="cuda")
+    product = _native._LIB
+    _native._LIB = ProbeDecode(product)
+    try:
+        for _ in range(3):
+            step.fused()
+        if probe.mie_probe_decode_timeline(buf.data_ptr()):
+            raise RuntimeError("mie_probe_decode_timeline failed")
+        runs = []
+        for _ in range(launches):
+            buf.zero_()
+            torch.cuda.synchronize()
+            step.fused()
+            torch.cuda.synchronize()
+            runs.append(buf.view(n_wg, 4).cpu().numpy().astype("uint64"))
+        probe.mie_probe_decode_timeline(None)
+    finally:
+        _native._LIB = product
+    import numpy as np
+
+    res = []
+    for rec in runs:
+        t0, t1 = rec[:, 0].astype(np.int64), rec[:, 1].astype(np.int64)
+        base = t0.min()
+        xcd = (rec[:, 2] >> np.uint64(32)) & np.uint64(0xF)
+        hw = rec[:, 2] & np.uint64(0xFFFFFFFF)
+        cu = xcd * np.uint64(1 << 16) + ((hw >> np.uint64(8)) & np.uint64(0xFF))  # XCD, then SE/SH/CU bits
+        ctx = (rec[:, 3] & np.uint64(0xFFFFFFFF)).astype(np.int64)
+        dur_us = (t1 - t0) / 100.0
+        kv_bytes = ctx * head_dim * 2 * 2  # K and V rows of one head, bf16
+        rate = kv_bytes / np.maximum(dur_us, 1e-3) / 1e3  # GB/s
+        ends = {}
+        counts = {}
+        for c, e in zip(cu.tolist(), ((t1 - base) / 100.0).tolist()):
+            ends[c] = max(ends.get(c, 0.0), e)
+            counts[c] = counts.get(c, 0) + 1
+        cu_end = np.array(sorted(ends.values()))
+        res.append({
+            "span_us": round(float((t1.max() - base) / 100.0), 2),
+            "workgroups": int(n_wg),
+            "cus_used": len(ends),
+            "xcds_used": int(len(set(xcd.tolist()))),
+            "workgroups_per_cu": {str(k): v for k, v in sorted(
+                {n: list(counts.values()).count(n) for n in set(counts.values())}.items())},
+            "cu_finish_us_min_median_max": [round(float(cu_end[0]), 2), round(float(np.median(cu_end)), 2),
+                                            round(float(cu_end[-1]), 2)],
+            "workgroup_gbs_p10_median_p90": [round(float(np.percentile(rate, q)), 1) for q in (10, 50, 90)],
+            "sum_over_cus_of_median_rate_tbs": round(float(np.median(rate)) * len(ends) / 1e3, 2),
+        })
+    return {"launches": res, "note": "config 4 fused step (workgroup form), probe build of the decode kernels"}
+
+
 def secondary_l2_reuse(torch, reps=5):
     """Whether one launch finds what the previous launch read in L2: 256
     workgroups each read 48 KiB (12 MiB, 1.5 MiB per XCD) after a 1 GiB read
@@ -722,6 +805,7 @@ def main():
             ("read_ceilings", secondary_read_ceilings),
             ("grid_sync", secondary_grid_sync),
             ("l2_reuse", secondary_l2_reuse),
+            ("decode_timeline", secondary_decode_timeline),
         ):
             if name not in chosen:
                 continue

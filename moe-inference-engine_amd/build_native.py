@@ -6,8 +6,10 @@ compiles each csrc/*.hip with hipcc (in parallel, one object per source) and
 links the objects into moe_engine/libmie_paged.so.  The library is written to
 a temporary name first and renamed, so a process that already mapped the old
 file keeps a consistent copy.  The measurement probes bench.py runs
-(csrc/probes/*.hip: read ceilings, launch floor) go into their own
-moe_engine/libmie_probes.so, apart from the product library.
+(csrc/probes/*.hip: read ceilings, launch floor, grid waits, L2 reuse) go into
+their own moe_engine/libmie_probes.so, apart from the product library, with a
+copy of the decode kernels built with MIE_DECODE_TIMELINE (per-workgroup
+timestamps).
 """
 
 import os
@@ -51,18 +53,24 @@ def _run(cmd, verbose):
     return proc.returncode, stderr
 
 
+# The probe library also carries an instrumented copy of the decode kernels
+# (with what they call), built with MIE_DECODE_TIMELINE.
+PROBE_PRODUCT_SOURCES = ("paged_decode.hip", "kv_copy.hip", "capi.hip")
+
+
 def build(verbose: bool = True) -> Path:
     _link(sorted(CSRC.glob("*.hip")), OUTPUT, verbose)
-    _link(sorted((CSRC / "probes").glob("*.hip")), PROBE_OUTPUT, verbose)
+    probe_sources = sorted((CSRC / "probes").glob("*.hip")) + [CSRC / n for n in PROBE_PRODUCT_SOURCES]
+    _link(probe_sources, PROBE_OUTPUT, verbose, ["-DMIE_DECODE_TIMELINE"])
     return OUTPUT
 
 
-def _link(sources, output: Path, verbose: bool) -> None:
+def _link(sources, output: Path, verbose: bool, extra=()) -> None:
     tmp = output.with_name(output.name + f".tmp{os.getpid()}")
     jobs = max(1, min(len(sources), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
     with tempfile.TemporaryDirectory(prefix="mie_build_") as objdir:
         objs = [str(Path(objdir) / (src.stem + ".o")) for src in sources]
-        compiles = [[hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", obj]
+        compiles = [[hipcc(), *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", obj]
                     for src, obj in zip(sources, objs)]
         with ThreadPoolExecutor(jobs) as pool:
             results = list(pool.map(lambda c: _run(c, verbose), compiles))
