@@ -29,6 +29,8 @@
  *   mie_block_plan_init, mie_block_decode <- one TransformerMoEBlock.forward for one
  *                        decode token (model.py:446-449 with :226-269): four or
  *                        five launches above from a stored plan, one call per token
+ *   mie_block_plan_set_embedding, mie_block_decode_embed <- the embedding (model.py:558)
+ *                        and the first block, the embedding inside the QKV launch
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -504,6 +506,24 @@ int32_t mie_block_plan_init(void* plan, int64_t plan_bytes, int32_t dim, int32_t
                             void* router_logits, void* expert_ids, void* route_weights, void* hidden_act,
                             void* out, void* acc);
 int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position, void* stream);
+
+/*
+ * Layer 0 of a decode step with the embedding folded into its QKV launch
+ * (token_embedding(ids) + positional_embedding(pos), model.py:558, then the
+ * first block): mie_block_plan_set_embedding stores the token table [vocab,
+ * dim], the positional table [max_positions, dim] (both the model dtype,
+ * 16-byte aligned) and a row x_out [dim] in a plan; mie_block_decode_embed
+ * (plan, token_id, counters, position, stream) is then mie_block_decode with
+ * x = round(token_table[*token_id] + pos_table[position]) (a float32 sum
+ * rounded once, as mie_embed; NaN for an id or position outside its table),
+ * formed inside the QKV launch from the device int64 token id and stored to
+ * x_out, the block's residual.  One launch fewer than mie_embed followed by
+ * mie_block_decode, with the same results.
+ */
+int32_t mie_block_plan_set_embedding(void* plan, const void* token_table, int32_t vocab, const void* pos_table,
+                                     int32_t max_positions, void* x_out);
+int32_t mie_block_decode_embed(const void* plan, const int64_t* token_id, const int32_t* counters,
+                               int32_t position, void* stream);
 
 #ifdef __cplusplus
 }

@@ -53,6 +53,13 @@ struct BlockPlan {
   // fused attention + output projection (mie_attn_out_acc): fixed-point sums
   // [dim + 1], or NULL for the five-launch form only
   void* acc;
+  // Layer 0 with the embedding folded into its QKV launch
+  // (mie_block_plan_set_embedding): the tables and the row x is formed in.
+  const void* tok_table;
+  int32_t vocab;
+  const void* pos_table;
+  int32_t max_positions;
+  void* x_emb;
 };
 
 // Contexts the four-launch form serves: each of a head's workgroups reads the
@@ -167,12 +174,42 @@ extern "C" int32_t mie_block_plan_init(
   return MIE_OK;
 }
 
-extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position,
-                                    void* stream) {
+namespace {
+
+// The block's QKV launch: x read, or formed from the embedding tables.
+int32_t qkv(const BlockPlan& p, const mie::QkvEmbedding& emb, bool embed, const void* x, const int32_t* pos_dev,
+            int32_t position, void* stream) {
+  if (embed)
+    return mie::qkv_append_embedded(emb, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool,
+                                    p.v_pool, p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table,
+                                    p.block_table_len, pos_dev, position, p.q, p.num_heads, p.head_dim,
+                                    p.block_size, p.dtype, stream);
+  return mie_qkv_append(x, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool, p.v_pool,
+                        p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table, p.block_table_len,
+                        pos_dev, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
+}
+
+}  // namespace
+
+namespace {
+
+// x: the block's input row, or (with token_id) NULL and the row formed from
+// the plan's embedding tables by the QKV launch.
+int32_t block_decode(const void* plan, const void* x, const int64_t* token_id, const int32_t* counters,
+                     int32_t position, void* stream) {
   if (!plan) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: null plan");
   BlockPlan p;
   memcpy(&p, plan, sizeof(p));
   if (p.magic != kPlanMagic) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: plan not initialised");
+  mie::QkvEmbedding emb{};
+  if (token_id) {
+    if (!p.tok_table)
+      return mie::fail(MIE_ERR_INVALID, "mie_block_decode_embed: the plan has no embedding (mie_block_plan_set_embedding)");
+    if (reinterpret_cast<uintptr_t>(token_id) % 8)
+      return mie::fail(MIE_ERR_INVALID, "mie_block_decode_embed: misaligned token id");
+    emb = mie::QkvEmbedding{token_id, p.tok_table, p.vocab, p.pos_table, p.max_positions, p.x_emb};
+    x = p.x_emb;
+  }
   if (!x || reinterpret_cast<uintptr_t>(x) % 16 != 0 || position < 0)
     return mie::fail(MIE_ERR_INVALID, "mie_block_decode: x %p (16-byte aligned) position %d", x, position);
   if (static_cast<int64_t>(position) >= static_cast<int64_t>(p.block_table_len) * p.block_size)
@@ -193,9 +230,7 @@ extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32
   if (fused) {
     // Four launches: QKV into the pool, attention with the output projection
     // summed into acc, then the MoE half forming x + out_proj(a) itself.
-    rc = mie_qkv_append(x, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool, p.v_pool,
-                        p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table, p.block_table_len,
-                        pos_dev, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
+    rc = qkv(p, emb, token_id != nullptr, x, pos_dev, position, stream);
     if (rc != MIE_OK) return rc;
     rc = mie::attn_out_launch(p.q, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head, p.num_blocks,
                               p.block_table, p.block_table_len, ctx_dev, max_ctx, max_ctx, p.num_heads, p.head_dim,
@@ -213,9 +248,7 @@ extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32
   if (ws_need > p.workspace_bytes)
     return mie::fail(MIE_ERR_WORKSPACE, "mie_block_decode: position %d needs a %lld-byte workspace, plan has %lld",
                      position, static_cast<long long>(ws_need), static_cast<long long>(p.workspace_bytes));
-  rc = mie_qkv_append(x, p.attn_ln_w, p.attn_ln_b, p.attn_ln_eps, p.w_in, p.b_in, p.dim, p.k_pool, p.v_pool,
-                      p.pool_stride_block, p.pool_stride_head, p.num_blocks, p.block_table, p.block_table_len,
-                      pos_dev, position, p.q, p.num_heads, p.head_dim, p.block_size, p.dtype, stream);
+  rc = qkv(p, emb, token_id != nullptr, x, pos_dev, position, stream);
   if (rc != MIE_OK) return rc;
   const int64_t row = static_cast<int64_t>(p.num_heads) * p.head_dim;
   rc = mie_paged_decode(p.q, row, p.head_dim, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head,
@@ -228,4 +261,38 @@ extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32
   return mie_moe_decode_block(p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1, p.b1, p.w2, p.b2,
                               p.num_experts, p.top_k, p.dim, p.hidden, p.router_logits, p.expert_ids,
                               p.route_weights, p.hidden_act, p.out, p.dtype, stream);
+}
+
+}  // namespace
+
+extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position,
+                                    void* stream) {
+  return block_decode(plan, x, nullptr, counters, position, stream);
+}
+
+extern "C" int32_t mie_block_decode_embed(const void* plan, const int64_t* token_id, const int32_t* counters,
+                                          int32_t position, void* stream) {
+  if (!token_id) return mie::fail(MIE_ERR_INVALID, "mie_block_decode_embed: null token id");
+  return block_decode(plan, nullptr, token_id, counters, position, stream);
+}
+
+extern "C" int32_t mie_block_plan_set_embedding(void* plan, const void* token_table, int32_t vocab,
+                                                const void* pos_table, int32_t max_positions, void* x_out) {
+  if (!plan) return mie::fail(MIE_ERR_INVALID, "mie_block_plan_set_embedding: null plan");
+  BlockPlan p;
+  memcpy(&p, plan, sizeof(p));
+  if (p.magic != kPlanMagic) return mie::fail(MIE_ERR_INVALID, "mie_block_plan_set_embedding: plan not initialised");
+  const int64_t one = 0;
+  const mie::QkvEmbedding e{&one, token_table, vocab, pos_table, max_positions, x_out};
+  const int32_t rc = mie::qkv_embedding_check(e, p.dim);
+  if (rc != MIE_OK) return rc;
+  if (x_out == p.q || x_out == p.attn || x_out == p.h || x_out == p.out)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_plan_set_embedding: x_out aliases one of the plan's rows");
+  p.tok_table = token_table;
+  p.vocab = vocab;
+  p.pos_table = pos_table;
+  p.max_positions = max_positions;
+  p.x_emb = x_out;
+  memcpy(plan, &p, sizeof(p));
+  return MIE_OK;
 }

@@ -199,3 +199,26 @@ int32_t moe_decode_block_acc_check(const void* x, const void* acc, const void* b
                                    const void* router_logits, const void* expert_ids, const void* route_weights,
                                    const void* hidden_act, const void* out, int32_t dtype);
 }  // namespace mie
+
+namespace mie {
+// The embedding folded into layer 0's QKV launch: x = round(token_table[
+// *token_id] + pos_table[position]) (float32 sum, one rounding; NaN for an id
+// or position outside its table), stored to x_out by the launch for the
+// block's residual.
+struct QkvEmbedding {
+  const int64_t* token_id;  // device
+  const void* token_table;  // [vocab, dim]
+  int32_t vocab;
+  const void* pos_table;    // [max_positions, dim]
+  int32_t max_positions;
+  void* x_out;              // [dim]
+};
+int32_t qkv_embedding_check(const QkvEmbedding& e, int32_t dim);
+// mie_qkv_append with x formed from the embedding tables.
+int32_t qkv_append_embedded(const QkvEmbedding& e, const void* ln_weight, const void* ln_bias, float ln_eps,
+                            const void* w_in, const void* b_in, int32_t dim, void* k_pool, void* v_pool,
+                            int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                            const int32_t* block_table, int32_t block_table_len, const int32_t* position_dev,
+                            int32_t position, void* q_out, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                            int32_t dtype, void* stream);
+}  // namespace mie

@@ -74,6 +74,15 @@ struct QkvArgs {
   int32_t head_dim;
   mie::FastDiv bs;
   mie::ArgmaxPair* picks;  // head form: one per workgroup, or NULL for logits only
+  // QKV form with the embedding folded in (layer 0 of a decode step): x is
+  // round(token_table[*token_id] + pos_table[position]) rather than read, and
+  // workgroup 0 stores it to x_out (the block's residual).  NULL: x is read.
+  const int64_t* token_id;
+  const void* tok_table;
+  int32_t vocab;
+  const void* pos_table;
+  int32_t max_pos;
+  void* x_out;
 };
 
 template <typename DT> struct Elt;
@@ -165,7 +174,21 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   //    Rows past the end repeat the last row and are not stored.
   u32x4_t wr[R][NCH], xw[NCH], gw[NCH], gb[NCH];
   const DT* w = static_cast<const DT*>(a.w_in);
-  const DT* x = static_cast<const DT*>(a.x);
+  // Embedding folded in: x's two rows, at addresses that depend on the token
+  // id and the position (read above with the position); an id or position
+  // outside its table reads row 0 and the row becomes NaN, as mie_embed
+  // writes it.
+  const bool embed = QKV && a.tok_table != nullptr;
+  int64_t tok_id = 0;
+  bool emb_ok = true;
+  if (QKV && embed) {
+    tok_id = *a.token_id;
+    emb_ok = tok_id >= 0 && tok_id < a.vocab && pos >= 0 && pos < a.max_pos;
+  }
+  const DT* x = embed ? static_cast<const DT*>(a.tok_table) + (emb_ok ? tok_id : 0) * dim
+                      : static_cast<const DT*>(a.x);
+  const DT* xp = static_cast<const DT*>(embed ? a.pos_table : a.x) + (embed && emb_ok ? static_cast<int64_t>(pos) * dim : 0);
+  u32x4_t pw[NCH];
   const bool norm = a.ln_w != nullptr;
   const DT* ln_w = norm ? static_cast<const DT*>(a.ln_w) : x;
   const DT* ln_b = a.ln_b ? static_cast<const DT*>(a.ln_b) : x;
@@ -178,6 +201,7 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
       wr[r][c] = __builtin_nontemporal_load(
           reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(min(r0 + r, rows - 1)) * dim + ic));
     xw[c] = *reinterpret_cast<const u32x4_t*>(x + ic);
+    if (embed) pw[c] = *reinterpret_cast<const u32x4_t*>(xp + ic);
     gw[c] = *reinterpret_cast<const u32x4_t*>(ln_w + ic);
     gb[c] = *reinterpret_cast<const u32x4_t*>(ln_b + ic);
   }
@@ -216,6 +240,28 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   float y[NCH][EPV];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) E::widen(xw[c], y[c]);
+  if (embed) {
+    // x = token row + positional row, summed in float32 and rounded once
+    // (mie_embed's arithmetic); workgroup 0 keeps it as the block's residual.
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      float q[EPV];
+      E::widen(pw[c], q);
+      const bool in = (c * 64 + lane) * EPV < dim;
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) y[c][e] = in ? (emb_ok ? E::round(y[c][e] + q[e]) : NAN) : 0.f;
+    }
+    if (blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        const int i = (c * 64 + lane) * EPV;
+        if (i < dim) {
+#pragma unroll
+          for (int e = 0; e < EPV; ++e) E::store(a.x_out, i + e, y[c][e]);
+        }
+      }
+    }
+  }
   if (norm) {
     float s = 0.f;
 #pragma unroll
@@ -399,16 +445,13 @@ int32_t linear_residual_check(const void* x, const void* weight, const void* out
 
 }  // namespace mie
 
-extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
-                                  const void* w_in, const void* b_in, int32_t dim, void* k_pool, void* v_pool,
-                                  int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
-                                  const int32_t* block_table, int32_t block_table_len, const int32_t* position_dev,
-                                  int32_t position, void* q_out, int32_t num_heads, int32_t head_dim,
-                                  int32_t block_size, int32_t dtype, void* stream) {
-  const int32_t rc = mie::qkv_append_check(x, ln_weight, ln_bias, w_in, dim, k_pool, v_pool, pool_stride_block,
-                                           pool_stride_head, num_blocks, block_table, block_table_len, position_dev,
-                                           position, q_out, num_heads, head_dim, block_size, dtype);
-  if (rc != MIE_OK) return rc;
+namespace {
+
+int32_t qkv_launch(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* w_in,
+                   const void* b_in, int32_t dim, void* k_pool, void* v_pool, int64_t pool_stride_block,
+                   int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table, int32_t block_table_len,
+                   const int32_t* position_dev, int32_t position, void* q_out, int32_t num_heads, int32_t head_dim,
+                   int32_t block_size, int32_t dtype, void* stream, const mie::QkvEmbedding* embed) {
   QkvArgs a{};
   a.rows = 3 * dim;
   a.x = x;
@@ -430,9 +473,66 @@ extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const vo
   a.q_out = q_out;
   a.head_dim = head_dim;
   a.bs = mie::FastDiv::make(static_cast<uint32_t>(block_size));
+  if (embed) {
+    a.token_id = embed->token_id;
+    a.tok_table = embed->token_table;
+    a.vocab = embed->vocab;
+    a.pos_table = embed->pos_table;
+    a.max_pos = embed->max_positions;
+    a.x_out = embed->x_out;
+  }
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == MIE_DTYPE_F32) return launch<float, kQkv>(a, st);
   return launch<uint16_t, kQkv>(a, st);
+}
+
+}  // namespace
+
+namespace mie {
+
+int32_t qkv_embedding_check(const QkvEmbedding& e, int32_t dim) {
+  if (!e.token_id || !e.token_table || !e.pos_table || !e.x_out || e.vocab <= 0 || e.max_positions <= 0)
+    return mie::fail(MIE_ERR_INVALID, "embedding: null pointer, vocab %d or positions %d", e.vocab, e.max_positions);
+  if (!aligned16(e.token_table) || !aligned16(e.pos_table) || !aligned16(e.x_out))
+    return mie::fail(MIE_ERR_INVALID, "embedding: the tables and the output row must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(e.token_id) % 8) return mie::fail(MIE_ERR_INVALID, "embedding: misaligned token id");
+  (void)dim;
+  return MIE_OK;
+}
+
+int32_t qkv_append_embedded(const QkvEmbedding& e, const void* ln_weight, const void* ln_bias, float ln_eps,
+                            const void* w_in, const void* b_in, int32_t dim, void* k_pool, void* v_pool,
+                            int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                            const int32_t* block_table, int32_t block_table_len, const int32_t* position_dev,
+                            int32_t position, void* q_out, int32_t num_heads, int32_t head_dim, int32_t block_size,
+                            int32_t dtype, void* stream) {
+  // The stand-in x only passes the shared checks; the kernel reads the tables.
+  int32_t rc = qkv_append_check(e.x_out, ln_weight, ln_bias, w_in, dim, k_pool, v_pool, pool_stride_block,
+                                pool_stride_head, num_blocks, block_table, block_table_len, position_dev, position,
+                                q_out, num_heads, head_dim, block_size, dtype);
+  if (rc != MIE_OK) return rc;
+  rc = qkv_embedding_check(e, dim);
+  if (rc != MIE_OK) return rc;
+  return qkv_launch(nullptr, ln_weight, ln_bias, ln_eps, w_in, b_in, dim, k_pool, v_pool, pool_stride_block,
+                    pool_stride_head, num_blocks, block_table, block_table_len, position_dev, position, q_out,
+                    num_heads, head_dim, block_size, dtype, stream, &e);
+}
+
+}  // namespace mie
+
+extern "C" int32_t mie_qkv_append(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps,
+                                  const void* w_in, const void* b_in, int32_t dim, void* k_pool, void* v_pool,
+                                  int64_t pool_stride_block, int64_t pool_stride_head, int32_t num_blocks,
+                                  const int32_t* block_table, int32_t block_table_len, const int32_t* position_dev,
+                                  int32_t position, void* q_out, int32_t num_heads, int32_t head_dim,
+                                  int32_t block_size, int32_t dtype, void* stream) {
+  const int32_t rc = mie::qkv_append_check(x, ln_weight, ln_bias, w_in, dim, k_pool, v_pool, pool_stride_block,
+                                           pool_stride_head, num_blocks, block_table, block_table_len, position_dev,
+                                           position, q_out, num_heads, head_dim, block_size, dtype);
+  if (rc != MIE_OK) return rc;
+  return qkv_launch(x, ln_weight, ln_bias, ln_eps, w_in, b_in, dim, k_pool, v_pool, pool_stride_block,
+                    pool_stride_head, num_blocks, block_table, block_table_len, position_dev, position, q_out,
+                    num_heads, head_dim, block_size, dtype, stream, nullptr);
 }
 
 extern "C" int32_t mie_linear_residual(const void* x, const void* weight, const void* bias, const void* residual,

@@ -145,6 +145,9 @@ _SIGNATURES = {
          _c_void_p],  # accumulator (int64 [dim + 1]) or NULL
     ),
     "mie_block_decode": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plan, x, counters, pos, stream
+    "mie_block_plan_set_embedding": (
+        _i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _i32, _c_void_p]),  # plan, tables, vocab, max positions, x_out
+    "mie_block_decode_embed": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plan, token id, ...
     "mie_attn_out_acc": (
         _i32,
         [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,  # q, pools, strides, num_blocks

@@ -692,6 +692,7 @@ class TransformerMoEBlock(nn.Module):
         self.attn_norm = LayerNorm(config.hidden_dim)
         self.moe_norm = LayerNorm(config.hidden_dim)
         self._one_token = None  # (key, cache weakref, launcher or None): see _decode_one_token
+        self._embed_row = None  # layer 0's embedding row for decode_token_ids
         self.register_load_state_dict_post_hook(TransformerMoEBlock._drop_plan_after_load)
 
     def drop_decode_plan(self) -> None:
@@ -743,7 +744,7 @@ class TransformerMoEBlock(nn.Module):
         return (layer_idx, id(cache), cache.attention_mode, cache.allocator.fuse_qkv, m["moe"].mode,
                 m["attn_norm"].eps, m["moe_norm"].eps, x.dtype, x.device, x.shape[-1], _TENSOR_EPOCH[0])
 
-    def _decode_one_token(self, x, cache, layer_idx, position):
+    def _decode_one_token(self, x, cache, layer_idx, position, embed=None):
         """The block for one decode token when both fused halves apply, from
         a launch plan (mie_block_decode): four launches for contexts the fused
         attention + output projection serves, else the five of fused_decode +
@@ -759,6 +760,8 @@ class TransformerMoEBlock(nn.Module):
                 or cache.graph_ctx.data_ptr() != graph_pos.data_ptr() + 4):
             return None  # the plan reads [position, length] as one device pair
         key = self._one_token_key(x, cache, layer_idx)
+        if embed is not None:
+            key = key + (embed[1].data_ptr(), embed[1].shape[0], embed[2].data_ptr(), embed[2].shape[0])
         plan = self._one_token
         # The weak reference rules out a new cache that reuses a dead one's id;
         # the plan itself holds no reference to the cache or its pools, so a
@@ -767,12 +770,32 @@ class TransformerMoEBlock(nn.Module):
             launcher = None
             if self.attention.fused_decode_supported(x, self.attn_norm, cache) and self.moe.fused_block_supported(
                     x, self.moe_norm):
-                launcher = self._build_one_token(x, cache, layer_idx)
+                launcher = self._build_one_token(x, cache, layer_idx, embed)
             plan = self._one_token = (key, weakref.ref(cache), launcher)
-        return None if plan[2] is None else plan[2](x, cache, position)
+        if plan[2] is None:
+            return None
+        return plan[2](x, cache, position) if embed is None else plan[2].embed(embed[0], cache, position)
+
+    def decode_token_ids(self, token_ids, cache, position, token_embedding, positional_embedding):
+        """The embedding (model.py:558) and this block for one decode token,
+        with the embedding folded into the block's QKV launch
+        (mie_block_decode_embed): token_ids is an int64 [1, 1] device tensor.
+        Returns None when the block's launch plan does not apply; the caller
+        then embeds and calls the block itself."""
+        w, pw = token_embedding.weight, positional_embedding.weight
+        if not (token_ids.dtype == torch.int64 and token_ids.numel() == 1 and token_ids.is_contiguous()
+                and token_ids.device == w.device and w.is_contiguous() and pw.is_contiguous() and pw.dtype == w.dtype
+                and pw.device == w.device and w.shape[1] == pw.shape[1]):
+            return None
+        row = self._embed_row
+        if row is None or row.dtype != w.dtype or row.device != w.device or row.shape[-1] != w.shape[1]:
+            row = self._embed_row = torch.empty((1, 1, w.shape[1]), dtype=w.dtype, device=w.device)
+        # The plan is keyed on the row it forms x in; the launcher then reads
+        # the token id and the tables instead of x.
+        return self._decode_one_token(row, cache, 0, position, embed=(token_ids, w, pw))
 
 
-    def _build_one_token(self, x, cache, layer_idx):
+    def _build_one_token(self, x, cache, layer_idx, embed=None):
         """A launch plan of the block's launches (mie_block_plan_init): each
         token is then one call, mie_block_decode(plan, x, counters, position).
         The plan holds an accumulator row for the fused attention + output
@@ -841,6 +864,35 @@ class TransformerMoEBlock(nn.Module):
                 check(rc, "mie_block_decode")
             return out
 
+        if embed is not None:
+            # Layer 0 with the embedding in its QKV launch: x is formed in the
+            # row `x` (the caller's _embed_row) from the token id and tables.
+            check(lib.mie_block_plan_set_embedding(plan, embed[1].data_ptr(), embed[1].shape[0], embed[2].data_ptr(),
+                                                   embed[2].shape[0], x.data_ptr()), "mie_block_plan_set_embedding")
+            run_embed = lib.mie_block_decode_embed
+
+            def launch_embed(token_ids, cache, position):
+                if cache.graph_pos is None:
+                    cache._reserve(position + 1)
+                    counters, bound = None, position
+                else:
+                    counters, bound = cache.graph_pos.data_ptr(), cache.graph_max_position
+                stream = stream_of(token_ids)
+                rc = run_embed(plan, token_ids.data_ptr(), counters, bound, stream)
+                if rc == _native.ERR_WORKSPACE:
+                    _, need = decode_plan(1, heads, head_dim, block_size, bound + 1, dtype, 0)
+                    old = held["ws"]
+                    init(torch.empty(max(need, 0 if old is None else 2 * old.numel()), dtype=torch.uint8,
+                                     device=device))
+                    check(lib.mie_block_plan_set_embedding(plan, embed[1].data_ptr(), embed[1].shape[0],
+                                                           embed[2].data_ptr(), embed[2].shape[0], x.data_ptr()),
+                          "mie_block_plan_set_embedding")
+                    rc = run_embed(plan, token_ids.data_ptr(), counters, bound, stream)
+                if rc:
+                    check(rc, "mie_block_decode_embed")
+                return out
+
+            launch.embed = launch_embed
         launch.buffers = (q, attn, h, acc, plan, held)  # kept alive with the plan
         return launch
 
@@ -902,6 +954,19 @@ class Model(nn.Module):
         position = cache.position
         assert position + seq_len <= self.max_seq_length, "KV cache is full"
         graph_pos = getattr(cache, "graph_pos", None)
+        decode = position > 0 and seq_len == 1
+        if decode:
+            self._preflight_decode(batch)
+        if decode and batch == 1 and not torch.is_grad_enabled():
+            # One decode token: the embedding inside layer 0's QKV launch when
+            # its launch plan applies.
+            x = self.MoEBlocks[0].decode_token_ids(token_ids, cache, position, self.token_embedding,
+                                                   self.positional_embedding)
+            if x is not None:
+                for i in range(1, len(self.MoEBlocks)):
+                    x = self.MoEBlocks[i](x, cache, i, position)
+                cache.position += seq_len
+                return x
         if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
             x = embedding.embed(token_ids, graph_pos, self.token_embedding, self.positional_embedding)
         elif (batch == 1 and seq_len <= 65535 and token_ids.dtype == torch.int64 and token_ids.is_contiguous()
@@ -912,18 +977,19 @@ class Model(nn.Module):
         else:
             pos = torch.arange(position, position + seq_len, device=token_ids.device)
             x = self.token_embedding(token_ids) + self.positional_embedding(pos)
-        # A forced-direct MoE must fail before layer 0 writes K/V or reserves a
-        # block (the embedding above touches no cache).  Only mode 'direct'
-        # can fail, so the others are skipped without a call.
-        if position > 0 and seq_len == 1:
-            for block in self.MoEBlocks:
-                moe = block._modules["moe"]
-                if moe.mode == "direct":
-                    moe.preflight_direct_decode(batch_size=batch)
         for i, block in enumerate(self.MoEBlocks):
             x = block(x, cache, i, position)
         cache.position += seq_len
         return x
+
+    def _preflight_decode(self, batch):
+        """A forced-direct MoE must fail before layer 0 writes K/V or reserves
+        a block (the embedding touches no cache).  Only mode 'direct' can
+        fail, so the others are skipped without a call."""
+        for block in self.MoEBlocks:
+            moe = block._modules["moe"]
+            if moe.mode == "direct":
+                moe.preflight_direct_decode(batch_size=batch)
 
     @torch.no_grad()
     def generate(self, token_ids, max_new_tokens, temperature=1.0, top_k=None, cache=None):

@@ -334,3 +334,44 @@ def test_block_plan_grows_its_workspace_for_split_contexts():
     for b in model.MoEBlocks:
         launcher = b._one_token[2]
         assert launcher is not None and launcher.buffers[-1]["ws"] is not None
+
+
+def test_embedding_folded_into_the_first_qkv_launch():
+    """For one decode token of a float32 model (the dtype the block's launch
+    plan serves), layer 0 forms x from the token id and the two
+    embedding tables inside its QKV launch (mie_block_decode_embed) and keeps
+    it as the block's residual.  Every step's logits equal those of the
+    separate embedding launch bit for bit (the same float32 sum, rounded once),
+    the residual row equals token_embedding[id] + positional_embedding[pos] as
+    torch rounds it, and a token id outside the vocabulary makes the row NaN
+    instead of reading past the table."""
+    print_case("embedding fold")
+    torch.manual_seed(3)
+    model = Model(ModelConfig(max_seq_length=256, num_layers=2)).to("cuda").eval()
+    ids = torch.randint(0, 1000, (1, 70), device="cuda")
+    alloc = model.new_block_allocator(num_blocks=16, block_size=16, attention_mode="direct")
+    first = model.MoEBlocks[0]
+    cache = alloc.new_cache()
+    got = stepwise_logits(model, ids, cache, 50)
+    cache.free()
+    assert first._one_token[0][-4] == model.token_embedding.weight.data_ptr(), "the folded plan did not run"
+    row = first._embed_row.clone()
+    with torch.no_grad():
+        want_row = model.token_embedding(ids[:, -1:]) + model.positional_embedding.weight[69]
+    assert torch.equal(row, want_row)
+    first.decode_token_ids = lambda *args, **kwargs: None
+    try:
+        cache = alloc.new_cache()
+        want = stepwise_logits(model, ids, cache, 50)
+        cache.free()
+    finally:
+        del first.decode_token_ids
+    assert torch.equal(got, want)
+    # An id past the vocabulary: the row (and so the logits) become NaN.
+    cache = alloc.new_cache()
+    with torch.no_grad():
+        model(ids[:, :5], cache)
+        bad = torch.tensor([[model.config.vocab_size]], device="cuda")
+        out = model(bad, cache)
+    cache.free()
+    assert torch.isnan(first._embed_row).all() and torch.isnan(out).all()
