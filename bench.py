@@ -39,7 +39,7 @@ METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
                    "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync", "l2_reuse",
-                   "decode_timeline")
+                   "decode_timeline", "atomic_sum")
 PROBES = ROOT / "moe-inference-engine_amd" / "moe_engine" / "libmie_probes.so"
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
@@ -462,6 +462,8 @@ def probes_lib():
     lib.mie_probe_read_regions.argtypes = [c.c_void_p, c.c_int64, c.c_int32, c.c_int32, c.c_int32, c.c_void_p,
                                            c.c_void_p]
     lib.mie_probe_read_regions.restype = c.c_int32
+    lib.mie_probe_atomic_sum.argtypes = [c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_void_p, c.c_void_p]
+    lib.mie_probe_atomic_sum.restype = c.c_int32
     return lib
 
 
@@ -622,6 +624,51 @@ def secondary_grid_sync(torch, iters=2000):
                 us = start.elapsed_time(stop) * 1e3 / iters
                 best = us if best is None else min(best, us)
             res[f"g{groups}_{name}"] = {"us_per_barrier": round(best, 3), "stale_reads": bad}
+    return res
+
+
+def secondary_atomic_sum(torch, outputs=768):
+    """What summing every workgroup's partial vector (768 values, config 1's
+    width) across workgroups costs with device-scope atomics
+    (csrc/probes/atomic_sum.hip): 128-512 workgroups adding into 1-16 copies
+    of the vector (workgroup g into copy g % copies) as exact int64
+    fixed-point or float32 sums, against plain stores of the partials.
+    Device time per launch (best of five runs of 300 back-to-back launches),
+    each sum checked against the exact total."""
+    import numpy as np
+
+    lib = probes_lib()
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def expected(groups):
+        g = np.arange(groups)[:, None]
+        i = np.arange(outputs)[None, :]
+        return (((((g * 131 + i * 7) & 255) - 128) / 256.0) * 2.0 ** 32).astype(np.int64).sum(0)
+
+    res = {}
+    for groups in (128, 256, 512):
+        for mode, name, copies_list in ((3, "stores", (1,)), (0, "int64", (1, 2, 4, 8, 16)), (2, "f32", (1, 4))):
+            for copies in copies_list:
+                rows = groups if mode == 3 else copies
+                acc = torch.zeros(rows * outputs, dtype=torch.float32 if mode == 2 else torch.int64, device="cuda")
+
+                def call(mode=mode, groups=groups, copies=copies, acc=acc):
+                    if lib.mie_probe_atomic_sum(mode, groups, outputs, copies, acc.data_ptr(), stream):
+                        raise RuntimeError("mie_probe_atomic_sum failed")
+
+                call()
+                torch.cuda.synchronize()
+                host = acc.view(rows, outputs).cpu()
+                if mode == 2:  # multiples of 2^-8 summed exactly in float32
+                    exact = np.array_equal(host.double().numpy().sum(0) * 2.0 ** 32, expected(groups))
+                else:
+                    exact = np.array_equal(host.numpy().sum(0), expected(groups))
+                best = None
+                for _ in range(5):
+                    us = timed_us(torch, call, iters=300, warmup=20)
+                    best = us if best is None else min(best, us)
+                key = f"g{groups}_{name}" + ("" if mode == 3 else f"_copies{copies}")
+                res[key] = {"us": round(best, 3), "exact": bool(exact)}
     return res
 
 
@@ -806,6 +853,7 @@ def main():
             ("grid_sync", secondary_grid_sync),
             ("l2_reuse", secondary_l2_reuse),
             ("decode_timeline", secondary_decode_timeline),
+            ("atomic_sum", secondary_atomic_sum),
         ):
             if name not in chosen:
                 continue

@@ -22,9 +22,10 @@
 // (which on MI355X needs an L2 writeback per publishing workgroup) and no
 // second launch.  The consumer (the MoE W1 launch of the same block,
 // mie_moe_decode_block_acc) forms h = x + (float(acc) * 2^-32 + b_out), and
-// its W2 launch clears acc for the next token.  A value of 2^31 or more in magnitude
-// (or not a number) cannot be held: such a partial sets acc[dim] instead, and
-// the consumer then writes NaN.
+// its W2 launch clears acc for the next token.  A partial of 2^31 / H or
+// more in magnitude (or not a number) is not added - the sum of the H heads'
+// partials could leave int64 - but sets acc[dim] instead, and the consumer
+// then writes NaN.
 //
 // Work decomposition: grid (8 * R * ceil(H / 8)) workgroups of 4 waves.  The
 // hardware dispatches workgroup i to XCD i mod 8, so workgroup (8 j + x) is
@@ -56,7 +57,6 @@ constexpr int kBatch = 8;         // wave loads of K (and of V) per memory round
 // with plain K/V loads 5.6 us, 2 with plain loads 5.7 us.
 constexpr int kRowSteps = 3;
 constexpr float kFix = 4294967296.0f;  // 2^32
-constexpr float kFixLimit = 2147483648.0f;  // |y| < 2^31
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -80,6 +80,7 @@ struct AttnOutArgs {
   int32_t R;  // row blocks per head
   int32_t rows_per_block;
   unsigned long long* acc;  // [dim + 1]
+  float fix_limit;  // |y| below this: the sum over the H heads stays inside int64
 };
 
 template <int D>
@@ -249,7 +250,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
     const int row = row0 + (s * kWaves + wave) * TPL + g;
     const float y = mie::group_sum<LPT>(dot4(wv[s], av, 0.f));
     if (lane % LPT == 0 && row < row_end) {
-      if (fabsf(y) < kFixLimit) {
+      if (fabsf(y) < a.fix_limit) {
         const long long fx = llrintf(y * kFix);
         atomicAdd(a.acc + row, static_cast<unsigned long long>(fx));
       } else {
@@ -312,6 +313,7 @@ int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, i
   a.w = static_cast<const float*>(w_out);
   a.dim = num_heads * head_dim;
   a.acc = static_cast<unsigned long long*>(acc);
+  a.fix_limit = 2147483648.0f / static_cast<float>(num_heads);  // H partials of |y| * 2^32 < 2^63 / H
   const int tpl = 64 / (head_dim / 4);
   a.rows_per_block = kWaves * tpl * kRowSteps;
   a.R = (a.dim + a.rows_per_block - 1) / a.rows_per_block;

@@ -136,6 +136,28 @@ def test_attn_out_adds_into_the_accumulator_and_flags_blocks_outside_the_pool():
     assert int(flagged[768]) != 0
 
 
+def test_attn_out_flags_partials_whose_head_sum_could_leave_int64():
+    """Each of the H heads adds one partial per row, so a partial is added
+    only below 2^31 / H in magnitude (the sum of H of them, times 2^32, stays
+    inside int64).  With V all ones every head's attention output is 1, so
+    y = W_out[i, h*D : (h+1)*D] . 1 = 64 w for a constant W_out = w: at
+    w = 5e6 (y = 3.2e8, above 2^31 / 12 = 1.8e8, below 2^31) the flag is set
+    - twelve such partials would wrap the sum - and at w = 5e5 the rows hold
+    12 * round(y * 2^32) exactly."""
+    print_case("attn_out int64 bound")
+    w = make_workload([40], num_heads=12, head_dim=64, block_size=16, dtype=torch.float32, seed=5)
+    w.v_pool.fill_(1.0)
+    for value, flagged in ((5e6, True), (5e5, False)):
+        w_out = torch.full((768, 768), value, device="cuda")
+        acc = torch.zeros(769, dtype=torch.int64, device="cuda")
+        attn_out(w, 0, w_out, acc)
+        torch.cuda.synchronize()
+        assert (int(acc[768]) != 0) == flagged
+        if not flagged:
+            got = acc[:768].double() * FIX
+            assert torch.allclose(got, torch.full_like(got, 12 * 64 * value), rtol=1e-6)
+
+
 def moe_inputs(dim, hidden, experts, seed):
     g = torch.Generator(device="cuda").manual_seed(seed)
     r = lambda *shape, s=1.0: torch.randn(*shape, generator=g, device="cuda") * s  # noqa: E731
