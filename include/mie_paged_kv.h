@@ -84,7 +84,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 12
+#define MIE_ABI_VERSION 13
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -506,6 +506,13 @@ int32_t mie_block_plan_init(void* plan, int64_t plan_bytes, int32_t dim, int32_t
                             void* router_logits, void* expert_ids, void* route_weights, void* hidden_act,
                             void* out, void* acc);
 int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position, void* stream);
+/*
+ * The number of launches mie_block_decode issues for `position` (the largest
+ * position, with counters): 4 (attention fused with out_proj), 5, or 6 when
+ * the decode splits the context and merges its partials.  Negative
+ * (-MIE_ERR_*) for a bad plan or position.  Issues nothing.
+ */
+int32_t mie_block_plan_launches(const void* plan, int32_t position);
 
 /*
  * Layer 0 of a decode step with the embedding folded into its QKV launch

@@ -265,6 +265,23 @@ int32_t block_decode(const void* plan, const void* x, const int64_t* token_id, c
 
 }  // namespace
 
+extern "C" int32_t mie_block_plan_launches(const void* plan, int32_t position) {
+  if (!plan) return -mie::fail(MIE_ERR_INVALID, "mie_block_plan_launches: null plan");
+  BlockPlan p;
+  memcpy(&p, plan, sizeof(p));
+  if (p.magic != kPlanMagic) return -mie::fail(MIE_ERR_INVALID, "mie_block_plan_launches: plan not initialised");
+  if (position < 0) return -mie::fail(MIE_ERR_INVALID, "mie_block_plan_launches: position %d", position);
+  const int32_t max_ctx = position + 1;
+  if (p.acc && max_ctx <= kFusedMaxCtx &&
+      (static_cast<int64_t>(max_ctx) + p.block_size - 1) / p.block_size <= mie::kAttnOutMaxBlocks)
+    return 4;
+  int64_t ws_need = 0;
+  const int32_t rc = mie_paged_decode_plan(1, p.num_heads, p.head_dim, p.block_size, max_ctx, p.dtype, 0, nullptr,
+                                           &ws_need);
+  if (rc != MIE_OK) return -rc;
+  return ws_need > 0 ? 6 : 5;  // a split context adds the partials' merge launch
+}
+
 extern "C" int32_t mie_block_decode(const void* plan, const void* x, const int32_t* counters, int32_t position,
                                     void* stream) {
   return block_decode(plan, x, nullptr, counters, position, stream);

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -145,6 +145,7 @@ _SIGNATURES = {
          _c_void_p],  # accumulator (int64 [dim + 1]) or NULL
     ),
     "mie_block_decode": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plan, x, counters, pos, stream
+    "mie_block_plan_launches": (_i32, [_c_void_p, _i32]),  # plan, position
     "mie_block_plan_set_embedding": (
         _i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _i32, _c_void_p]),  # plan, tables, vocab, max positions, x_out
     "mie_block_decode_embed": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plan, token id, ...

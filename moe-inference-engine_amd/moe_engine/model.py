@@ -893,6 +893,7 @@ class TransformerMoEBlock(nn.Module):
                 return out
 
             launch.embed = launch_embed
+        launch.plan = plan
         launch.buffers = (q, attn, h, acc, plan, held)  # kept alive with the plan
         return launch
 

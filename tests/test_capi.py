@@ -193,11 +193,33 @@ def test_block_decode_refuses_a_position_past_the_table_before_launching():
 
 def test_block_plan_ignores_the_accumulator_for_shapes_the_fused_attention_lacks():
     """head_dim 96 has the five-launch form only: a plan given an accumulator
-    still initialises (and would run five launches)."""
+    still initialises, and runs five launches at every position (six where
+    the decode splits the context)."""
     lib = _native.lib()
     plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
     args = _valid_plan_args(dim=192, heads=2, head_dim=96, sblk=2 * 16 * 96, shead=16 * 96)
     assert lib.mie_block_plan_init(plan, len(plan), *args) == 0, lib.mie_last_error()
+    assert lib.mie_block_plan_launches(plan, 0) == 5
+    assert lib.mie_block_plan_launches(plan, 100) == 5
+
+
+def test_block_plan_launch_count_follows_the_form():
+    """head_dim 32 with an accumulator: four launches up to 1024 cached
+    tokens, then the five-launch form, six once the two-head decode splits
+    its context (workspace needed); without the accumulator always the
+    five-launch form.  Bad plans and positions are refused."""
+    lib = _native.lib()
+    plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
+    assert lib.mie_block_plan_init(plan, len(plan), *_valid_plan_args(table_len=200, num_blocks=200)) == 0
+    assert lib.mie_block_plan_launches(plan, 0) == 4
+    assert lib.mie_block_plan_launches(plan, 1023) == 4
+    assert lib.mie_block_plan_launches(plan, 1024) in (5, 6)
+    assert lib.mie_block_plan_launches(plan, 3000) == 6
+    plain = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
+    assert lib.mie_block_plan_init(plain, len(plain), *_valid_plan_args(acc=0)) == 0
+    assert lib.mie_block_plan_launches(plain, 0) == 5
+    assert lib.mie_block_plan_launches(plan, -1) == -1
+    assert lib.mie_block_plan_launches(ctypes.create_string_buffer(len(plan)), 0) == -1
 
 
 @pytest.mark.parametrize("change,code,message", [

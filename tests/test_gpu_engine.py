@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from conftest import print_case
+from moe_engine import _native
 from moe_engine.model import Model, ModelConfig
 
 pytestmark = pytest.mark.gpu
@@ -147,7 +148,13 @@ def test_config1_greedy_tokens_identical_across_paths():
     assert diff < 1e-2
 
 
-def test_cached_one_token_plan_follows_cache_and_weight_changes():
+# head_dim 32: the block plan takes the four-launch form (attention fused with
+# out_proj), which TINY's head_dim 4 lacks.
+TINY_FUSED = dict(TINY, hidden_dim=64, num_heads=2)
+
+
+@pytest.mark.parametrize("cfg,launches", [(TINY, 5), (TINY_FUSED, 4)], ids=["five_launch", "four_launch"])
+def test_cached_one_token_plan_follows_cache_and_weight_changes(cfg, launches):
     """The eager one-token decode runs each block from a cached launch plan
     (TransformerMoEBlock._decode_one_token).  Every decode below must equal
     the same step with the plan disabled (the per-call fused path), to float32
@@ -155,10 +162,10 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
     allocator, reloaded weights (new tensors, assign=True), the MoE mode, a
     module conversion, a parameter replaced by hand (with drop_decode_plan),
     and the allocator's fuse_qkv switch."""
-    print_case("cached one-token plan")
+    print_case("cached one-token plan", launches)
     torch.manual_seed(0)
-    model = Model(ModelConfig(**TINY)).to("cuda").eval()
-    ids = torch.randint(0, TINY["vocab_size"], (1, 12), device="cuda")
+    model = Model(ModelConfig(**cfg)).to("cuda").eval()
+    ids = torch.randint(0, cfg["vocab_size"], (1, 12), device="cuda")
 
     def run(cache_factory, use_plan):
         blocks = list(model.MoEBlocks)
@@ -187,6 +194,8 @@ def test_cached_one_token_plan_follows_cache_and_weight_changes():
 
     check(alloc_a.new_cache)
     assert all(b._one_token is not None and b._one_token[2] is not None for b in model.MoEBlocks)
+    lib = _native.lib()
+    assert all(lib.mie_block_plan_launches(b._one_token[2].plan, 11) == launches for b in model.MoEBlocks)
     check(alloc_b.new_cache)
     check(alloc_a.new_cache)
     # New parameter tensors at new addresses.
@@ -279,17 +288,23 @@ def test_hidden_states_is_the_callers_tensor():
 
 def test_block_plan_switches_forms_at_1024_tokens():
     """A sequence that crosses 1024 cached tokens moves from the four-launch
-    block (attention fused with out_proj) to the five-launch one mid-sequence;
+    block (attention fused with out_proj; head_dim 32) to the five-launch one
+    mid-sequence (the two-head decode then splits its context: six launches);
     every step's logits stay within float32 rounding of the per-call path."""
     print_case("block plan form switch")
     torch.manual_seed(2)
-    cfg = dict(max_seq_length=1100, vocab_size=96, num_layers=2, hidden_dim=64, num_heads=4, num_experts=4, top_k=2)
+    cfg = dict(max_seq_length=1100, vocab_size=96, num_layers=2, hidden_dim=64, num_heads=2, num_experts=4, top_k=2)
     model = Model(ModelConfig(**cfg)).to("cuda").eval()
     ids = torch.randint(0, cfg["vocab_size"], (1, 1040), device="cuda")
     alloc = model.new_block_allocator(num_blocks=70, block_size=16, attention_mode="direct")
     cache = alloc.new_cache()
     got = stepwise_logits(model, ids, cache, 1015)
     cache.free()
+    lib = _native.lib()
+    for b in model.MoEBlocks:
+        plan = b._one_token[2].plan
+        assert lib.mie_block_plan_launches(plan, 1015) == 4 and lib.mie_block_plan_launches(plan, 1023) == 4
+        assert lib.mie_block_plan_launches(plan, 1024) >= 5 and lib.mie_block_plan_launches(plan, 1038) >= 5
     for b in model.MoEBlocks:
         b.drop_decode_plan()
         b._decode_one_token = lambda *args, **kwargs: None
