@@ -69,6 +69,7 @@ class GraphedDecoder:
         self.partition_tokens = partition_tokens
         self.graph = None
         self._graph_out = None
+        self._plans = None
         self.logits = None
         self.next_token = None
         self.replays = 0
@@ -131,6 +132,11 @@ class GraphedDecoder:
                     # host position its forward advanced.
                     cache.position = position
                     self.graph = graph
+                    # The replays use the blocks' launch plans' rows,
+                    # accumulators and workspaces as captured; a block keeps
+                    # one plan, which a decode on another cache (or a change
+                    # of the block) replaces, so the decoder holds them.
+                    self._plans = [block._one_token for block in self.model.MoEBlocks]
             else:
                 self.graph.replay()
                 cache.position += 1

@@ -28,16 +28,26 @@ E2E = dict(max_seq_length=1024, vocab_size=50257, num_layers=12, hidden_dim=768,
            num_experts=8, top_k=2, ffn_dim=2048)
 
 
-def tiny_model(dtype=torch.float32, max_seq_length=None):
+def tiny_model(dtype=torch.float32, max_seq_length=None, **over):
     torch.manual_seed(0)
-    cfg = TINY if max_seq_length is None else dict(TINY, max_seq_length=max_seq_length)
+    cfg = dict(TINY, **over)
+    if max_seq_length is not None:
+        cfg["max_seq_length"] = max_seq_length
     return Model(ModelConfig(**cfg)).to("cuda", dtype).eval()
 
 
-@pytest.mark.parametrize("block_size,max_seq_length,num_blocks", [(4, 128, 80), (16, 128, 80), (16, 2200, 140)])
-def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks):
-    print_case("graph replay vs eager", block_size, max_seq_length, num_blocks)
-    model = tiny_model(max_seq_length=max_seq_length)
+# (hidden_dim, num_heads): head_dim 32 has the four-launch block (attention
+# fused with out_proj) up to 1024 positions; TINY's head_dim 4 only the
+# five-launch one.
+@pytest.mark.parametrize("block_size,max_seq_length,num_blocks,hidden_dim,num_heads,launches", [
+    (4, 128, 80, 64, 2, 4),
+    (16, 128, 80, 64, 2, 4),
+    (16, 128, 80, 32, 8, 5),
+    (16, 2200, 140, 64, 2, 6),  # the two-head decode splits 2200 positions: partitions + merge
+])
+def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks, hidden_dim, num_heads, launches):
+    print_case("graph replay vs eager", block_size, max_seq_length, num_blocks, hidden_dim, num_heads)
+    model = tiny_model(max_seq_length=max_seq_length, hidden_dim=hidden_dim, num_heads=num_heads)
     allocator = model.new_block_allocator(num_blocks=num_blocks, block_size=block_size, attention_mode="direct")
     graphed, eager = allocator.new_cache(), allocator.new_cache()
     prompt = torch.randint(0, TINY["vocab_size"], (1, 9), device="cuda")
@@ -64,6 +74,45 @@ def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks)
     graphed.free()
     eager.free()
     assert len(allocator.free_blocks) == allocator.num_blocks
+
+
+def test_replays_keep_the_captured_plans_alive():
+    """The captured step points at the block plans' rows, accumulators and
+    workspaces.  After capture every block's plan is dropped, and the freed
+    memory is handed out again (torch's small blocks of the rows' and the
+    accumulator's sizes, filled with junk), while eager steps on another
+    cache build new plans.  The replays must still give the eager step's
+    logits: the decoder holds the plans it captured."""
+    import gc
+
+    print_case("graph keeps its plans")
+    model = tiny_model(hidden_dim=64, num_heads=2)
+    allocator = model.new_block_allocator(num_blocks=80, block_size=16, attention_mode="direct")
+    graphed, eager = allocator.new_cache(), allocator.new_cache()
+    prompt = torch.randint(0, TINY["vocab_size"], (1, 9), device="cuda")
+    junk = []
+    with torch.no_grad():
+        first = model(prompt, graphed)[:, -1]
+        model(prompt, eager)
+        decoder = GraphedDecoder(model, graphed)
+        token = first.argmax(-1, keepdim=True)
+        decoder.prime(token)
+        for step in range(12):
+            got = decoder.step()  # step 0 runs eagerly and captures
+            got_logits = decoder.logits.clone()
+            if step == 1:
+                for block in model.MoEBlocks:
+                    block.drop_decode_plan()
+                gc.collect()
+                junk = [torch.full((n,), -7, dtype=torch.int64, device="cuda") for n in (64, 128) for _ in range(4096)]
+            want = model(token, eager)[:, -1]
+            torch.cuda.synchronize()
+            torch.testing.assert_close(got_logits, want, atol=2e-5, rtol=2e-5, msg=lambda m: f"step {step}: {m}")
+            token = want.argmax(-1, keepdim=True)
+            assert torch.equal(got, token), f"step {step}"
+    del junk
+    graphed.free()
+    eager.free()
 
 
 def test_generate_graphed_matches_generate():
