@@ -18,6 +18,7 @@ import pytest
 import torch
 
 from conftest import print_case
+from moe_engine import _native
 from moe_engine.graphs import GraphedDecoder, generate_graphed
 from moe_engine.model import Model, ModelConfig
 
@@ -70,6 +71,12 @@ def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks,
             assert torch.equal(got, token), f"step {step}"
             assert graphed.position == eager.position
     assert decoder.replays == 99
+    # The form the captured blocks took, for the capture's position bound.
+    bound = min(max_seq_length, num_blocks * block_size) - 1
+    lib = _native.lib()
+    for plan in decoder._plans:
+        assert plan is not None and plan[2] is not None
+        assert lib.mie_block_plan_launches(plan[2].plan, bound) == launches
     assert graphed.block_table != eager.block_table
     graphed.free()
     eager.free()
