@@ -25,7 +25,7 @@ else uses Model.generate.
 import torch
 
 from moe_engine import paged_attention, projection
-from moe_engine.model import EOS_TOKEN_ID, PagedKVCache
+from moe_engine.model import _TENSOR_EPOCH, EOS_TOKEN_ID, PagedKVCache
 
 
 class GraphedDecoder:
@@ -70,6 +70,7 @@ class GraphedDecoder:
         self.graph = None
         self._graph_out = None
         self._plans = None
+        self._epoch = None  # _TENSOR_EPOCH at capture
         self.logits = None
         self.next_token = None
         self.replays = 0
@@ -112,6 +113,11 @@ class GraphedDecoder:
         if cache.position >= self.model.max_seq_length:
             raise RuntimeError("KV cache is full")
         cache._reserve(cache.position + 1)
+        if self.graph is not None and self._epoch != _TENSOR_EPOCH[0]:
+            # A tensor the captured step reads was replaced (a conversion, an
+            # assigning load, a parameter swapped with drop_decode_plan):
+            # run eagerly and capture again.
+            self.graph = self._graph_out = self._plans = None
         self._graph_mode(True)
         try:
             if self.graph is None:
@@ -137,6 +143,7 @@ class GraphedDecoder:
                     # one plan, which a decode on another cache (or a change
                     # of the block) replaces, so the decoder holds them.
                     self._plans = [block._one_token for block in self.model.MoEBlocks]
+                    self._epoch = _TENSOR_EPOCH[0]
             else:
                 self.graph.replay()
                 cache.position += 1

@@ -40,14 +40,15 @@ EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
 MOE_MODES = ("auto", "direct", "reference")
 
-# A block's one-token launch plan (TransformerMoEBlock._decode_one_token) holds
-# raw device addresses of parameters, buffers and expert storages.  Every
-# operation that can put a new tensor in their place inside the modules below -
-# device / dtype conversion (_apply), assignment of a parameter, buffer or
-# submodule (which load_state_dict(assign=True) and the expert repacking go
-# through) - advances this epoch, and a plan built under an earlier epoch is
-# rebuilt before its next use.  Writing through .data or in place keeps the
-# addresses, so it needs nothing.
+# A block's one-token launch plan (TransformerMoEBlock._decode_one_token) and a
+# captured decode step (moe_engine.graphs) hold raw device addresses of
+# parameters, buffers and expert storages.  Every operation that can put a new
+# tensor in their place inside the modules below - device / dtype conversion
+# (_apply), assignment of a parameter, buffer or submodule (which
+# load_state_dict(assign=True) and the expert repacking go through) - advances
+# this epoch, and a plan or captured step made under an earlier epoch is made
+# again before its next use.  Writing in place keeps the addresses, so it needs
+# nothing.
 _TENSOR_EPOCH = [0]
 
 
@@ -84,6 +85,11 @@ class Linear(_TracksReplacement, nn.Linear):
 
 class LayerNorm(_TracksReplacement, nn.LayerNorm):
     """nn.LayerNorm whose tensor replacements invalidate launch plans."""
+
+
+class Embedding(_TracksReplacement, nn.Embedding):
+    """nn.Embedding whose tensor replacements invalidate launch plans (the
+    first block's plan reads both tables) and captured decode steps."""
 
 
 @dataclass
@@ -700,8 +706,11 @@ class TransformerMoEBlock(nn.Module):
         new one.  Conversions (.to(), .float(), ...), loads and assignments of
         tensors or submodules anywhere in the block invalidate the plan by
         themselves (_TENSOR_EPOCH); code that swaps a tensor's storage some
-        other way (param.data = ...) calls this."""
+        other way (param.data = ...) calls this; it also advances the epoch, so
+        every other plan and captured decode step built on the old tensors is
+        rebuilt before its next use."""
         self._one_token = None
+        _tensors_replaced()
 
     @staticmethod
     def _drop_plan_after_load(module, _incompatible_keys) -> None:
@@ -903,8 +912,8 @@ class Model(nn.Module):
         super().__init__()
         self.config = config
         self.max_seq_length = config.max_seq_length
-        self.token_embedding = nn.Embedding(config.vocab_size, config.hidden_dim)
-        self.positional_embedding = nn.Embedding(config.max_seq_length, config.hidden_dim)
+        self.token_embedding = Embedding(config.vocab_size, config.hidden_dim)
+        self.positional_embedding = Embedding(config.max_seq_length, config.hidden_dim)
         self.output_projection = Linear(config.hidden_dim, config.vocab_size)
         self.MoEBlocks = nn.ModuleList(TransformerMoEBlock(config) for _ in range(config.num_layers))
         self.final_norm = LayerNorm(config.hidden_dim)

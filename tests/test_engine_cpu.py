@@ -388,10 +388,24 @@ def test_submodule_changes_advance_the_plan_epoch():
         lambda: block.attn_norm.float(),
         lambda: setattr(block.attention.out_proj, "weight", torch.nn.Parameter(torch.zeros(32, 32))),
         lambda: setattr(block.moe_norm, "bias", torch.nn.Parameter(torch.zeros(32))),
+        # The embedding tables (the first block's plan and a captured decode
+        # step read them) and a plan dropped by hand.
+        lambda: setattr(model.positional_embedding, "weight", torch.nn.Parameter(torch.zeros(128, 32))),
+        lambda: model.token_embedding.float(),
+        lambda: model.load_state_dict({k: v.clone() for k, v in model.state_dict().items()}, assign=True),
+        lambda: block.drop_decode_plan(),
     ):
         before = model_mod._TENSOR_EPOCH[0]
         change()
         assert model_mod._TENSOR_EPOCH[0] > before
+    # Decoding leaves the epoch alone (a plan or a captured step built for it stays valid).
+    before = model_mod._TENSOR_EPOCH[0]
+    with torch.no_grad():
+        cache = model.new_block_allocator(num_blocks=8, block_size=4).new_cache()
+        model(torch.tensor([[1, 2, 3]]), cache)
+        model(torch.tensor([[4]]), cache)
+    assert model_mod._TENSOR_EPOCH[0] == before
     # State-dict names and module types the reference's callers check are unchanged.
     assert isinstance(block.attn_norm, torch.nn.LayerNorm) and isinstance(block.moe.router, torch.nn.Linear)
+    assert isinstance(model.token_embedding, torch.nn.Embedding)
     assert "MoEBlocks.0.attention.out_proj.weight" in model.state_dict()

@@ -122,6 +122,44 @@ def test_replays_keep_the_captured_plans_alive():
     eager.free()
 
 
+def test_replaced_weights_are_captured_again():
+    """A captured step reads the weights' addresses.  After the weights are
+    replaced - an assigning load, then a parameter swapped by hand with
+    drop_decode_plan - the next step captures again, and its logits follow
+    the new weights (against the eager step on another cache)."""
+    print_case("graph recaptures after replacement")
+    model = tiny_model(hidden_dim=64, num_heads=2)
+    allocator = model.new_block_allocator(num_blocks=80, block_size=16, attention_mode="direct")
+    graphed, eager = allocator.new_cache(), allocator.new_cache()
+    prompt = torch.randint(0, TINY["vocab_size"], (1, 9), device="cuda")
+    with torch.no_grad():
+        first = model(prompt, graphed)[:, -1]
+        model(prompt, eager)
+        decoder = GraphedDecoder(model, graphed)
+        token = first.argmax(-1, keepdim=True)
+        decoder.prime(token)
+        captures = 0
+        for step in range(9):
+            if step == 3:
+                model.load_state_dict({k: v.clone() * 0.5 for k, v in model.state_dict().items()}, assign=True)
+            if step == 6:
+                norm = model.MoEBlocks[1].attn_norm
+                norm.weight.data = norm.weight.detach() * 2  # a new tensor behind the same parameter
+                model.MoEBlocks[1].drop_decode_plan()
+            replays = decoder.replays
+            got = decoder.step()
+            captures += decoder.replays == replays
+            got_logits = decoder.logits.clone()
+            want = model(token, eager)[:, -1]
+            torch.cuda.synchronize()
+            torch.testing.assert_close(got_logits, want, atol=2e-5, rtol=2e-5, msg=lambda m: f"step {step}: {m}")
+            token = want.argmax(-1, keepdim=True)
+            assert torch.equal(got, token), f"step {step}"
+        assert captures == 3 and decoder.replays == 6
+    graphed.free()
+    eager.free()
+
+
 def test_generate_graphed_matches_generate():
     print_case("generate_graphed")
     model = tiny_model()
