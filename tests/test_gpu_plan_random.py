@@ -1,0 +1,101 @@
+"""Drawn model shapes through the block launch plans, against the per-call
+fused path and a graph replay.
+
+Each case draws a float32 model (width, heads, so head_dim 32, 64, 96 or 128;
+experts, top-k, expert width), a block size and a prompt, prefills, then
+decodes a few tokens through Model.forward with the plans (the embedding in
+the first block's QKV launch, the four- or five-launch block by head_dim and
+context) and with the plans switched off (each half its own fused launches,
+a separate embedding).  Logits must agree to float32 rounding of the
+different summation orders: rtol / atol 1e-4, the reference's float32 bound
+for paged against contiguous attention (tests/test_paged_attention.py:148).
+Some cases start past 1024 cached tokens, where the plan takes the
+five-launch block (and, with few heads, a split context and a workspace).
+The greedy tokens of a graphed decode must equal Model.generate's.
+"""
+
+import random
+
+import pytest
+import torch
+
+from conftest import print_case
+from moe_engine import _native
+from moe_engine.graphs import generate_graphed
+from moe_engine.model import Model, ModelConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def draw(seed):
+    rng = random.Random(seed)
+    head_dim = rng.choice([32, 64, 96, 128])
+    heads = rng.choice([1, 2, 3, 4, 6])
+    long = rng.random() < 0.3
+    return dict(
+        hidden_dim=head_dim * heads,
+        num_heads=heads,
+        num_layers=rng.choice([1, 2, 3]),
+        num_experts=rng.choice([2, 4, 8]),
+        top_k=None,  # drawn below, at most the experts
+        ffn_dim=rng.choice([64, 128, 256, 512]),
+        vocab_size=rng.choice([97, 256, 1000]),
+        block_size=rng.choice([1, 4, 16, 32]),
+        prompt=rng.randint(1020, 1100) if long else rng.randint(1, 60),
+        decode=rng.randint(3, 8),
+        top_k_draw=rng.random(),
+    )
+
+
+CASES = list(range(24))
+
+
+@pytest.mark.parametrize("seed", CASES)
+def test_plans_match_the_per_call_path(seed):
+    c = draw(seed)
+    top_k = 1 + int(c["top_k_draw"] * min(c["num_experts"], 4))
+    top_k = min(top_k, c["num_experts"])
+    cfg = dict(max_seq_length=c["prompt"] + c["decode"] + 1, vocab_size=c["vocab_size"], num_layers=c["num_layers"],
+               hidden_dim=c["hidden_dim"], num_heads=c["num_heads"], num_experts=c["num_experts"], top_k=top_k,
+               ffn_dim=c["ffn_dim"])
+    print_case("plan random", seed, cfg, "block", c["block_size"], "prompt", c["prompt"], "decode", c["decode"])
+    torch.manual_seed(seed)
+    model = Model(ModelConfig(**cfg)).to("cuda").eval()
+    ids = torch.randint(0, c["vocab_size"], (1, c["prompt"] + c["decode"]), device="cuda")
+    blocks = -(-(c["prompt"] + c["decode"] + 1) // c["block_size"]) + 2
+    alloc = model.new_block_allocator(num_blocks=blocks, block_size=c["block_size"], attention_mode="direct")
+
+    def run(plans):
+        saved = [b._decode_one_token for b in model.MoEBlocks]
+        if not plans:
+            for b in model.MoEBlocks:
+                b._decode_one_token = lambda *args, **kwargs: None
+        try:
+            cache = alloc.new_cache()
+            with torch.no_grad():
+                model(ids[:, : c["prompt"]], cache)
+                out = [model(ids[:, t : t + 1], cache)[:, -1] for t in range(c["prompt"], ids.shape[1])]
+            cache.free()
+            return torch.stack(out, 1)
+        finally:
+            for b, f in zip(model.MoEBlocks, saved):
+                b._decode_one_token = f
+
+    got = run(True)
+    plan = model.MoEBlocks[0]._one_token
+    assert plan is not None and plan[2] is not None, "the block plan did not run"
+    launches = _native.lib().mie_block_plan_launches(plan[2].plan, ids.shape[1] - 1)
+    fused_shape = c["hidden_dim"] // c["num_heads"] in (32, 64, 128)
+    assert (launches == 4) == (fused_shape and ids.shape[1] <= 1024)
+    want = run(False)
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
+    # The same model decoding greedily from a HIP graph.
+    if c["prompt"] <= 60:
+        prompt = ids[0, : c["prompt"]]
+        cache = alloc.new_cache()
+        eager = model.generate(prompt, max_new_tokens=c["decode"], temperature=0, cache=cache)
+        cache.free()
+        cache = alloc.new_cache()
+        graphed = generate_graphed(model, prompt, c["decode"], cache)
+        cache.free()
+        assert torch.equal(graphed, eager)
