@@ -832,6 +832,7 @@ class TransformerMoEBlock(nn.Module):
         acc = torch.zeros(dim + 1, dtype=torch.int64, device=device)
         plan = ctypes.create_string_buffer(lib.mie_block_plan_bytes())
         held = {}  # the split-context workspace the plan points at
+        tables = None if embed is None else (embed[1], embed[2])  # token and positional tables
 
         def init(ws):
             held["ws"] = ws
@@ -847,11 +848,20 @@ class TransformerMoEBlock(nn.Module):
                 moe._router_logits.data_ptr(), moe._expert_ids.data_ptr(), moe._route_weights.data_ptr(),
                 moe._expert_hidden.data_ptr(), moe._direct_out.data_ptr(), acc.data_ptr(),
             ), "mie_block_plan_init")
+            if tables is not None:
+                # Layer 0 with the embedding in its QKV launch: x is formed in
+                # the row `x` (the block's _embed_row) from the token id and
+                # the tables.
+                w, pw = tables
+                check(lib.mie_block_plan_set_embedding(plan, w.data_ptr(), w.shape[0], pw.data_ptr(), pw.shape[0],
+                                                       x.data_ptr()), "mie_block_plan_set_embedding")
 
         init(None)
-        run = lib.mie_block_decode
 
-        def launch(x, cache, position):
+        def run(fn, arg, cache, position, stream):
+            """One call of the plan.  A longer context splits into partitions:
+            the call then fails before launching anything, and the plan is set
+            up again with a workspace at least twice the last one."""
             if cache.graph_pos is None:
                 cache._reserve(position + 1)
                 counters, bound = None, position
@@ -859,50 +869,28 @@ class TransformerMoEBlock(nn.Module):
                 # Blocks were reserved before the replay; the launches read the
                 # device [position, length] pair, bounded by the capacity.
                 counters, bound = cache.graph_pos.data_ptr(), cache.graph_max_position
-            stream = stream_of(x)
-            rc = run(plan, x.data_ptr(), counters, bound, stream)
+            rc = fn(plan, arg, counters, bound, stream)
             if rc == _native.ERR_WORKSPACE:
-                # A longer context splits into partitions: the plan is set up
-                # again with a workspace at least twice the last one (nothing
-                # was launched).
                 _, need = decode_plan(1, heads, head_dim, block_size, bound + 1, dtype, 0)
                 old = held["ws"]
                 init(torch.empty(max(need, 0 if old is None else 2 * old.numel()), dtype=torch.uint8, device=device))
-                rc = run(plan, x.data_ptr(), counters, bound, stream)
+                rc = fn(plan, arg, counters, bound, stream)
             if rc:
                 check(rc, "mie_block_decode")
             return out
 
-        if embed is not None:
-            # Layer 0 with the embedding in its QKV launch: x is formed in the
-            # row `x` (the caller's _embed_row) from the token id and tables.
-            check(lib.mie_block_plan_set_embedding(plan, embed[1].data_ptr(), embed[1].shape[0], embed[2].data_ptr(),
-                                                   embed[2].shape[0], x.data_ptr()), "mie_block_plan_set_embedding")
-            run_embed = lib.mie_block_decode_embed
+        decode, decode_embed = lib.mie_block_decode, lib.mie_block_decode_embed
 
-            def launch_embed(token_ids, cache, position):
-                if cache.graph_pos is None:
-                    cache._reserve(position + 1)
-                    counters, bound = None, position
-                else:
-                    counters, bound = cache.graph_pos.data_ptr(), cache.graph_max_position
-                stream = stream_of(token_ids)
-                rc = run_embed(plan, token_ids.data_ptr(), counters, bound, stream)
-                if rc == _native.ERR_WORKSPACE:
-                    _, need = decode_plan(1, heads, head_dim, block_size, bound + 1, dtype, 0)
-                    old = held["ws"]
-                    init(torch.empty(max(need, 0 if old is None else 2 * old.numel()), dtype=torch.uint8,
-                                     device=device))
-                    check(lib.mie_block_plan_set_embedding(plan, embed[1].data_ptr(), embed[1].shape[0],
-                                                           embed[2].data_ptr(), embed[2].shape[0], x.data_ptr()),
-                          "mie_block_plan_set_embedding")
-                    rc = run_embed(plan, token_ids.data_ptr(), counters, bound, stream)
-                if rc:
-                    check(rc, "mie_block_decode_embed")
-                return out
+        def launch(x, cache, position):
+            return run(decode, x.data_ptr(), cache, position, stream_of(x))
 
+        def launch_embed(token_ids, cache, position):
+            return run(decode_embed, token_ids.data_ptr(), cache, position, stream_of(token_ids))
+
+        if tables is not None:
             launch.embed = launch_embed
         launch.plan = plan
+        launch.held = held
         launch.buffers = (q, attn, h, acc, plan, held)  # kept alive with the plan
         return launch
 
@@ -967,7 +955,7 @@ class Model(nn.Module):
         decode = position > 0 and seq_len == 1
         if decode:
             self._preflight_decode(batch)
-        if decode and batch == 1 and not torch.is_grad_enabled():
+        if decode and batch == 1 and len(self.MoEBlocks) and not torch.is_grad_enabled():
             # One decode token: the embedding inside layer 0's QKV launch when
             # its launch plan applies.
             x = self.MoEBlocks[0].decode_token_ids(token_ids, cache, position, self.token_embedding,

@@ -348,7 +348,7 @@ def test_block_plan_grows_its_workspace_for_split_contexts():
     assert torch.equal(run(True), run(False))
     for b in model.MoEBlocks:
         launcher = b._one_token[2]
-        assert launcher is not None and launcher.buffers[-1]["ws"] is not None
+        assert launcher is not None and launcher.held["ws"] is not None
 
 
 def test_embedding_folded_into_the_first_qkv_launch():
