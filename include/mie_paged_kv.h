@@ -458,7 +458,8 @@ int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_o
  *   mie_qkv_append(x, attn norm, in_proj, pools, block_table, position) -> q
  *   mie_attn_out_acc(q, pools, block_table, ctx = position + 1, out_proj) -> acc
  *   mie_moe_decode_block_acc(x, acc, out_proj bias, moe norm, router, experts) -> h, out
- * otherwise five:
+ * otherwise five (six when the decode splits the context into partitions
+ * and merges them):
  *   mie_qkv_append(...)                                                   -> q
  *   mie_paged_decode(q, pools, block_table, ctx = position + 1)           -> attn
  *   mie_linear_residual(attn, out_proj, residual x)                        -> h
