@@ -14,6 +14,7 @@ five-launch block (and, with few heads, a split context and a workspace).
 The greedy tokens of a graphed decode must equal Model.generate's.
 """
 
+import os
 import random
 
 import pytest
@@ -47,7 +48,8 @@ def draw(seed):
     )
 
 
-CASES = list(range(24))
+# MIE_PLAN_RANDOM_CASES widens the sweep for a one-off run.
+CASES = list(range(int(os.environ.get("MIE_PLAN_RANDOM_CASES", "24"))))
 
 
 @pytest.mark.parametrize("seed", CASES)
