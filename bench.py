@@ -594,7 +594,8 @@ def secondary_grid_sync(torch, iters=2000):
     workgroups meeting at a device counter `iters` times, in three memory
     disciplines (csrc/probes/grid_sync.hip): device-scope relaxed data
     (mode 1: no L2 writeback), one agent release/acquire per workgroup
-    (mode 2), and __threadfence in every thread (mode 0).  Best of five
+    (mode 2), both (mode 3: the release has no dirty L2 lines to write
+    back), and __threadfence in every thread (mode 0).  Best of five
     launches, microseconds per barrier, with the count of stale reads seen
     by the checks."""
     lib = probes_lib()
@@ -604,7 +605,8 @@ def secondary_grid_sync(torch, iters=2000):
         counter = torch.zeros(1, dtype=torch.int32, device="cuda")
         flags = torch.zeros(2, dtype=torch.int32, device="cuda")
         vec = torch.zeros(2 * groups * 256, dtype=torch.float32, device="cuda")
-        for mode, name in ((1, "device_scope_data"), (2, "release_acquire_per_group"), (0, "threadfence_all")):
+        for mode, name in ((1, "device_scope_data"), (2, "release_acquire_per_group"),
+                           (3, "device_scope_data_release_acquire"), (0, "threadfence_all")):
             best, bad = None, 0
             for _ in range(5):
                 counter.zero_()

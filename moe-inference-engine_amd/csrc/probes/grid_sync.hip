@@ -11,7 +11,10 @@
 //      barrier: no L2 writeback;
 //   2  plain stores; one agent-scope release fence per workgroup before its
 //      arrival and one acquire fence after the wait (one L2 writeback per
-//      workgroup).
+//      workgroup);
+//   3  the data as in mode 1 (device-scope atomic stores and loads) and the
+//      fences as in mode 2: formally ordered, with nothing dirty in the L2
+//      for the release to write back.
 // Every wait is bounded: a wave that spins past the limit raises a global
 // flag, every waiter leaves once the flag is up, and the launch reports it,
 // so the grid always drains.
@@ -36,17 +39,17 @@ __global__ __launch_bounds__(256) void barrier_kernel(unsigned* counter, float* 
     float* buf = vec + static_cast<size_t>(it & 1) * G * per_group;
     for (int i = threadIdx.x; i < per_group; i += blockDim.x) {
       const float v = static_cast<float>((it * 7 + blockIdx.x * 3 + i) & 0xffff);
-      if (MODE == 1) {
+      if (MODE == 1 || MODE == 3) {
         __hip_atomic_store(&buf[blockIdx.x * per_group + i], v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         buf[blockIdx.x * per_group + i] = v;
       }
     }
     if (MODE == 0) __threadfence();
-    if (MODE == 1) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if (MODE == 1 || MODE == 3) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
     if (threadIdx.x == 0) {
-      if (MODE == 2) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      if (MODE == 2 || MODE == 3) __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
       __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const unsigned target = static_cast<unsigned>(it + 1) * G;
       long spins = 0;
@@ -58,19 +61,20 @@ __global__ __launch_bounds__(256) void barrier_kernel(unsigned* counter, float* 
         if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) break;
         __builtin_amdgcn_s_sleep(1);
       }
-      if (MODE == 2) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      if (MODE == 2 || MODE == 3) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) stop = 1;
     }
     __syncthreads();
     if (MODE == 0) __threadfence();
-    if (MODE == 1) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    if (MODE == 1 || MODE == 3) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
     if (stop) break;
     for (int j = threadIdx.x; j < 32; j += blockDim.x) {
       const int src = (blockIdx.x + 1 + (j >> 2) * 37) % G;
       const int i = (j & 3) * (per_group / 4);
       const float want = static_cast<float>((it * 7 + src * 3 + i) & 0xffff);
       float* p = &buf[src * per_group + i];
-      const float got = MODE == 1 ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : *p;
+      const float got = MODE == 1 || MODE == 3 ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                               : *p;
       wrong += got != want;
     }
   }
@@ -94,6 +98,7 @@ extern "C" int32_t mie_probe_grid_barrier(int32_t mode, int32_t groups, int32_t 
     case 0: fn = reinterpret_cast<const void*>(&barrier_kernel<0>); break;
     case 1: fn = reinterpret_cast<const void*>(&barrier_kernel<1>); break;
     case 2: fn = reinterpret_cast<const void*>(&barrier_kernel<2>); break;
+    case 3: fn = reinterpret_cast<const void*>(&barrier_kernel<3>); break;
     default: return 1;
   }
   const hipError_t e = hipLaunchCooperativeKernel(fn, dim3(groups), dim3(256), args, 0,
