@@ -24,6 +24,7 @@ attention out_proj, in_proj xavier, the experts' two linears each, router), so
 a seeded model has the reference's weights.
 """
 
+import collections
 import ctypes
 import math
 import weakref
@@ -50,6 +51,10 @@ MOE_MODES = ("auto", "direct", "reference")
 # again before its next use.  Writing in place keeps the addresses, so it needs
 # nothing.
 _TENSOR_EPOCH = [0]
+
+# One-token launch plans a block keeps (the most recently used): sequences
+# decoded in turn each find theirs.
+_KEPT_PLANS = 4
 
 
 def _tensors_replaced() -> None:
@@ -697,7 +702,8 @@ class TransformerMoEBlock(nn.Module):
         self.moe = MoEFeedForward(config.hidden_dim, config.expert_hidden_dim, config.num_experts, config.top_k)
         self.attn_norm = LayerNorm(config.hidden_dim)
         self.moe_norm = LayerNorm(config.hidden_dim)
-        self._one_token = None  # (key, cache weakref, launcher or None): see _decode_one_token
+        self._one_token = None  # the last plan used: (key, cache weakref, launcher or None); see _decode_one_token
+        self._plans = collections.OrderedDict()  # key -> plan, the most recently used last
         self._embed_row = None  # layer 0's embedding row for decode_token_ids
         self.register_load_state_dict_post_hook(TransformerMoEBlock._drop_plan_after_load)
 
@@ -710,6 +716,7 @@ class TransformerMoEBlock(nn.Module):
         every other plan and captured decode step built on the old tensors is
         rebuilt before its next use."""
         self._one_token = None
+        self._plans.clear()
         _tensors_replaced()
 
     @staticmethod
@@ -774,13 +781,22 @@ class TransformerMoEBlock(nn.Module):
         plan = self._one_token
         # The weak reference rules out a new cache that reuses a dead one's id;
         # the plan itself holds no reference to the cache or its pools, so a
-        # finished sequence's pools can be freed.
+        # finished sequence's pools can be freed.  The last few plans are kept,
+        # so sequences decoded in turn do not rebuild them every token.
         if plan is None or plan[0] != key or plan[1]() is not cache:
-            launcher = None
-            if self.attention.fused_decode_supported(x, self.attn_norm, cache) and self.moe.fused_block_supported(
-                    x, self.moe_norm):
-                launcher = self._build_one_token(x, cache, layer_idx, embed)
-            plan = self._one_token = (key, weakref.ref(cache), launcher)
+            plan = self._plans.get(key)
+            if plan is None or plan[1]() is not cache:
+                launcher = None
+                if self.attention.fused_decode_supported(x, self.attn_norm, cache) and \
+                        self.moe.fused_block_supported(x, self.moe_norm):
+                    launcher = self._build_one_token(x, cache, layer_idx, embed)
+                plan = (key, weakref.ref(cache), launcher)
+                self._plans[key] = plan
+                if len(self._plans) > _KEPT_PLANS:
+                    self._plans.popitem(last=False)
+            else:
+                self._plans.move_to_end(key)
+            self._one_token = plan
         if plan[2] is None:
             return None
         return plan[2](x, cache, position) if embed is None else plan[2].embed(embed[0], cache, position)

@@ -390,3 +390,42 @@ def test_embedding_folded_into_the_first_qkv_launch():
         out = model(bad, cache)
     cache.free()
     assert torch.isnan(first._embed_row).all() and torch.isnan(out).all()
+
+
+def test_sequences_decoded_in_turn_keep_their_plans():
+    """Two sequences decoded in turn, one token each, find their own launch
+    plans again - a block keeps its last few - instead of rebuilding them
+    every token; each sequence's logits equal those it gets decoded alone,
+    bit for bit (the same launches)."""
+    print_case("plans of sequences in turn")
+    torch.manual_seed(4)
+    model = Model(ModelConfig(**TINY_FUSED)).to("cuda").eval()
+    alloc = model.new_block_allocator(num_blocks=40, block_size=4, attention_mode="direct")
+    ids = torch.randint(0, TINY_FUSED["vocab_size"], (2, 30), device="cuda")
+    builds = []
+    for b in model.MoEBlocks:
+        build = b._build_one_token
+        b._build_one_token = lambda *args, _build=build, **kwargs: builds.append(1) or _build(*args, **kwargs)
+    try:
+        alone = []
+        for s in range(2):
+            cache = alloc.new_cache()
+            alone.append(stepwise_logits(model, ids[s : s + 1], cache, 6))
+            cache.free()
+        builds.clear()
+        caches = [alloc.new_cache(), alloc.new_cache()]
+        steps = [[], []]
+        with torch.no_grad():
+            for s in range(2):
+                steps[s].append(model(ids[s : s + 1, :6], caches[s])[:, -1])
+            for t in range(6, 30):
+                for s in range(2):
+                    steps[s].append(model(ids[s : s + 1, t : t + 1], caches[s])[:, -1])
+        for s in range(2):
+            assert torch.equal(torch.stack(steps[s], 1), alone[s])
+        assert len(builds) == 2 * len(model.MoEBlocks), f"{len(builds)} plan builds for two sequences"
+        for c in caches:
+            c.free()
+    finally:
+        for b in model.MoEBlocks:
+            b.__dict__.pop("_build_one_token", None)
