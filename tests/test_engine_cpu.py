@@ -155,6 +155,19 @@ def test_generate_validates_arguments():
             engine.generate(prompt, **args)
 
 
+def test_cache_follows_model_dtype():
+    """The contiguous cache (the comparator) takes the model's dtype too."""
+    engine = make_engine().double()
+    ids = torch.randint(0, 96, (1, 8))
+    with torch.no_grad():
+        full = engine(ids, engine.new_cache())
+        cache = engine.new_cache()
+        engine(ids[:, :4], cache)
+        step = engine(ids[:, 4:5], cache)
+    assert full.dtype == torch.float64 and step.dtype == torch.float64
+    torch.testing.assert_close(step[:, -1], full[:, 4])
+
+
 def test_paged_cache_follows_model_dtype():
     engine = make_engine().double()
     ids = torch.randint(0, 96, (1, 8))
