@@ -150,10 +150,9 @@ __device__ __forceinline__ float reduce_rows(const float (&v)[R], int lane) {
 // c), and normalises with wave reductions: no LDS and no barrier, so all of a
 // wave's global reads - weights, x, norm, bias, residual - are issued together
 // and the launch waits on one memory round trip.
-template <typename DT, int NCH, int MODE, int R, bool EMBED = false>
+template <typename DT, int NCH, int MODE, int R>
 __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   constexpr bool QKV = MODE == kQkv;
-  static_assert(QKV || !EMBED, "the embedding is folded into the QKV form only");
   using E = Elt<DT>;
   constexpr int EPV = E::kPerVec;
   const int wave = threadIdx.x >> 6;
@@ -162,24 +161,10 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   const int rows = a.rows;
   const int r0 = (blockIdx.x * kWavesPerGroup + wave) * R;
 
-  // 0. QKV: the token's position (and, with the embedding folded in, its id),
-  //    read first with vector loads: scalar loads complete out of order, so
-  //    the wait the kernel's own argument loads need would also wait for
-  //    them and hold the weight loads back a memory round.  Both are read
-  //    unconditionally - an absent one from a stand-in address, its value
-  //    dropped - since a load under a branch is waited for at the join.  The
-  //    block-table read and the embedding rows that depend on them are
-  //    issued after the weight loads, so they overlap them.
+  // 0. QKV: the token's position, read first; the block-table read that
+  //    depends on it is issued after the weight loads, so both overlap them.
   int pos = -1;
-  constexpr bool embed = EMBED;
-  int64_t tok_raw = 0;
-  if constexpr (QKV) {
-    const int32_t* pp = a.position_dev ? a.position_dev : a.block_table;
-    const int32_t dev_pos = __hip_atomic_load(const_cast<int32_t*>(pp), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if constexpr (EMBED)
-      tok_raw = __hip_atomic_load(const_cast<int64_t*>(a.token_id), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    pos = a.position_dev ? dev_pos : a.position;
-  }
+  if constexpr (QKV) pos = a.position_dev ? *a.position_dev : a.position;
 
   // 1. All global reads, unconditional so that they go out together: a load
   //    under a branch whose result merges with a default at the join makes
@@ -189,12 +174,24 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   //    Rows past the end repeat the last row and are not stored.
   u32x4_t wr[R][NCH], xw[NCH], gw[NCH], gb[NCH];
   const DT* w = static_cast<const DT*>(a.w_in);
+  // Embedding folded in: x's two rows, at addresses that depend on the token
+  // id and the position (read above with the position); an id or position
+  // outside its table reads row 0 and the row becomes NaN, as mie_embed
+  // writes it.
+  const bool embed = QKV && a.tok_table != nullptr;
+  int64_t tok_id = 0;
+  bool emb_ok = true;
+  if (QKV && embed) {
+    tok_id = *a.token_id;
+    emb_ok = tok_id >= 0 && tok_id < a.vocab && pos >= 0 && pos < a.max_pos;
+  }
+  const DT* x = embed ? static_cast<const DT*>(a.tok_table) + (emb_ok ? tok_id : 0) * dim
+                      : static_cast<const DT*>(a.x);
+  const DT* xp = static_cast<const DT*>(embed ? a.pos_table : a.x) + (embed && emb_ok ? static_cast<int64_t>(pos) * dim : 0);
+  u32x4_t pw[NCH];
   const bool norm = a.ln_w != nullptr;
-  // Stand-ins for absent norm parameters: the weights, which do not depend on
-  // the token.
-  const DT* ln_w = norm ? static_cast<const DT*>(a.ln_w) : w;
-  const DT* ln_b = a.ln_b ? static_cast<const DT*>(a.ln_b) : w;
-  // The weights first: they depend on nothing.
+  const DT* ln_w = norm ? static_cast<const DT*>(a.ln_w) : x;
+  const DT* ln_b = a.ln_b ? static_cast<const DT*>(a.ln_b) : x;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = (c * 64 + lane) * EPV;
@@ -203,31 +200,11 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
     for (int r = 0; r < R; ++r)
       wr[r][c] = __builtin_nontemporal_load(
           reinterpret_cast<const u32x4_t*>(w + static_cast<int64_t>(min(r0 + r, rows - 1)) * dim + ic));
-  }
-  // With the embedding folded in, the rows below are at addresses that depend
-  // on the token id and the position: nothing that waits for those two may
-  // move above the weight loads.
-  if constexpr (EMBED) __builtin_amdgcn_sched_barrier(0);
-  // Embedding folded in: x's two rows; an id or position outside its table
-  // reads row 0 and the row becomes NaN, as mie_embed writes it.
-  const int64_t tok_id = embed ? tok_raw : 0;
-  const bool emb_ok = !embed || (tok_id >= 0 && tok_id < a.vocab && pos >= 0 && pos < a.max_pos);
-  const DT* x = embed ? static_cast<const DT*>(a.tok_table) + (emb_ok ? tok_id : 0) * dim
-                      : static_cast<const DT*>(a.x);
-  const DT* xp = static_cast<const DT*>(embed ? a.pos_table : a.x) + (embed && emb_ok ? static_cast<int64_t>(pos) * dim : 0);
-  u32x4_t pw[NCH];
-#pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int i = (c * 64 + lane) * EPV;
-    const int ic = i < dim ? i : 0;
     xw[c] = *reinterpret_cast<const u32x4_t*>(x + ic);
-    if constexpr (EMBED) pw[c] = *reinterpret_cast<const u32x4_t*>(xp + ic);
+    if (embed) pw[c] = *reinterpret_cast<const u32x4_t*>(xp + ic);
     gw[c] = *reinterpret_cast<const u32x4_t*>(ln_w + ic);
     gb[c] = *reinterpret_cast<const u32x4_t*>(ln_b + ic);
   }
-  // Keep the scheduler from hoisting work that waits for the position (its
-  // move to a scalar register for the block-table slot) above these loads.
-  if constexpr (QKV) __builtin_amdgcn_sched_barrier(0);
   constexpr int kGroup = 64 / R;  // lanes that finish one row
   const int r_store = r0 + lane / kGroup;
   const bool storing = lane % kGroup == 0 && r_store < rows;
@@ -263,7 +240,7 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   float y[NCH][EPV];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) E::widen(xw[c], y[c]);
-  if constexpr (EMBED) {
+  if (embed) {
     // x = token row + positional row, summed in float32 and rounded once
     // (mie_embed's arithmetic); workgroup 0 keeps it as the block's residual.
 #pragma unroll
@@ -370,9 +347,9 @@ __device__ __forceinline__ void projection_body(const QkvArgs& a) {
   E::store(is_v ? a.v_pool : a.k_pool, phys * a.sblk + h * a.shead + static_cast<int64_t>(slot) * a.head_dim + d, out);
 }
 
-template <typename DT, int NCH, bool EMBED>
+template <typename DT, int NCH>
 __global__ __launch_bounds__(256) void qkv_append_kernel(QkvArgs a) {
-  projection_body<DT, NCH, kQkv, kRowsPerWave, EMBED>(a);
+  projection_body<DT, NCH, kQkv, kRowsPerWave>(a);
 }
 
 template <typename DT, int NCH>
@@ -399,11 +376,7 @@ int32_t launch(const QkvArgs& a, hipStream_t st) {
 #define MIE_PROJ_CASE(N)                                             \
   case N:                                                            \
     if (MODE == kQkv) {                                              \
-      if (a.tok_table) {                                             \
-        qkv_append_kernel<DT, N, true><<<groups, 256, 0, st>>>(a);   \
-      } else {                                                       \
-        qkv_append_kernel<DT, N, false><<<groups, 256, 0, st>>>(a);  \
-      }                                                              \
+      qkv_append_kernel<DT, N><<<groups, 256, 0, st>>>(a);           \
     } else if (MODE == kLinear) {                                    \
       linear_residual_kernel<DT, N><<<groups, 256, 0, st>>>(a);      \
     } else {                                                         \
