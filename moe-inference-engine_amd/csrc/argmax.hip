@@ -71,12 +71,6 @@ __global__ __launch_bounds__(kThreads) void argmax_kernel(const float* __restric
 __global__ __launch_bounds__(kThreads) void argmax_pairs_kernel(const mie::ArgmaxPair* __restrict__ p, int n,
                                                                 int limit, int64_t* out, int32_t* advance,
                                                                 int n_advance) {
-  // The counters to advance, read with the pairs rather than after the merge
-  // (one memory round fewer); nothing else in the launch touches them.  The
-  // read is unconditional (a load under a branch is waited for at its join):
-  // with nothing to advance it re-reads the first pair and is dropped.
-  const int32_t* adv_src = n_advance > 0 ? advance : reinterpret_cast<const int32_t*>(p);
-  const int32_t adv = adv_src[static_cast<int>(threadIdx.x) < n_advance ? threadIdx.x : 0];
   float v = -INFINITY;
   int idx = INT_MAX;
   for (int j0 = 0; j0 < n; j0 += kPairsPerThread * kThreads) {
@@ -91,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void argmax_pairs_kernel(const mie::Argma
   }
   block_argmax(v, idx);
   if (threadIdx.x == 0) *out = idx < limit ? idx : 0;
-  if (threadIdx.x < n_advance) advance[threadIdx.x] = adv + 1;
+  if (threadIdx.x < n_advance) advance[threadIdx.x] += 1;
 }
 
 }  // namespace
