@@ -474,7 +474,10 @@ def secondary_decode_timeline(torch, launches=3):
     clock, XCD and hardware id per workgroup).  Per launch: the kernel span,
     how many workgroups each CU ran and when each CU finished, and each
     workgroup's read rate (its sequence's K and V bytes for one head over
-    its duration)."""
+    its duration); and, over the workgroups of sequences longer than 4096
+    tokens, when each of the 16 waves finished its slice as a fraction of its
+    workgroup's duration (mean per wave index, and the median spread between
+    the first and the last wave)."""
     import ctypes
 
     from moe_engine import _native, workloads
@@ -497,7 +500,8 @@ def secondary_decode_timeline(torch, launches=3):
     w = step.w
     heads, head_dim = w.k_pool.shape[2], w.k_pool.shape[4]
     n_wg = heads * len(w.lens)
-    buf = torch.zeros(n_wg * 4, dtype=torch.int64, device="cuda")
+    words = 20  # the probe build's record: 4 words, then 16 wave end times
+    buf = torch.zeros(n_wg * words, dtype=torch.int64, device="cuda")
     product = _native._LIB
     _native._LIB = ProbeDecode(product)
     try:
@@ -511,7 +515,7 @@ def secondary_decode_timeline(torch, launches=3):
             torch.cuda.synchronize()
             step.fused()
             torch.cuda.synchronize()
-            runs.append(buf.view(n_wg, 4).cpu().numpy().astype("uint64"))
+            runs.append(buf.view(n_wg, words).cpu().numpy().astype("uint64"))
         probe.mie_probe_decode_timeline(None)
     finally:
         _native._LIB = product
@@ -527,6 +531,8 @@ def secondary_decode_timeline(torch, launches=3):
         ctx = (rec[:, 3] & np.uint64(0xFFFFFFFF)).astype(np.int64)
         dur_us = (t1 - t0) / 100.0
         kv_bytes = ctx * head_dim * 2 * 2  # K and V rows of one head, bf16
+        wave_rel = (rec[:, 4:].astype(np.int64) - t0[:, None]) / np.maximum(t1 - t0, 1)[:, None]
+        long_seq = ctx > 4096
         rate = kv_bytes / np.maximum(dur_us, 1e-3) / 1e3  # GB/s
         ends = {}
         counts = {}
@@ -545,6 +551,8 @@ def secondary_decode_timeline(torch, launches=3):
                                             round(float(cu_end[-1]), 2)],
             "workgroup_gbs_p10_median_p90": [round(float(np.percentile(rate, q)), 1) for q in (10, 50, 90)],
             "sum_over_cus_of_median_rate_tbs": round(float(np.median(rate)) * len(ends) / 1e3, 2),
+            "wave_end_fraction_by_wave": [round(float(v), 3) for v in wave_rel[long_seq].mean(0)],
+            "wave_end_spread_median": round(float(np.median(wave_rel[long_seq].max(1) - wave_rel[long_seq].min(1))), 3),
         })
     return {"launches": res, "note": "config 4 fused step (workgroup form), probe build of the decode kernels"}
 
@@ -694,7 +702,9 @@ def secondary_launch_floor(torch):
 def secondary_read_ceilings(torch):
     """Read ceilings of the decode's access pattern: 768 MiB per call (about
     config 4's 785 MB) in 2 KiB chunks - one bf16 (block, head) tile - at
-    random chunk ids of a 4 GiB buffer and in order, read into registers with
+    random chunk ids of a 4 GiB buffer, in runs of 12 consecutive chunks at
+    random places (a block's 12 heads, 24 KiB: the read unit of a workgroup
+    that took all heads of a sequence) and in order, read into registers with
     non-temporal loads (the decode kernels' way) or staged through LDS with
     global_load_lds, with 1-8 chunks in flight per wave (csrc/probes)."""
     lib = probes_lib()
@@ -702,7 +712,11 @@ def secondary_read_ceilings(torch):
     n = (768 << 20) // 2048
     buf = torch.empty(chunks * 2048, dtype=torch.uint8, device="cuda")
     gen = torch.Generator().manual_seed(0)
-    orders = {"random": torch.randperm(chunks, generator=gen)[:n].to(torch.int32).cuda(),
+    random_ids = torch.randperm(chunks, generator=gen)[:n].to(torch.int32).cuda()
+    run = 12
+    starts = torch.randperm(chunks // run, generator=gen)[: n // run].to(torch.int64) * run
+    orders = {"random": random_ids,
+              "runs_of_12": (starts[:, None] + torch.arange(run)).reshape(-1).to(torch.int32).cuda(),
               "in_order": torch.arange(n, dtype=torch.int32, device="cuda")}
     groups = 2048
     out = torch.empty(groups * 256, dtype=torch.int32, device="cuda")

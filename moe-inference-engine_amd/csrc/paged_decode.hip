@@ -225,7 +225,15 @@ __device__ __forceinline__ void store_out(char* base, int64_t elem_off, const fl
 // wave: m (running max, log2 units) and l are uniform across lanes; acc holds
 // the head_dim slice jl = lane % LPT; bad is wave-uniform and set when a block
 // id outside the pool was met.
-template <int DT, int D, bool FAST, int KW = 16>
+//
+// YIELD: the wave lowers its issue priority (s_setprio 3, 2, 1, 0) as it
+// passes each quarter of its tiles, and ends at 0.  The workgroup form splits
+// one sequence among 16 waves with equal slices, and the SIMD's arbiter
+// favours the oldest ready wave: on MI355X (config 4) waves 0-3 finished at
+// 0.68 of the workgroup's time, waves 12-14 at 0.97.  A wave that gets ahead
+// now yields to the waves behind it (spread 0.31 -> 0.12).  Only the timing
+// changes: every wave reads the same tokens and the result is bit-identical.
+template <int DT, int D, bool FAST, int KW = 16, bool YIELD = false>
 __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, int t_begin, int t_end, int lane,
                                              float& m, float& l, float* acc, bool& bad, int32_t win_ids = -1) {
   using G = Geometry<DT, D, KW>;
@@ -376,9 +384,16 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
   // so no tile past the range is read.
   Words<NW> kA[ROWS], vA[ROWS], kB[ROWS], vB[ROWS];
   const int ntiles = (t_end - t_begin + TILE - 1) / TILE;  // >= 1
+  [[maybe_unused]] const int q1 = ntiles / 4, q2 = ntiles / 2, q3 = (3 * ntiles) / 4;
+  if constexpr (YIELD) __builtin_amdgcn_s_setprio(3);
   issue(t_begin, kA, vA);
   int t0 = t_begin;
   for (int i = 0; i + 2 < ntiles; i += 2, t0 += 2 * TILE) {
+    if constexpr (YIELD) {
+      if (i >= q3) __builtin_amdgcn_s_setprio(0);
+      else if (i >= q2) __builtin_amdgcn_s_setprio(1);
+      else if (i >= q1) __builtin_amdgcn_s_setprio(2);
+    }
     issue(t0 + TILE, kB, vB);
     consume(t0, kA, vA);
     issue(t0 + 2 * TILE, kA, vA);
@@ -407,6 +422,7 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int h, 
     m = mn;
   }
   if constexpr (!FAST) bad = __any(bad);
+  if constexpr (YIELD) __builtin_amdgcn_s_setprio(0);
 }
 
 // One work item: sequence b (ctx tokens, ctx > 0), head h, partition `part`,
@@ -552,9 +568,10 @@ struct WgOrder {
 #ifdef MIE_DECODE_TIMELINE
 // Measurement build only (libmie_probes.so, bench.py's decode_timeline): when
 // set, each workgroup of the workgroup form records its start and end on the
-// 100 MHz real-time clock, its XCD and hardware id, and its sequence and
-// length, 4 words per workgroup in grid order.  The product library is built
-// without it.
+// 100 MHz real-time clock, its XCD and hardware id, its sequence and length,
+// then the time each of its waves finished its slice: kTimelineWords words
+// per workgroup in grid order.  The product library is built without it.
+constexpr int kTimelineWords = 4 + kSplitWaves;
 __device__ uint64_t* g_decode_timeline;
 #endif
 
@@ -570,6 +587,12 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   __shared__ float s_m[kStates], s_l[kStates];
   __shared__ float s_acc[kStates][D];
   __shared__ int s_bad;
+  // At least 72 VGPRs, so at most 7 waves per SIMD (28 per CU): one 16-wave
+  // workgroup runs per CU and the next one starts as soon as one wave per
+  // SIMD has ended.  At 8 waves per SIMD (the f32 shapes compile to <= 64
+  // VGPRs) two whole workgroups share a CU from the start; at config 4's
+  // shape in f32 that measured 2.5 % slower on MI355X.  Emits no code.
+  asm volatile("" ::: "v71");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int h = blockIdx.x;
@@ -595,7 +618,12 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   for (int i = 0; i < VEC; ++i) acc[i] = 0.f;
   bool bad = false;
   if (t_begin < t_end)
-    attend_range<DT, D, FAST, kWgTileWords>(a, b, h, t_begin, t_end, lane, m, l, acc, bad, win_ids);
+    attend_range<DT, D, FAST, kWgTileWords, true>(a, b, h, t_begin, t_end, lane, m, l, acc, bad, win_ids);
+#ifdef MIE_DECODE_TIMELINE
+  if (lane == 0 && g_decode_timeline)
+    g_decode_timeline[kTimelineWords * (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) + 4 + wave] =
+        wall_clock64();
+#endif
   __syncthreads();  // s_bad is cleared
   const int g = lane / LPT;
   const int jl = lane % LPT;
@@ -667,7 +695,7 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   __syncthreads();
 #ifdef MIE_DECODE_TIMELINE
   if (threadIdx.x == 0 && g_decode_timeline) {
-    uint64_t* r = g_decode_timeline + 4 * (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x);
+    uint64_t* r = g_decode_timeline + kTimelineWords * (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x);
     r[0] = tl_start;
     r[1] = wall_clock64();
     // HW_REG_XCC_ID (bits 3:0) and HW_REG_HW_ID (all 32 bits).
@@ -1215,7 +1243,8 @@ extern "C" int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, i
 
 #ifdef MIE_DECODE_TIMELINE
 // Measurement build only: sets (or, with NULL, clears) the buffer the
-// workgroup form records into, 4 uint64 per workgroup of the next launches.
+// workgroup form records into, kTimelineWords (20) uint64 per workgroup of the
+// next launches.
 extern "C" int32_t mie_probe_decode_timeline(void* buffer) {
   const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_decode_timeline), &buffer, sizeof(buffer));
   return e == hipSuccess ? 0 : 2;
