@@ -588,10 +588,10 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   __shared__ float s_acc[kStates][D];
   __shared__ int s_bad;
   // At least 72 VGPRs, so at most 7 waves per SIMD (28 per CU): one 16-wave
-  // workgroup runs per CU and the next one starts as soon as one wave per
-  // SIMD has ended.  At 8 waves per SIMD (the f32 shapes compile to <= 64
-  // VGPRs) two whole workgroups share a CU from the start; at config 4's
-  // shape in f32 that measured 2.5 % slower on MI355X.  Emits no code.
+  // workgroup runs per CU at a time.  At 8 waves per SIMD (the f32 shapes
+  // compile to <= 64 VGPRs) two whole workgroups share a CU, twice the random
+  // read streams per CU; on MI355X that measured 2.5 % slower at config 4's
+  // shape in f32, and 30 % slower for a 64-VGPR bf16 build.  Emits no code.
   asm volatile("" ::: "v71");
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
