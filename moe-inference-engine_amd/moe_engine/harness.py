@@ -39,7 +39,7 @@ import time
 import torch
 import torch.nn.functional as F
 
-from moe_engine import paged_attention
+from moe_engine import _native, paged_attention, projection
 from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig
 
 SYSTEMS = ("contiguous", "paged-gather", "paged-direct")
@@ -133,6 +133,18 @@ def attention_micro(config=None, contexts=(16, 64, 256, 1024), device="cuda", dt
     return results
 
 
+def greedy_pick(logits):
+    """The next token from [1, S, vocab] logits: the argmax of the last
+    position, as the reference's timed loop takes it
+    (benchmarks/ab_compare.py:58,64).  On a ROCm device in float32 it is one
+    mie_argmax launch, the pick Model.generate makes at temperature 0; else
+    torch.argmax.  Both give torch.argmax's index (first maximum, NaN largest)."""
+    last = logits[:, -1, :]
+    if last.dtype == torch.float32 and last.is_contiguous() and _native.is_rocm_device(last):
+        return projection.argmax(last.reshape(-1)).view(1, 1)
+    return last.argmax(dim=-1, keepdim=True)
+
+
 def run_round(model, cache, prompt_ids, new_tokens):
     """One prefill and `new_tokens` greedy decode steps; returns
     (prefill seconds, per-step seconds, generated tokens)."""
@@ -144,13 +156,13 @@ def run_round(model, cache, prompt_ids, new_tokens):
         logits = model(prompt_ids.unsqueeze(0), cache)
         sync(device)
         prefill_s = time.perf_counter() - start
-        step_input = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+        step_input = greedy_pick(logits)
         steps = []
         for _ in range(new_tokens):
             sync(device)
             start = time.perf_counter()
             logits = model(step_input, cache)
-            step_input = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+            step_input = greedy_pick(logits)
             sync(device)
             steps.append(time.perf_counter() - start)
             tokens.append(int(step_input))
@@ -173,7 +185,7 @@ def run_round_graphed(model, state, prompt_ids, new_tokens):
         logits = model(prompt_ids.unsqueeze(0), cache)
         sync(device)
         prefill_s = time.perf_counter() - start
-        step_input = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+        step_input = greedy_pick(logits)
         if state.get("decoder") is None:
             state["decoder"] = GraphedDecoder(model, cache)
         decoder = state["decoder"]

@@ -1,7 +1,9 @@
 """Host-side pieces of the latency harness on the CPU: the contiguous-direct
-system's cache is the contiguous cache's layout, and the parity report
-(the reference's scripts/check_parity.py schema) of a path against itself."""
+system's cache is the contiguous cache's layout, the parity report (the
+reference's scripts/check_parity.py schema) of a path against itself, and the
+timed loop's greedy pick (torch.argmax's index; on the GPU through mie_argmax)."""
 
+import pytest
 import torch
 
 from moe_engine import harness
@@ -42,3 +44,31 @@ def test_graph_systems_and_pairs_are_named():
     assert harness.is_graph_system(harness.GRAPH_SYSTEM) and harness.is_graph_system("contiguous-direct-graph")
     assert not harness.is_graph_system("paged-direct")
     assert set(harness.SYSTEMS) < set(harness.ALL_SYSTEMS)
+
+
+def _pick_cases(device):
+    g = torch.Generator().manual_seed(4)
+    base = torch.randn(1, 3, 1000, generator=g)
+    tie = base.clone()
+    tie[0, -1, [17, 400, 901]] = 50.0  # the first of equal maxima
+    nan = base.clone()
+    nan[0, -1, [33, 700]] = float("nan")  # NaN counts as the largest
+    only_last_row = base.clone()
+    only_last_row[0, 0, 5] = 99.0  # a larger value outside the last position is ignored
+    return [t.to(device) for t in (base, tie, nan, only_last_row)]
+
+
+def test_greedy_pick_is_torch_argmax_of_the_last_position():
+    for logits in _pick_cases("cpu"):
+        assert torch.equal(harness.greedy_pick(logits), logits[:, -1, :].argmax(dim=-1, keepdim=True))
+
+
+@pytest.mark.gpu
+def test_greedy_pick_on_the_gpu_is_one_mie_argmax_with_torch_order():
+    """On a ROCm device the harness picks through mie_argmax (as Model.generate
+    does): the same index as torch.argmax, ties and NaN included."""
+    for logits in _pick_cases("cuda"):
+        want = logits[:, -1, :].float().cpu().argmax(dim=-1, keepdim=True)
+        got = harness.greedy_pick(logits)
+        assert got.shape == (1, 1) and got.dtype == torch.int64
+        assert torch.equal(got.cpu(), want)
