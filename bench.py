@@ -359,7 +359,7 @@ def secondary_config3(torch):
             "gather_bytes_per_layer": gb,
         }
         del tables
-    # Prefill scatter (SURVEY f1): the whole context written through the table in one launch per layer.
+    # Prefill scatter: the whole context written through the table in one launch per layer.
     C = 8192
     table = torch.zeros(NB, dtype=torch.int32, device="cuda")
     table[: C // BS] = perm[: C // BS]
@@ -378,7 +378,7 @@ def secondary_config3(torch):
 
 
 def secondary_moe(torch):
-    """Fused MoE decode (SURVEY f2) at config 1's shape: d 768, FFN 2048, top-2
+    """Fused MoE decode at config 1's shape: d 768, FFN 2048, top-2
     of 8, float32.  Bytes per call: the router and the two selected experts'
     W1, b1, W2, b2, read once."""
     from moe_engine.model import MoEFeedForward
@@ -788,7 +788,11 @@ def secondary_e2e(torch, rounds=5, new_tokens=64, cpu_rounds=2):
     Parity: the reference's report (scripts/check_parity.py:64-93) of the GPU
     paged-direct path against the CPU path, and the GPU tokens against the
     reference engine's own tokens for this configuration
-    (tests/golden/reference_config1.json, written by the reference's code)."""
+    (tests/golden/reference_config1.json, written by the reference's code).
+
+    MoE A/B: the contiguous system's decode with the PyTorch per-expert MoE
+    against the fused kernels (moe_engine.harness.moe_ab_compare,
+    benchmarks/moe_ab_compare.py:66-200), 3 rounds of 16 tokens."""
     from moe_engine import harness
 
     model = harness.make_model(harness.CONFIG1, seed=0, device="cuda")
@@ -818,6 +822,19 @@ def secondary_e2e(torch, rounds=5, new_tokens=64, cpu_rounds=2):
             parity["tokens_equal_reference_engine"] = parity["tokens"] == golden["tokens"]["paged_gather"]
     parity.pop("tokens")
     report["parity"] = parity
+
+    log("config 1 MoE A/B")
+    # The reference's MoE A/B (benchmarks/moe_ab_compare.py): contiguous cache,
+    # PyTorch per-expert MoE against the fused kernels, interleaved rounds.
+    moe_ab = harness.moe_ab_compare(model, prompt, rounds=3, new_tokens=16, system="contiguous")
+    report["moe_ab"] = {
+        "system": moe_ab["system"],
+        "decode_median_ms": {mode: s["decode_median_ms"] for mode, s in moe_ab["summary"].items()},
+        "paired_delta_direct_minus_reference_ms": moe_ab["paired_delta_direct_minus_reference"],
+        "tokens_identical": moe_ab["tokens_identical"],
+        "rounds": moe_ab["rounds"],
+        "new_tokens": moe_ab["new_tokens"],
+    }
     return report
 
 

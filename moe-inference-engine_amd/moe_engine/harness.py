@@ -11,6 +11,9 @@ the real checkpoint and tokenizer are not available here:
   ab_compare       interleaved rounds of every system with a rotating start,
                    paired per-round deltas and a Student-t 95 % interval
                    (benchmarks/ab_compare.py:49-198)
+  moe_ab_compare   the same for the MoE decode path: 'reference' (PyTorch
+                   per-expert) against 'direct' (fused HIP) on one cache
+                   system (benchmarks/moe_ab_compare.py:66-200)
 
 System names are the reference's: "contiguous", "paged-gather",
 "paged-direct", plus
@@ -28,6 +31,7 @@ this engine's fused MoE half), so paged-direct minus contiguous also counts
 the fused attention kernels.  Run as a module for a JSON report:
 
     python -m moe_engine.harness ab --rounds 5 --new-tokens 64
+    python -m moe_engine.harness moe-ab --rounds 9 --systems contiguous
 """
 
 import argparse
@@ -279,6 +283,74 @@ def ab_compare(model, prompt_ids, systems=SYSTEMS, rounds=5, new_tokens=64, bloc
     }
 
 
+MOE_AB_MODES = ("reference", "direct")
+
+
+def moe_ab_compare(model, prompt_ids, rounds=9, new_tokens=64, system="contiguous", block_size=16):
+    """The MoE decode path A/B of benchmarks/moe_ab_compare.py:66-200: the
+    same prompt and cache system decoded greedily with the MoE in
+    'reference' mode (the PyTorch per-expert path) and in 'direct' mode (the
+    fused HIP kernels), interleaved over `rounds` rounds whose first mode
+    alternates, after one short warm-up round per mode.  Reports each mode's
+    step statistics with per-round totals, the paired per-round delta
+    direct - reference with its 95 % interval, and whether both modes chose
+    the same tokens.  The model's MoE modes are restored afterwards."""
+    if rounds < 2 or new_tokens < 1:
+        raise ValueError("moe_ab_compare needs at least 2 rounds and 1 new token")
+    if is_graph_system(system):
+        raise ValueError("moe_ab_compare runs eager systems; the reference MoE path cannot be captured")
+    saved = [block.moe.mode for block in model.MoEBlocks]
+
+    def decode(mode, tokens):
+        model.set_moe_mode(mode)
+        cache = make_cache(model, system, block_size)
+        try:
+            return run_round(model, cache, prompt_ids, tokens)
+        finally:
+            release(cache)
+
+    try:
+        for mode in MOE_AB_MODES:
+            decode(mode, min(new_tokens, 8))
+        runs = {mode: [] for mode in MOE_AB_MODES}
+        for r in range(rounds):
+            first = r % 2
+            for mode in MOE_AB_MODES[first:] + MOE_AB_MODES[:first]:
+                runs[mode].append(decode(mode, new_tokens))
+    finally:
+        for block, mode in zip(model.MoEBlocks, saved):
+            block.moe.set_mode(mode)
+
+    summary, round_means = {}, {}
+    for mode, results in runs.items():
+        pooled = sorted(t for _, steps, _ in results for t in steps)
+        totals = [sum(steps) for _, steps, _ in results]
+        round_means[mode] = [sum(steps) / len(steps) * 1e3 for _, steps, _ in results]
+        summary[mode] = {
+            "prefill_median_ms": round(statistics.median(p for p, _, _ in results) * 1e3, 3),
+            "total_decode_steps": len(pooled),
+            "total_decode_s": round(sum(pooled), 6),
+            "decode_median_ms": round(statistics.median(pooled) * 1e3, 3),
+            "decode_p90_ms": round(pooled[int(len(pooled) * 0.9)] * 1e3, 3),
+            "decode_tok_per_sec": round(len(pooled) / sum(pooled), 3),
+            "per_round_total_decode_ms": [round(t * 1e3, 3) for t in totals],
+            "per_round_decode_tok_per_sec": [round(new_tokens / t, 3) for t in totals],
+            "per_round_mean_ms": [round(m, 4) for m in round_means[mode]],
+        }
+    token_sets = {mode: [tokens for _, _, tokens in results] for mode, results in runs.items()}
+    reference_tokens = token_sets["reference"][0]
+    return {
+        "system": system,
+        "summary": summary,
+        "paired_delta_direct_minus_reference": paired_t_summary(
+            [d - r for d, r in zip(round_means["direct"], round_means["reference"])]),
+        "tokens_identical": all(t == reference_tokens for ts in token_sets.values() for t in ts),
+        "rounds": rounds,
+        "new_tokens": new_tokens,
+        "prompt_tokens": int(prompt_ids.numel()),
+    }
+
+
 def stepwise_logits(model, seq, cache, prompt_len):
     """Logits [T, vocab] for every position of `seq` ([1, T] ids): the prompt
     as one prefill, then one decode step per later token (teacher forcing)."""
@@ -353,25 +425,34 @@ def context_sweep(model, contexts=(16, 64, 256, 1024), systems=SYSTEMS, steps=16
 
 def main(argv=None):
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    parser.add_argument("mode", choices=["ab", "micro", "sweep"])
+    parser.add_argument("mode", choices=["ab", "moe-ab", "micro", "sweep"])
     parser.add_argument("--rounds", type=int, default=5)
     parser.add_argument("--new-tokens", type=int, default=64)
     parser.add_argument("--prompt-tokens", type=int, default=32)
     parser.add_argument("--contexts", default="16,64,256,1024")
-    parser.add_argument("--systems", default=",".join(SYSTEMS), help="any of " + ", ".join(ALL_SYSTEMS))
+    parser.add_argument("--systems", default=None,
+                        help="any of " + ", ".join(ALL_SYSTEMS) + " (moe-ab: one eager system, default contiguous)")
     parser.add_argument("--device", default="cuda")
     args = parser.parse_args(argv)
     contexts = [int(c) for c in args.contexts.split(",")]
+    systems = (args.systems or ("contiguous" if args.mode == "moe-ab" else ",".join(SYSTEMS))).split(",")
+    if args.mode == "moe-ab" and (len(systems) != 1 or systems[0] not in ALL_SYSTEMS or is_graph_system(systems[0])):
+        parser.error("moe-ab takes one eager system: " + ", ".join(s for s in ALL_SYSTEMS if not is_graph_system(s)))
+    if args.mode == "moe-ab" and (args.rounds < 2 or args.new_tokens < 1):
+        parser.error("--rounds must be at least 2 and --new-tokens positive")
     if args.mode == "micro":
         report = attention_micro(contexts=contexts, device=args.device)
     else:
         model = make_model(device=args.device)
-        if args.mode == "ab":
+        if args.mode in ("ab", "moe-ab"):
             gen = torch.Generator().manual_seed(0)
             prompt = torch.randint(0, CONFIG1["vocab_size"], (args.prompt_tokens,), generator=gen).to(args.device)
-            report = ab_compare(model, prompt, args.systems.split(","), args.rounds, args.new_tokens)
+            if args.mode == "ab":
+                report = ab_compare(model, prompt, systems, args.rounds, args.new_tokens)
+            else:
+                report = moe_ab_compare(model, prompt, args.rounds, args.new_tokens, systems[0])
         else:
-            report = context_sweep(model, contexts, args.systems.split(","))
+            report = context_sweep(model, contexts, systems)
     print(json.dumps(report, indent=2))
 
 

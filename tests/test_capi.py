@@ -90,8 +90,9 @@ def test_invalid_arguments_fail_before_launch():
 
 
 def test_integration_binding_matches_the_library_signatures():
-    """The ctypes binding INTEGRATION.md offers the reference declares, for
-    every entry point it binds, the argument types moe_engine._native uses."""
+    """The ctypes binding the repository's integration notes give the
+    reference declares, for every entry point it binds, the argument types
+    moe_engine._native uses."""
     import types
 
     text = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()

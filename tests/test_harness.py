@@ -72,3 +72,88 @@ def test_greedy_pick_on_the_gpu_is_one_mie_argmax_with_torch_order():
         got = harness.greedy_pick(logits)
         assert got.shape == (1, 1) and got.dtype == torch.int64
         assert torch.equal(got.cpu(), want)
+
+
+def test_moe_ab_rejects_what_the_reference_rejects():
+    model = Model(ModelConfig(**TINY)).eval()
+    prompt = torch.zeros(3, dtype=torch.long)
+    with pytest.raises(ValueError, match="2 rounds"):
+        harness.moe_ab_compare(model, prompt, rounds=1)
+    with pytest.raises(ValueError, match="2 rounds"):
+        harness.moe_ab_compare(model, prompt, rounds=2, new_tokens=0)
+    with pytest.raises(ValueError, match="eager"):
+        harness.moe_ab_compare(model, prompt, rounds=2, system=harness.GRAPH_SYSTEM)
+    # The command line refuses the same before it builds a model.
+    for argv in (["moe-ab", "--rounds", "1"], ["moe-ab", "--new-tokens", "0"],
+                 ["moe-ab", "--systems", "paged-direct-graph"], ["moe-ab", "--systems", "contiguous,paged-direct"],
+                 ["moe-ab", "--systems", "no-such-system"]):
+        with pytest.raises(SystemExit):
+            harness.main(argv + ["--device", "cpu"])
+
+
+def test_moe_ab_alternates_modes_and_restores_them(monkeypatch):
+    """Warm-up of each mode at min(new_tokens, 8) tokens, then rounds whose
+    first mode alternates; every round decodes on a fresh cache of the
+    chosen system; the summary's per-round figures and the paired delta come
+    from the rounds' step times; the blocks get their own modes back."""
+    model = Model(ModelConfig(**TINY)).eval()
+    model.MoEBlocks[1].moe.set_mode("reference")
+    calls = []
+    step_ms = {"reference": 3.0, "direct": 1.0}
+
+    def fake_round(m, cache, prompt_ids, new_tokens):
+        modes = {block.moe.mode for block in m.MoEBlocks}
+        assert len(modes) == 1  # the whole model runs one mode at a time
+        mode = modes.pop()
+        calls.append((mode, new_tokens, type(cache).__name__))
+        r = sum(1 for c in calls if c[0] == mode)
+        return 0.5, [(step_ms[mode] + 0.1 * r) * 1e-3] * new_tokens, [7] * new_tokens
+
+    monkeypatch.setattr(harness, "run_round", fake_round)
+    prompt = torch.zeros(4, dtype=torch.long)
+    rep = harness.moe_ab_compare(model, prompt, rounds=3, new_tokens=12, system="paged-gather")
+    assert [c[:2] for c in calls] == [("reference", 8), ("direct", 8),
+                                      ("reference", 12), ("direct", 12),
+                                      ("direct", 12), ("reference", 12),
+                                      ("reference", 12), ("direct", 12)]
+    assert {c[2] for c in calls} == {"PagedKVCache"}
+    assert [block.moe.mode for block in model.MoEBlocks] == ["auto", "reference"]
+    ref, direct = rep["summary"]["reference"], rep["summary"]["direct"]
+    assert ref["total_decode_steps"] == direct["total_decode_steps"] == 36
+    assert ref["per_round_mean_ms"] == pytest.approx([3.2, 3.3, 3.4])
+    assert direct["per_round_total_decode_ms"] == pytest.approx([12 * 1.2, 12 * 1.3, 12 * 1.4])
+    delta = rep["paired_delta_direct_minus_reference"]
+    assert delta["mean_delta_ms"] == pytest.approx(-2.0) and delta["ci95_ms"] == pytest.approx([-2.0, -2.0])
+    assert rep["tokens_identical"] and rep["system"] == "paged-gather" and rep["prompt_tokens"] == 4
+
+
+def test_moe_ab_restores_modes_when_a_round_fails(monkeypatch):
+    model = Model(ModelConfig(**TINY)).eval()
+
+    def failing_round(m, cache, prompt_ids, new_tokens):
+        if m.MoEBlocks[0].moe.mode == "direct":
+            raise RuntimeError("direct MoE decode is unavailable")
+        return 0.1, [1e-3] * new_tokens, [1] * new_tokens
+
+    monkeypatch.setattr(harness, "run_round", failing_round)
+    with pytest.raises(RuntimeError, match="unavailable"):
+        harness.moe_ab_compare(model, torch.zeros(2, dtype=torch.long), rounds=2, new_tokens=2)
+    assert [block.moe.mode for block in model.MoEBlocks] == ["auto", "auto"]
+
+
+@pytest.mark.gpu
+def test_moe_ab_on_the_gpu_decodes_the_same_tokens_both_ways():
+    """The real A/B on a small model: the PyTorch per-expert MoE and the fused
+    HIP MoE choose the same greedy tokens on the contiguous and paged-direct
+    systems, and the report carries both modes and the paired delta."""
+    cfg = dict(max_seq_length=64, vocab_size=512, num_layers=2, hidden_dim=64, num_heads=4, num_experts=4, top_k=2)
+    model = harness.make_model(cfg, device="cuda")
+    assert all(block.moe.direct_configuration_supported(1) for block in model.MoEBlocks)
+    prompt = torch.randint(0, cfg["vocab_size"], (6,), generator=torch.Generator().manual_seed(3)).cuda()
+    for system in ("contiguous", "paged-direct"):
+        rep = harness.moe_ab_compare(model, prompt, rounds=2, new_tokens=5, system=system)
+        assert rep["tokens_identical"], system
+        assert set(rep["summary"]) == {"reference", "direct"}
+        assert rep["summary"]["direct"]["total_decode_steps"] == 10
+        assert len(rep["paired_delta_direct_minus_reference"]["per_round_delta_ms"]) == 2
+    assert {block.moe.mode for block in model.MoEBlocks} == {"auto"}
