@@ -20,6 +20,8 @@
  *   mie_argmax        <- Model.generate's greedy torch.argmax   src/moe_engine/model.py:603
  *   mie_lm_head       <- final_norm + output_projection (model.py:564-565) and,
  *                        optionally, the greedy argmax (:603) for one token
+ *   mie_argmax_pairs  <- Model.generate's greedy torch.argmax (model.py:603) of
+ *                        logits mie_lm_head just wrote, from its per-workgroup picks
  *   mie_embed         <- token_embedding(ids) + positional_embedding(pos)  src/moe_engine/model.py:558
  *   mie_attn_out_acc  <- paged_attention.decode then out_proj for one decode
  *                        token (model.py:263 then :268), per head, summed into
@@ -84,7 +86,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 13
+#define MIE_ABI_VERSION 14
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -355,12 +357,14 @@ int32_t mie_embed(const void* token_ids, const int32_t* positions, int32_t posit
  * dim as for mie_qkv_append_supported.  x, W and the norm parameters 16-byte
  * aligned.
  *
- * token_out (int64, or NULL for the logits only): the index of the largest
- * stored logit in torch.argmax's order (first index of the maximum, NaN
- * largest), computed by a second one-workgroup launch from per-workgroup
- * picks kept in `workspace` (mie_lm_head_workspace(vocab) bytes, 8-byte
- * aligned).  Nothing needs clearing beforehand, so both launches can be
- * captured in a graph.
+ * workspace (mie_lm_head_workspace(vocab) bytes, 4-byte aligned, or NULL):
+ * the launch also leaves there each workgroup's pick of its rows - the
+ * largest stored logit in torch.argmax's order (first index of the maximum,
+ * NaN largest) - at no extra launch.  token_out (int64, or NULL; needs the
+ * workspace): the index of the largest logit, merged from those picks by a
+ * second one-workgroup launch.  Without token_out, mie_argmax_pairs makes the
+ * same merge later.  Nothing needs clearing beforehand, so both launches can
+ * be captured in a graph.
  *
  * advance (device int32[n_advance], n_advance <= 64; needs token_out): each
  * counter is incremented by one after the pick, in the same launch - a
@@ -371,6 +375,15 @@ int64_t mie_lm_head_workspace(int32_t vocab);
 int32_t mie_lm_head(const void* x, const void* ln_weight, const void* ln_bias, float ln_eps, const void* weight,
                     const void* bias, int32_t vocab, int32_t dim, void* logits, void* token_out, void* workspace,
                     int64_t workspace_bytes, int32_t* advance, int32_t n_advance, int32_t dtype, void* stream);
+
+/*
+ * Greedy pick (model.py:603) of the logits a mie_lm_head call of the same
+ * `vocab` wrote together with `workspace`: the per-workgroup picks there are
+ * merged into *out (int64) in one launch of one workgroup - the index
+ * torch.argmax returns for those logits, as long as neither they nor the
+ * workspace were written since.  Queue it on the head's stream, or after it.
+ */
+int32_t mie_argmax_pairs(const void* workspace, int64_t workspace_bytes, int32_t vocab, void* out, void* stream);
 
 /*
  * mie_paged_decode without the workspace arguments: an entry point that

@@ -108,3 +108,19 @@ extern "C" int32_t mie_argmax(const void* x, int64_t n, void* out, int32_t dtype
                                                                        static_cast<int64_t*>(out));
   return mie::check_launch("argmax_kernel");
 }
+
+extern "C" int32_t mie_argmax_pairs(const void* workspace, int64_t workspace_bytes, int32_t vocab, void* out,
+                                    void* stream) {
+  const int64_t need = mie_lm_head_workspace(vocab);
+  if (need <= 0) return mie::fail(MIE_ERR_INVALID, "mie_argmax_pairs: vocab %d", vocab);
+  if (!workspace || !out) return mie::fail(MIE_ERR_INVALID, "mie_argmax_pairs: null pointer");
+  if (workspace_bytes < need)
+    return mie::fail(MIE_ERR_INVALID, "mie_argmax_pairs: the picks of %d logits take %lld bytes (got %lld)", vocab,
+                     static_cast<long long>(need), static_cast<long long>(workspace_bytes));
+  if (reinterpret_cast<uintptr_t>(workspace) % alignof(mie::ArgmaxPair) ||
+      reinterpret_cast<uintptr_t>(out) % alignof(int64_t))
+    return mie::fail(MIE_ERR_INVALID, "mie_argmax_pairs: misaligned workspace or token");
+  return mie::launch_argmax_pairs(static_cast<const mie::ArgmaxPair*>(workspace),
+                                  static_cast<int32_t>(need / static_cast<int64_t>(sizeof(mie::ArgmaxPair))), vocab,
+                                  static_cast<int64_t*>(out), nullptr, 0, static_cast<hipStream_t>(stream));
+}

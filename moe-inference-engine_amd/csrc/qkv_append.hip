@@ -568,12 +568,12 @@ extern "C" int32_t mie_lm_head(const void* x, const void* ln_weight, const void*
   if (!aligned16(weight) || !aligned16(x) || !aligned16(ln_weight) || !aligned16(ln_bias))
     return mie::fail(MIE_ERR_INVALID, "mie_lm_head: x, the norm parameters and the weight must be 16-byte aligned");
   const int64_t need = mie_lm_head_workspace(vocab);
-  if (token_out && (!workspace || workspace_bytes < need))
+  if ((token_out || workspace) && (!workspace || workspace_bytes < need))
     return mie::fail(MIE_ERR_INVALID, "mie_lm_head: the pick needs a %lld-byte workspace (got %lld)",
                      static_cast<long long>(need), static_cast<long long>(workspace ? workspace_bytes : 0));
   if (n_advance < 0 || n_advance > 64 || (n_advance > 0 && (!advance || !token_out)))
     return mie::fail(MIE_ERR_INVALID, "mie_lm_head: %d counters to advance (at most 64, with a token)", n_advance);
-  if (token_out && (reinterpret_cast<uintptr_t>(workspace) % alignof(mie::ArgmaxPair) ||
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) % alignof(mie::ArgmaxPair) ||
                     reinterpret_cast<uintptr_t>(token_out) % alignof(int64_t)))
     return mie::fail(MIE_ERR_INVALID, "mie_lm_head: misaligned workspace or token");
   QkvArgs a{};
@@ -586,7 +586,7 @@ extern "C" int32_t mie_lm_head(const void* x, const void* ln_weight, const void*
   a.w_in = weight;
   a.b_in = bias;
   a.dim = dim;
-  a.picks = token_out ? static_cast<mie::ArgmaxPair*>(workspace) : nullptr;
+  a.picks = static_cast<mie::ArgmaxPair*>(workspace);  // NULL: no picks
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int32_t rc = dtype == MIE_DTYPE_F32 ? launch<float, kHead>(a, st) : launch<uint16_t, kHead>(a, st);
   if (rc != MIE_OK || !token_out) return rc;

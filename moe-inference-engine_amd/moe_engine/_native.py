@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -132,6 +132,7 @@ _SIGNATURES = {
          _c_void_p, _i32, _c_void_p],  # out, dtype, stream
     ),
     "mie_lm_head_workspace": (_i64, [_i32]),
+    "mie_argmax_pairs": (_i32, [_c_void_p, _i64, _i32, _c_void_p, _c_void_p]),  # workspace, bytes, vocab, out, stream
     "mie_block_plan_bytes": (_i64, []),
     "mie_block_plan_init": (
         _i32,

@@ -942,7 +942,10 @@ class Model(nn.Module):
         if x.shape[0] == 1 and x.shape[1] == 1 and not torch.is_grad_enabled() and self._head_on_device(x):
             # One decode token at inference: final norm and LM head in one
             # launch (no autograd graph; with gradients on, the modules run).
-            return projection.lm_head(x.view(-1), self.final_norm, self.output_projection).view(1, 1, -1)
+            # The head keeps its workgroups' picks, so a greedy pick of these
+            # logits (projection.argmax) is one small merge launch.
+            return projection.lm_head(x.view(-1), self.final_norm, self.output_projection,
+                                      keep_pick=True).view(1, 1, -1)
         return self.output_projection(self.final_norm(x))
 
     def _head_on_device(self, x) -> bool:

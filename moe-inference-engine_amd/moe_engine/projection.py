@@ -7,7 +7,9 @@
   (model.py:564-565), optionally with generate's greedy torch.argmax (:603)
   written to a device token, in two launches.
 - argmax (mie_argmax): generate's greedy torch.argmax (model.py:603) over one
-  row of float32 logits, in one launch.
+  row of float32 logits, in one launch.  For the logits an lm_head call with
+  keep_pick=True just wrote it merges the head's per-workgroup picks
+  (mie_argmax_pairs) instead of reading the row again.
 
 float32 or bfloat16.
 """
@@ -15,6 +17,25 @@ float32 or bfloat16.
 import torch
 
 from moe_engine import _native
+
+# The logits of the last lm_head(keep_pick=True) call, with the picks its
+# workgroups left: (logits, their version counter then, picks).  Holding the
+# logits keeps their memory from being reused, so a tensor at their address
+# is one of their views, and views share the version counter, which counts
+# every in-place write.
+_last_pick = None
+_pick_workspaces = {}  # (device, vocab) -> the picks' workspace
+
+
+def _kept_picks(x):
+    """The workspace of picks that describe x, or None."""
+    rec = _last_pick
+    if rec is None or x.is_inference():
+        return None
+    logits, version, workspace = rec
+    if x.data_ptr() != logits.data_ptr() or x.numel() != logits.numel() or x.device != logits.device:
+        return None
+    return workspace if x._version == version else None
 
 
 def supported(cols: int, dtype: torch.dtype) -> bool:
@@ -59,7 +80,7 @@ def linear_residual(x, weight, bias=None, residual=None, out=None):
     return out
 
 
-def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=None):
+def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=None, keep_pick=False):
     """linear(norm(x)) for one token (norm a LayerNorm or None), written to
     `out` ([vocab], allocated when None); with `token_out` (an int64 device
     tensor of one element) also the index of the largest logit, as
@@ -67,7 +88,11 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     head_workspace_bytes(vocab)) holds the per-workgroup picks; it is
     allocated when None.  `advance` (a contiguous int32 device tensor, with
     token_out): every element is incremented by one after the pick, in the
-    same launch.  Returns out."""
+    same launch.  keep_pick (without token_out, float32): the launch leaves
+    its picks in a workspace of this module's, and argmax(out) merges them
+    while out is unmodified and no later keep_pick call replaced them.
+    Returns out."""
+    global _last_pick
     weight, bias = linear.weight, linear.bias
     if weight.dim() != 2 or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous [vocab, dim] matrix")
@@ -93,7 +118,18 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     elif out.numel() != vocab or not out.is_contiguous():
         raise ValueError(f"out must hold {vocab} contiguous values")
     ws_ptr, ws_bytes = 0, 0
-    if token_out is not None:
+    keep_pick = keep_pick and token_out is None and dtype == torch.float32 and not out.is_inference()
+    if keep_pick:
+        key = (device, vocab)
+        workspace = _pick_workspaces.get(key)
+        if workspace is None:
+            workspace = _pick_workspaces[key] = torch.empty(head_workspace_bytes(vocab), dtype=torch.uint8,
+                                                            device=device)
+        ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel()
+        _last_pick = None  # the picks are overwritten from here on
+    elif _last_pick is not None and out.data_ptr() == _last_pick[0].data_ptr():
+        _last_pick = None  # the kernel rewrites the recorded logits without counting a version
+    if not keep_pick and token_out is not None:
         if token_out.dtype != torch.int64 or token_out.numel() != 1 or token_out.device != device:
             raise ValueError("token_out must be one int64 value on the weight's device")
         need = head_workspace_bytes(vocab)
@@ -117,19 +153,31 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
         ),
         "mie_lm_head",
     )
+    if keep_pick:
+        _last_pick = (out, out._version, workspace)
     return out
 
 
 def argmax(x, out=None):
     """torch.argmax of the contiguous float32 device vector x (the first index
     of the maximum, NaN counting as the largest), written to `out` (an int64
-    device tensor of one element, allocated when None).  Returns out."""
+    device tensor of one element, allocated when None): a merge of the head's
+    kept picks when x is the unmodified output of the last
+    lm_head(keep_pick=True), else one pass over x.  Returns out."""
     if not (_native.is_rocm_device(x) and x.dtype == torch.float32 and x.is_contiguous()) or x.numel() == 0:
         raise ValueError("mie_argmax takes a non-empty contiguous float32 vector on a ROCm device")
     if out is None:
         out = torch.empty(1, dtype=torch.int64, device=x.device)
     elif out.dtype != torch.int64 or out.numel() != 1 or out.device != x.device:
         raise ValueError("out must be one int64 value on x's device")
+    picks = _kept_picks(x)
+    if picks is not None:
+        _native.check(
+            _native.lib().mie_argmax_pairs(picks.data_ptr(), picks.numel(), x.numel(), out.data_ptr(),
+                                           _native.stream_of(x)),
+            "mie_argmax_pairs",
+        )
+        return out
     _native.check(
         _native.lib().mie_argmax(x.data_ptr(), x.numel(), out.data_ptr(), _native.dtype_code(x.dtype),
                                  _native.stream_of(x)),

@@ -34,6 +34,12 @@ def argmax_args(**over):
     return list(a.values())
 
 
+def argmax_pairs_args(**over):
+    a = dict(ws=ptr(), ws_bytes=_native.lib().mie_lm_head_workspace(50257), vocab=50257, out=ptr(), stream=None)
+    a.update(over)
+    return list(a.values())
+
+
 def embed_args(**over):
     a = dict(ids=ptr(), positions=ptr(), position=0, n=1, tok=ptr(), vocab=1000, pos_table=ptr(), max_pos=128,
              dim=64, out=ptr(), dtype=F32, stream=None)
@@ -112,6 +118,12 @@ CASES = [
     ("mie_argmax", argmax_args(dtype=BF16), UNSUPPORTED, b"float32 only"),
     ("mie_argmax", argmax_args(n=0), INVALID, b"n=0"),
     ("mie_argmax", argmax_args(x=None), INVALID, b"null pointer"),
+    ("mie_argmax_pairs", argmax_pairs_args(vocab=0), INVALID, b"vocab 0"),
+    ("mie_argmax_pairs", argmax_pairs_args(ws=None), INVALID, b"null pointer"),
+    ("mie_argmax_pairs", argmax_pairs_args(out=None), INVALID, b"null pointer"),
+    ("mie_argmax_pairs", argmax_pairs_args(ws_bytes=64), INVALID, b"take"),
+    ("mie_argmax_pairs", argmax_pairs_args(ws=ptr() + 2), INVALID, b"misaligned"),
+    ("mie_argmax_pairs", argmax_pairs_args(out=ptr() + 4), INVALID, b"misaligned"),
     ("mie_embed", embed_args(dtype=3), UNSUPPORTED, b"dtype 3"),
     ("mie_embed", embed_args(n=-1), INVALID, b"n -1"),
     ("mie_embed", embed_args(vocab=0), INVALID, b"vocab 0"),
@@ -126,6 +138,8 @@ CASES = [
     ("mie_lm_head", lm_head_args(logits=None), INVALID, b"null pointer"),
     ("mie_lm_head", lm_head_args(ln_w=None), INVALID, b"norm bias needs a norm weight"),
     ("mie_lm_head", lm_head_args(ws_bytes=8), INVALID, b"workspace"),
+    ("mie_lm_head", lm_head_args(token=None, advance=None, n_advance=0, ws_bytes=8), INVALID, b"workspace"),
+    ("mie_lm_head", lm_head_args(token=None, advance=None, n_advance=0, ws=ptr() + 2), INVALID, b"misaligned"),
     ("mie_lm_head", lm_head_args(n_advance=65), INVALID, b"counters to advance"),
     ("mie_lm_head", lm_head_args(token=ptr() + 4), INVALID, b"misaligned"),
     ("mie_qkv_append", qkv_args(dim=6, heads=1, head_dim=6), UNSUPPORTED, b"not built"),

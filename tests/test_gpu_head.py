@@ -117,6 +117,69 @@ def test_lm_head_pick_keeps_argmax_ties_and_nan_rules():
     assert int(token) == 0 == pick(logits)
 
 
+class _Counted:
+    """Counts calls of two library entry points (the full pick and the merge
+    of kept picks) while forwarding them."""
+
+    def __init__(self, monkeypatch):
+        from moe_engine import _native
+
+        lib = _native.lib()
+        self.calls = {"mie_argmax": 0, "mie_argmax_pairs": 0}
+        for name in self.calls:
+            real = getattr(lib, name)
+
+            def counted(*args, _real=real, _name=name):
+                self.calls[_name] += 1
+                return _real(*args)
+
+            monkeypatch.setattr(lib, name, counted)
+
+
+@torch.no_grad()
+def test_argmax_of_fresh_head_logits_merges_the_kept_picks(monkeypatch):
+    """lm_head(keep_pick=True) leaves its workgroups' picks; argmax of those
+    logits, or of a view of them, merges the picks (one small launch) and
+    returns torch.argmax's index, ties and NaN included.  Logits written
+    since - in place, by a later head call into the same buffer, or replaced
+    by a newer keep_pick call - are read in full instead."""
+    counted = _Counted(monkeypatch)
+    vocab, dim = 5000, 64
+    x, ln, linear = make_head(vocab, dim, torch.float32, True, True, seed=9)
+    logits = projection.lm_head(x, ln, linear, keep_pick=True)
+    assert int(projection.argmax(logits)) == pick(logits)
+    assert int(projection.argmax(logits.view(1, 1, -1)[:, -1, :].reshape(-1))) == pick(logits)
+    assert counted.calls == {"mie_argmax": 0, "mie_argmax_pairs": 2}
+
+    # Ties across workgroups (the lowest index wins) and NaN (the first wins).
+    x2, _, tied = make_head(vocab, dim, torch.float32, False, False, seed=5)
+    tied.weight.mul_(0.01)
+    for row in (3, 77, 4321, 4999):
+        tied.weight[row] = x2 * 0.5
+    logits = projection.lm_head(x2, None, tied, keep_pick=True)
+    assert int(projection.argmax(logits)) == 3 == pick(logits)
+    tied.weight[2500, 0] = float("nan")
+    tied.weight[4000, 0] = float("nan")
+    logits = projection.lm_head(x2, None, tied, keep_pick=True)
+    assert int(projection.argmax(logits)) == 2500 == pick(logits)
+    assert counted.calls["mie_argmax"] == 0
+
+    # Written in place after the head: a full pick of the new values.
+    logits = projection.lm_head(x, ln, linear, keep_pick=True)
+    logits[4990] = 1e30
+    assert int(projection.argmax(logits)) == 4990
+    assert counted.calls["mie_argmax"] == 1
+    # A newer keep_pick call replaces the picks: the older logits are read in full.
+    old = projection.lm_head(x, ln, linear, keep_pick=True)
+    new = projection.lm_head(x2, None, tied, keep_pick=True)
+    assert int(projection.argmax(old)) == pick(old) and counted.calls["mie_argmax"] == 2
+    assert int(projection.argmax(new)) == pick(new) and counted.calls["mie_argmax"] == 2
+    # A head call without keep_pick rewriting the recorded logits drops the picks.
+    kept = projection.lm_head(x2, None, tied, keep_pick=True)
+    projection.lm_head(x, ln, linear, out=kept)
+    assert int(projection.argmax(kept)) == pick(kept) and counted.calls["mie_argmax"] == 3
+
+
 def test_lm_head_advances_counters_after_the_pick():
     x, ln, linear = make_head(700, 64, torch.float32, True, True, seed=2)
     token = torch.zeros(1, dtype=torch.int64, device="cuda")
