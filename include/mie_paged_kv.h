@@ -33,6 +33,8 @@
  *                        five launches above from a stored plan, one call per token
  *   mie_block_plan_set_embedding, mie_block_decode_embed <- the embedding (model.py:558)
  *                        and the first block, the embedding inside the QKV launch
+ *   mie_blocks_decode <- Model.forward's embedding and blocks for one decode token
+ *                        (model.py:558-562): every block plan in one call
  *
  * Conventions shared by every entry point
  *   - Pointers are device pointers unless stated otherwise.  The library
@@ -86,7 +88,7 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 14
+#define MIE_ABI_VERSION 15
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
@@ -545,6 +547,21 @@ int32_t mie_block_plan_set_embedding(void* plan, const void* token_table, int32_
                                      int32_t max_positions, void* x_out);
 int32_t mie_block_decode_embed(const void* plan, const int64_t* token_id, const int32_t* counters,
                                int32_t position, void* stream);
+
+/*
+ * The embedding and every block of the decoder for one decode token in one
+ * call (Model.forward's blocks, model.py:558-562): plans[0] is a plan with
+ * the embedding set (as for mie_block_decode_embed), and plans[i] for i > 0
+ * takes plans[i - 1]'s output row `out` as its input x.  The launches are
+ * those of mie_block_decode_embed(plans[0], ...) followed by
+ * mie_block_decode(plans[i], out of plans[i - 1], ...), in order, bit for
+ * bit.  Every plan is checked before the first launch, so an error -
+ * MIE_ERR_WORKSPACE when a split context outgrew a plan's workspace
+ * included - launches nothing; the caller can then run the blocks one by one.
+ * 1 <= num_plans <= 256.
+ */
+int32_t mie_blocks_decode(const void* const* plans, int32_t num_plans, const int64_t* token_id,
+                          const int32_t* counters, int32_t position, void* stream);
 
 #ifdef __cplusplus
 }

@@ -71,6 +71,9 @@ struct BlockPlan {
 // five-launch decode takes its partition form.
 constexpr int32_t kFusedMaxCtx = 1024;
 
+// Blocks one mie_blocks_decode call runs.
+constexpr int32_t kMaxStepBlocks = 256;
+
 }  // namespace
 
 extern "C" int64_t mie_block_plan_bytes(void) { return static_cast<int64_t>(sizeof(BlockPlan)); }
@@ -193,21 +196,37 @@ int32_t qkv(const BlockPlan& p, const mie::QkvEmbedding& emb, bool embed, const 
 
 namespace {
 
+// One block call, checked: the plan, its input row and the position, and
+// whether the launches it would make fit the plan (the fused form, or the
+// decode's split-context workspace).  Nothing is launched here.
+struct BlockCall {
+  BlockPlan p;
+  mie::QkvEmbedding emb;
+  bool embed;
+  const void* x;
+  const int32_t* pos_dev;
+  const int32_t* ctx_dev;
+  int32_t position, max_ctx;
+  bool fused;
+  int64_t ws_need;
+};
+
 // x: the block's input row, or (with token_id) NULL and the row formed from
 // the plan's embedding tables by the QKV launch.
-int32_t block_decode(const void* plan, const void* x, const int64_t* token_id, const int32_t* counters,
-                     int32_t position, void* stream) {
+int32_t check_call(const void* plan, const void* x, const int64_t* token_id, const int32_t* counters,
+                   int32_t position, BlockCall* c) {
   if (!plan) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: null plan");
-  BlockPlan p;
+  BlockPlan& p = c->p;
   memcpy(&p, plan, sizeof(p));
   if (p.magic != kPlanMagic) return mie::fail(MIE_ERR_INVALID, "mie_block_decode: plan not initialised");
-  mie::QkvEmbedding emb{};
+  c->emb = mie::QkvEmbedding{};
+  c->embed = token_id != nullptr;
   if (token_id) {
     if (!p.tok_table)
       return mie::fail(MIE_ERR_INVALID, "mie_block_decode_embed: the plan has no embedding (mie_block_plan_set_embedding)");
     if (reinterpret_cast<uintptr_t>(token_id) % 8)
       return mie::fail(MIE_ERR_INVALID, "mie_block_decode_embed: misaligned token id");
-    emb = mie::QkvEmbedding{token_id, p.tok_table, p.vocab, p.pos_table, p.max_positions, p.x_emb};
+    c->emb = mie::QkvEmbedding{token_id, p.tok_table, p.vocab, p.pos_table, p.max_positions, p.x_emb};
     x = p.x_emb;
   }
   if (!x || reinterpret_cast<uintptr_t>(x) % 16 != 0 || position < 0)
@@ -217,50 +236,64 @@ int32_t block_decode(const void* plan, const void* x, const int64_t* token_id, c
                      p.block_table_len);
   if (x == p.h || x == p.q || x == p.attn)
     return mie::fail(MIE_ERR_INVALID, "mie_block_decode: x aliases one of the plan's intermediate rows");
+  c->x = x;
   // With counters the position and context length are read on the device
   // (counters[0], counters[1]) and `position` bounds them: it sizes the
   // launch and chooses the form.
-  const int32_t* pos_dev = counters;
-  const int32_t* ctx_dev = counters ? counters + 1 : nullptr;
-  const int32_t max_ctx = position + 1;
-  const bool fused = p.acc && max_ctx <= kFusedMaxCtx &&
-                     (static_cast<int64_t>(max_ctx) + p.block_size - 1) / p.block_size <= mie::kAttnOutMaxBlocks;
+  c->pos_dev = counters;
+  c->ctx_dev = counters ? counters + 1 : nullptr;
+  c->position = position;
+  c->max_ctx = position + 1;
+  c->fused = p.acc && c->max_ctx <= kFusedMaxCtx &&
+             (static_cast<int64_t>(c->max_ctx) + p.block_size - 1) / p.block_size <= mie::kAttnOutMaxBlocks;
+  c->ws_need = 0;
+  if (c->fused) return MIE_OK;
+  // The decode's split-context workspace is checked before anything is
+  // launched, so a call that cannot finish changes nothing.
+  const int32_t rc = mie_paged_decode_plan(1, p.num_heads, p.head_dim, p.block_size, c->max_ctx, p.dtype, 0, nullptr,
+                                           &c->ws_need);
+  if (rc != MIE_OK) return rc;
+  if (c->ws_need > p.workspace_bytes)
+    return mie::fail(MIE_ERR_WORKSPACE, "mie_block_decode: position %d needs a %lld-byte workspace, plan has %lld",
+                     position, static_cast<long long>(c->ws_need), static_cast<long long>(p.workspace_bytes));
+  return MIE_OK;
+}
+
+// The launches of a checked call.
+int32_t launch_call(const BlockCall& c, void* stream) {
+  const BlockPlan& p = c.p;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  int32_t rc;
-  if (fused) {
+  int32_t rc = qkv(p, c.emb, c.embed, c.x, c.pos_dev, c.position, stream);
+  if (rc != MIE_OK) return rc;
+  if (c.fused) {
     // Four launches: QKV into the pool, attention with the output projection
     // summed into acc, then the MoE half forming x + out_proj(a) itself.
-    rc = qkv(p, emb, token_id != nullptr, x, pos_dev, position, stream);
-    if (rc != MIE_OK) return rc;
     rc = mie::attn_out_launch(p.q, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head, p.num_blocks,
-                              p.block_table, p.block_table_len, ctx_dev, max_ctx, max_ctx, p.num_heads, p.head_dim,
-                              p.block_size, p.scale, p.w_out, p.acc, st);
+                              p.block_table, p.block_table_len, c.ctx_dev, c.max_ctx, c.max_ctx, p.num_heads,
+                              p.head_dim, p.block_size, p.scale, p.w_out, p.acc, st);
     if (rc != MIE_OK) return rc;
-    return mie_moe_decode_block_acc(x, p.acc, p.b_out, p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1,
+    return mie_moe_decode_block_acc(c.x, p.acc, p.b_out, p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1,
                                     p.b1, p.w2, p.b2, p.num_experts, p.top_k, p.dim, p.hidden, p.router_logits,
                                     p.expert_ids, p.route_weights, p.hidden_act, p.out, p.dtype, stream);
   }
-  // The decode's split-context workspace is checked before anything is
-  // launched, so a call that cannot finish changes nothing.
-  int64_t ws_need = 0;
-  rc = mie_paged_decode_plan(1, p.num_heads, p.head_dim, p.block_size, max_ctx, p.dtype, 0, nullptr, &ws_need);
-  if (rc != MIE_OK) return rc;
-  if (ws_need > p.workspace_bytes)
-    return mie::fail(MIE_ERR_WORKSPACE, "mie_block_decode: position %d needs a %lld-byte workspace, plan has %lld",
-                     position, static_cast<long long>(ws_need), static_cast<long long>(p.workspace_bytes));
-  rc = qkv(p, emb, token_id != nullptr, x, pos_dev, position, stream);
-  if (rc != MIE_OK) return rc;
   const int64_t row = static_cast<int64_t>(p.num_heads) * p.head_dim;
   rc = mie_paged_decode(p.q, row, p.head_dim, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head,
-                        p.num_blocks, p.block_table, p.block_table_len, ctx_dev, nullptr, max_ctx, max_ctx, 1,
+                        p.num_blocks, p.block_table, p.block_table_len, c.ctx_dev, nullptr, c.max_ctx, c.max_ctx, 1,
                         p.num_heads, p.head_dim, p.block_size, p.scale, p.attn, row, p.head_dim, p.dtype,
-                        ws_need ? p.workspace : nullptr, ws_need, 0, p.dtype, stream);
+                        c.ws_need ? p.workspace : nullptr, c.ws_need, 0, p.dtype, stream);
   if (rc != MIE_OK) return rc;
-  rc = mie_linear_residual(p.attn, p.w_out, p.b_out, x, p.h, p.dim, p.dim, p.dtype, stream);
+  rc = mie_linear_residual(p.attn, p.w_out, p.b_out, c.x, p.h, p.dim, p.dim, p.dtype, stream);
   if (rc != MIE_OK) return rc;
   return mie_moe_decode_block(p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1, p.b1, p.w2, p.b2,
                               p.num_experts, p.top_k, p.dim, p.hidden, p.router_logits, p.expert_ids,
                               p.route_weights, p.hidden_act, p.out, p.dtype, stream);
+}
+
+int32_t block_decode(const void* plan, const void* x, const int64_t* token_id, const int32_t* counters,
+                     int32_t position, void* stream) {
+  BlockCall c;
+  const int32_t rc = check_call(plan, x, token_id, counters, position, &c);
+  return rc != MIE_OK ? rc : launch_call(c, stream);
 }
 
 }  // namespace
@@ -311,5 +344,29 @@ extern "C" int32_t mie_block_plan_set_embedding(void* plan, const void* token_ta
   p.max_positions = max_positions;
   p.x_emb = x_out;
   memcpy(plan, &p, sizeof(p));
+  return MIE_OK;
+}
+
+extern "C" int32_t mie_blocks_decode(const void* const* plans, int32_t num_plans, const int64_t* token_id,
+                                     const int32_t* counters, int32_t position, void* stream) {
+  if (!plans || num_plans <= 0 || num_plans > kMaxStepBlocks)
+    return mie::fail(MIE_ERR_INVALID, "mie_blocks_decode: %d plans (1 to %d)", num_plans, kMaxStepBlocks);
+  if (!token_id) return mie::fail(MIE_ERR_INVALID, "mie_blocks_decode: null token id");
+  // Every block is checked before the first launch, so a call that cannot
+  // finish (a split context that outgrew a plan's workspace included)
+  // launches nothing; the second pass checks each block again (a few hundred
+  // nanoseconds) and launches it.  Block i > 0 reads block i - 1's output row.
+  for (int pass = 0; pass < 2; ++pass) {
+    const void* prev_out = nullptr;
+    for (int32_t i = 0; i < num_plans; ++i) {
+      BlockCall c;
+      int32_t rc = check_call(plans[i], prev_out, i == 0 ? token_id : nullptr, counters, position, &c);
+      if (rc != MIE_OK) return rc;
+      if (c.p.out == prev_out)
+        return mie::fail(MIE_ERR_INVALID, "mie_blocks_decode: blocks %d and %d share an output row", i - 1, i);
+      prev_out = c.p.out;
+      if (pass == 1 && (rc = launch_call(c, stream)) != MIE_OK) return rc;
+    }
+  }
   return MIE_OK;
 }

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -149,6 +149,7 @@ _SIGNATURES = {
     "mie_block_plan_launches": (_i32, [_c_void_p, _i32]),  # plan, position
     "mie_block_plan_set_embedding": (
         _i32, [_c_void_p, _c_void_p, _i32, _c_void_p, _i32, _c_void_p]),  # plan, tables, vocab, max positions, x_out
+    "mie_blocks_decode": (_i32, [_c_void_p, _i32, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plans, n, token id, counters, position, stream
     "mie_block_decode_embed": (_i32, [_c_void_p, _c_void_p, _c_void_p, _i32, _c_void_p]),  # plan, token id, ...
     "mie_attn_out_acc": (
         _i32,

@@ -61,9 +61,15 @@ def _tensors_replaced() -> None:
     _TENSOR_EPOCH[0] += 1
 
 
+# Plain attributes a launch plan is built from: a MoE layer's mode and a
+# norm's eps.  Changing one advances _TENSOR_EPOCH like a tensor replacement.
+_PLAN_SETTINGS = ("mode", "eps")
+
+
 class _TracksReplacement:
     """Mixin for the modules a launch plan reads from: conversion or
-    assignment of a tensor or submodule advances _TENSOR_EPOCH."""
+    assignment of a tensor or submodule, or a change of a setting in
+    _PLAN_SETTINGS, advances _TENSOR_EPOCH."""
 
     def _apply(self, fn, recurse=True):
         result = super()._apply(fn, recurse=recurse)
@@ -71,8 +77,9 @@ class _TracksReplacement:
         return result
 
     def __setattr__(self, name, value):
+        changed = name in _PLAN_SETTINGS and getattr(self, name, None) != value
         super().__setattr__(name, value)
-        if isinstance(value, (torch.Tensor, nn.Module)):
+        if changed or isinstance(value, (torch.Tensor, nn.Module)):
             _tensors_replaced()
 
     def register_buffer(self, name, tensor, persistent=True):
@@ -707,6 +714,13 @@ class TransformerMoEBlock(nn.Module):
         self._embed_row = None  # layer 0's embedding row for decode_token_ids
         self.register_load_state_dict_post_hook(TransformerMoEBlock._drop_plan_after_load)
 
+    def __getstate__(self):
+        # Copies and pickles leave the launch plans behind: a plan points at
+        # this block's tensors, and a copy builds its own on first use.
+        state = super().__getstate__().copy()
+        state.update(_one_token=None, _plans=collections.OrderedDict(), _embed_row=None)
+        return state
+
     def drop_decode_plan(self) -> None:
         """Forget the one-token launch plan; the next decode token builds a
         new one.  Conversions (.to(), .float(), ...), loads and assignments of
@@ -905,6 +919,7 @@ class TransformerMoEBlock(nn.Module):
 
         if tables is not None:
             launch.embed = launch_embed
+        launch.out = out
         launch.plan = plan
         launch.held = held
         launch.buffers = (q, attn, h, acc, plan, held)  # kept alive with the plan
@@ -922,6 +937,10 @@ class Model(nn.Module):
         self.MoEBlocks = nn.ModuleList(TransformerMoEBlock(config) for _ in range(config.num_layers))
         self.final_norm = LayerNorm(config.hidden_dim)
         self.output_projection.weight = self.token_embedding.weight  # tied
+        # The embedding and every block for one decode token as one library
+        # call over the blocks' launch plans (_run_decode_step): step key ->
+        # (cache weakref, plan array, launchers), the most recently used last.
+        self._steps = collections.OrderedDict()
 
     def new_cache(self, batch_size: int = 1) -> KVCache:
         weight = self.token_embedding.weight
@@ -972,9 +991,15 @@ class Model(nn.Module):
         assert position + seq_len <= self.max_seq_length, "KV cache is full"
         graph_pos = getattr(cache, "graph_pos", None)
         decode = position > 0 and seq_len == 1
+        one_token = decode and batch == 1 and len(self.MoEBlocks) and not torch.is_grad_enabled()
+        if one_token and graph_pos is None:
+            x = self._run_decode_step(token_ids, cache, position)
+            if x is not None:
+                cache.position += seq_len
+                return x
         if decode:
             self._preflight_decode(batch)
-        if decode and batch == 1 and len(self.MoEBlocks) and not torch.is_grad_enabled():
+        if one_token:
             # One decode token: the embedding inside layer 0's QKV launch when
             # its launch plan applies.
             x = self.MoEBlocks[0].decode_token_ids(token_ids, cache, position, self.token_embedding,
@@ -983,6 +1008,8 @@ class Model(nn.Module):
                 for i in range(1, len(self.MoEBlocks)):
                     x = self.MoEBlocks[i](x, cache, i, position)
                 cache.position += seq_len
+                if graph_pos is None:
+                    self._build_decode_step(token_ids, cache)
                 return x
         if graph_pos is not None:  # device-side position (HIP-graph decode, moe_engine.graphs)
             x = embedding.embed(token_ids, graph_pos, self.token_embedding, self.positional_embedding)
@@ -998,6 +1025,83 @@ class Model(nn.Module):
             x = block(x, cache, i, position)
         cache.position += seq_len
         return x
+
+    def _apply(self, fn, recurse=True):
+        # A conversion replaces the tensors the kept steps' plans point at.
+        self._steps.clear()
+        return super()._apply(fn, recurse=recurse)
+
+    def __getstate__(self):
+        # Copies and pickles leave the decode steps behind (they point at this
+        # model's buffers); a copy builds its own on first use.
+        state = super().__getstate__().copy()
+        state["_steps"] = collections.OrderedDict()
+        return state
+
+    @staticmethod
+    def _step_key(token_ids, cache):
+        """What a decode step is built for besides the blocks' plans: the
+        cache (by identity, with a weak reference beside it), its attention
+        mode, the allocator's fuse_qkv switch, the token's device and the
+        tensor epoch, which every conversion, replacement, MoE mode or norm
+        eps change advances - so the blocks' own plan keys hold too.  None
+        for a cache without a block pool."""
+        alloc = getattr(cache, "allocator", None)
+        if alloc is None:
+            return None
+        return id(cache), cache.attention_mode, alloc.fuse_qkv, token_ids.device, _TENSOR_EPOCH[0]
+
+    def _build_decode_step(self, token_ids, cache):
+        """After a decode token ran block by block from launch plans (layer 0
+        with the embedding inside its QKV launch), keep those plans as one
+        step for the cache's next tokens.  The step holds the plans'
+        launchers, which own their buffers, and no reference to the cache or
+        its pools; the last few steps are kept, so sequences decoded in turn
+        each find theirs."""
+        key = self._step_key(token_ids, cache)
+        if key is None:
+            return
+        step = self._steps.get(key)
+        if step is not None and step[0]() is cache:
+            return
+        launchers = []
+        for block in self.MoEBlocks:
+            plan = block._one_token
+            if plan is None or plan[2] is None or plan[1]() is not cache:
+                return
+            launchers.append(plan[2])
+        if not hasattr(launchers[0], "embed"):
+            return
+        plans = (ctypes.c_void_p * len(launchers))(*(ctypes.addressof(l.plan) for l in launchers))
+        self._steps[key] = (weakref.ref(cache), plans, launchers)
+        self._steps.move_to_end(key)
+        if len(self._steps) > _KEPT_PLANS:
+            self._steps.popitem(last=False)
+
+    def _run_decode_step(self, token_ids, cache, position):
+        """The embedding and every block for one decode token in one call
+        (mie_blocks_decode): the launches the blocks' plans make one by one,
+        in the same order, with the host's per-block work gone from the time
+        before the first launch.  None when no step was built for this key,
+        or when a split context outgrew a plan's workspace (nothing launched;
+        the blocks one by one then grow it)."""
+        if not self._steps:
+            return None
+        key = self._step_key(token_ids, cache)
+        step = self._steps.get(key)
+        if step is None or step[0]() is not cache:
+            return None
+        if not (token_ids.dtype == torch.int64 and token_ids.numel() == 1 and token_ids.is_contiguous()):
+            return None
+        _, plans, launchers = step
+        cache._reserve(position + 1)
+        rc = _native.lib().mie_blocks_decode(plans, len(launchers), token_ids.data_ptr(), None, position,
+                                             _native.stream_of(token_ids))
+        if rc == _native.ERR_WORKSPACE:
+            del self._steps[key]
+            return None
+        _native.check(rc, "mie_blocks_decode")
+        return launchers[-1].out
 
     def _preflight_decode(self, batch):
         """A forced-direct MoE must fail before layer 0 writes K/V or reserves

@@ -426,3 +426,42 @@ def test_submodule_changes_advance_the_plan_epoch():
     assert isinstance(block.attn_norm, torch.nn.LayerNorm) and isinstance(block.moe.router, torch.nn.Linear)
     assert isinstance(model.token_embedding, torch.nn.Embedding)
     assert "MoEBlocks.0.attention.out_proj.weight" in model.state_dict()
+
+
+def test_mode_and_eps_changes_advance_the_plan_epoch():
+    """A launch plan is built from a MoE layer's mode and each norm's eps:
+    changing either retires every plan and decode step (the epoch moves);
+    setting the value a module already holds does not."""
+    from moe_engine.model import _TENSOR_EPOCH
+
+    model = Model(ModelConfig(**TINY)).eval()
+    block = model.MoEBlocks[0]
+    before = _TENSOR_EPOCH[0]
+    block.moe.set_mode(block.moe.mode)
+    block.attn_norm.eps = block.attn_norm.eps
+    assert _TENSOR_EPOCH[0] == before
+    block.moe.set_mode("reference")
+    assert _TENSOR_EPOCH[0] == before + 1
+    block.moe_norm.eps = 1e-3
+    assert _TENSOR_EPOCH[0] == before + 2
+
+
+def test_copies_leave_launch_plans_and_steps_behind():
+    """A plan or decode step points at its own model's tensors, so deepcopy
+    and pickling give a model without them (it builds its own on first use);
+    the original keeps its own."""
+    import copy
+    import ctypes
+    import pickle
+
+    model = Model(ModelConfig(**TINY)).eval()
+    model._steps["key"] = (None, (ctypes.c_void_p * 2)(1, 2), [])  # pointers: not copyable themselves
+    block = model.MoEBlocks[1]
+    block._plans["key"] = ("key", None, None)
+    block._one_token = ("key", None, None)
+    for twin in (copy.deepcopy(model), pickle.loads(pickle.dumps(model))):
+        assert not twin._steps and all(not b._plans and b._one_token is None for b in twin.MoEBlocks)
+        for a, b in zip(model.state_dict().values(), twin.state_dict().values()):
+            assert torch.equal(a, b)
+    assert len(model._steps) == 1 and block._one_token is not None
+

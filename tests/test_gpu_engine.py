@@ -298,8 +298,16 @@ def test_block_plan_switches_forms_at_1024_tokens():
     ids = torch.randint(0, cfg["vocab_size"], (1, 1040), device="cuda")
     alloc = model.new_block_allocator(num_blocks=70, block_size=16, attention_mode="direct")
     cache = alloc.new_cache()
-    got = stepwise_logits(model, ids, cache, 1015)
+    calls = _CountedSteps()
+    try:
+        got = stepwise_logits(model, ids, cache, 1015)
+    finally:
+        calls.restore()
     cache.free()
+    # The one-call step built at 1016 tokens (no workspace) met the split
+    # context at 1024: it launched nothing, the blocks grew their workspaces
+    # one by one, and a new step served the rest.
+    assert calls.refused >= 1 and calls.done == (1040 - 1015 - 1) - calls.refused
     lib = _native.lib()
     for b in model.MoEBlocks:
         plan = b._one_token[2].plan
@@ -345,10 +353,109 @@ def test_block_plan_grows_its_workspace_for_split_contexts():
             for b, f in zip(blocks, saved):
                 b._decode_one_token = f
 
-    assert torch.equal(run(True), run(False))
+    calls = _CountedSteps()
+    try:
+        assert torch.equal(run(True), run(False))
+    finally:
+        calls.restore()
+    # The first decode token grew the workspaces block by block; the model's
+    # one-call step, built after it, served the tokens that followed.
+    assert calls.done == (2070 - 2055 - 1) - calls.refused
     for b in model.MoEBlocks:
         launcher = b._one_token[2]
         assert launcher is not None and launcher.held["ws"] is not None
+
+
+class _CountedSteps:
+    """Counts mie_blocks_decode calls (the model's one-call decode step):
+    those that ran and those refused for want of a workspace."""
+
+    def __init__(self):
+        self.lib = _native.lib()
+        self.real = self.lib.mie_blocks_decode
+        self.done = self.refused = 0
+
+        def counted(*args):
+            rc = self.real(*args)
+            if rc == _native.ERR_WORKSPACE:
+                self.refused += 1
+            elif rc == 0:
+                self.done += 1
+            return rc
+
+        self.lib.mie_blocks_decode = counted
+
+    def restore(self):
+        self.lib.mie_blocks_decode = self.real
+
+
+def test_decode_step_runs_every_block_in_one_call():
+    """After a sequence's first decode token has built the blocks' launch
+    plans, each later token runs the embedding and every block in one
+    library call (mie_blocks_decode) - the same launches, so the logits equal
+    the block-by-block path bit for bit.  Sequences decoded in turn keep their
+    own steps; a MoE mode or norm eps change retires the step (the epoch
+    moves) and the next tokens follow the change."""
+    print_case("one-call decode step")
+    torch.manual_seed(6)
+    model = Model(ModelConfig(**TINY_FUSED)).to("cuda").eval()
+    alloc = model.new_block_allocator(num_blocks=40, block_size=4, attention_mode="direct")
+    ids = torch.randint(0, TINY_FUSED["vocab_size"], (2, 30), device="cuda")
+
+    def block_by_block(rows, prefill):
+        saved = model._run_decode_step
+        model._run_decode_step = lambda *args, **kwargs: None
+        try:
+            cache = alloc.new_cache()
+            return stepwise_logits(model, rows, cache, prefill)
+        finally:
+            cache.free()
+            model._run_decode_step = saved
+
+    calls = _CountedSteps()
+    try:
+        cache = alloc.new_cache()
+        got = stepwise_logits(model, ids[:1], cache, 6)
+        cache.free()
+        assert calls.done == 30 - 6 - 1 and calls.refused == 0  # the first decode token builds the step
+        assert torch.equal(got, block_by_block(ids[:1], 6))
+
+        # Two sequences in turn: each finds its own step after its first token.
+        calls.done = 0
+        caches = [alloc.new_cache(), alloc.new_cache()]
+        steps = [[], []]
+        with torch.no_grad():
+            for s in range(2):
+                steps[s].append(model(ids[s : s + 1, :6], caches[s])[:, -1])
+            for t in range(6, 30):
+                for s in range(2):
+                    steps[s].append(model(ids[s : s + 1, t : t + 1], caches[s])[:, -1])
+        for c in caches:
+            c.free()
+        assert calls.done == 2 * (30 - 6 - 1)
+        for s in range(2):
+            assert torch.equal(torch.stack(steps[s], 1), block_by_block(ids[s : s + 1], 6))
+
+        # A norm eps change retires the step; the next tokens use the new eps.
+        calls.done = 0
+        model.MoEBlocks[1].moe_norm.eps = 1e-2
+        cache = alloc.new_cache()
+        got = stepwise_logits(model, ids[:1], cache, 6)
+        cache.free()
+        assert calls.done == 30 - 6 - 1
+        assert torch.equal(got, block_by_block(ids[:1], 6))
+
+        # The reference MoE path has no launch plan: no step while it is set.
+        calls.done = 0
+        model.set_moe_mode("reference")
+        cache = alloc.new_cache()
+        ref = stepwise_logits(model, ids[:1], cache, 6)
+        cache.free()
+        assert calls.done == 0
+        model.set_moe_mode("auto")
+        torch.testing.assert_close(ref, got, rtol=1e-4, atol=1e-4)
+    finally:
+        calls.restore()
 
 
 def test_embedding_folded_into_the_first_qkv_launch():
