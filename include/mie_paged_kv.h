@@ -271,8 +271,9 @@ int32_t mie_linear_residual(const void* x, const void* weight, const void* bias,
                             int32_t dtype, void* stream);
 
 /*
- * Router and top-k of the fused MoE decode for ONE token, float32
- * (fused_moe.route, fused_moe.py:274-309):
+ * Router and top-k of the fused MoE decode for ONE token (fused_moe.route,
+ * fused_moe.py:274-309), x and router_weight in `dtype` (float32 or
+ * bfloat16), the logits and route weights float32 in both:
  *
  *   router_logits[e] = router_weight[e, :] . x            e < num_experts
  *   expert_ids[s]    = the top_k experts, largest logit first, lower id on ties
@@ -286,7 +287,7 @@ int32_t mie_moe_route(const void* x, const void* router_weight, int32_t num_expe
                       void* route_weights, int32_t dtype, void* stream);
 
 /*
- * Fused top-k mixture of experts for ONE decode token, float32, with no
+ * Fused top-k mixture of experts for ONE decode token, with no
  * device-to-host synchronisation.  Replaces MoEFeedForward's PyTorch path for
  * a single token (model.py:443-461; its torch.where syncs once per expert) and
  * serves the reference's Triton fused MoE decode (fused_moe.py:312-380):
@@ -304,6 +305,14 @@ int32_t mie_moe_route(const void* x, const void* router_weight, int32_t num_expe
  * multiples of 4.  The routing outputs are those of mie_moe_route.  Two
  * launches on `stream` (the W1 launch routes in every workgroup); nothing
  * needs clearing beforehand.  dim <= 2048.
+ *
+ * dtype (float32 or bfloat16) is that of x, the weights, hidden_act and out;
+ * router_logits and route_weights are float32 either way, the routing the
+ * reference keeps in float32 (model.py:450-453).  Sums run in float32.  In
+ * bfloat16 each value is rounded where the reference's PyTorch path stores
+ * one: each Linear's output (sum plus bias, rounded once), GELU's, the route
+ * weight, the weighted product and each partial sum of the expert-id-ordered
+ * sum.
  */
 int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1,
                        const void* b1, const void* w2, const void* b2, int32_t num_experts,
@@ -318,8 +327,9 @@ int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1,
  *
  * with MoE as in mie_moe_decode (routing outputs and hidden_act filled the
  * same way) and the norm skipped when ln_weight is NULL.  The norm uses the
- * biased variance in float32 (nn.LayerNorm); the residual add rounds once.
- * Same arguments and limits as mie_moe_decode; out may alias x.  Two launches.
+ * biased variance in float32 (nn.LayerNorm), its output rounded to `dtype`;
+ * the residual add rounds once.  Same arguments, dtypes and limits as
+ * mie_moe_decode; out may alias x.  Two launches.
  */
 int32_t mie_moe_decode_block(const void* x, const void* ln_weight, const void* ln_bias,
                              float ln_eps, const void* router_weight, const void* w1,
@@ -452,8 +462,9 @@ int32_t mie_attn_out_acc(const void* q, const void* k_pool, const void* v_pool, 
  * and acc cleared to zeros for the next token.  Two launches: h_out is formed
  * in the W1 launch (every workgroup forms it in registers, one stores it), the
  * W2 launch adds it and clears acc.  Arguments and limits as
- * mie_moe_decode_block; acc (int64 [dim + 1]), h_out and b_out (may be NULL)
- * 16-byte aligned; h_out must not alias x.
+ * mie_moe_decode_block, float32 only (mie_attn_out_acc's dtype); acc (int64
+ * [dim + 1]), h_out and b_out (may be NULL) 16-byte aligned; h_out must not
+ * alias x.
  */
 int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_out, void* h_out,
                                  const void* ln_weight, const void* ln_bias, float ln_eps, const void* router_weight,
@@ -500,7 +511,7 @@ int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_o
  * used, and one plan serves calls in stream order.
  *
  * mie_block_plan_init makes every host check of the launches (built width,
- * head_dim and dtype - the MoE half is float32 only -, shapes, strides,
+ * head_dim and dtype, shapes, strides,
  * alignment, null pointers) and fails with their status, so an initialised
  * plan never stops between launches.  The decode reads at most
  * block_table_len table entries (block_table_len >= 1).  mie_block_decode

@@ -1,4 +1,5 @@
-// Fused top-k mixture-of-experts for one decode token (float32), no host sync.
+// Fused top-k mixture-of-experts for one decode token (float32 or bfloat16),
+// no host sync.
 //
 // Replaces, for a single token, the reference's PyTorch MoE path
 // (src/moe_engine/model.py:443-461), whose per-expert torch.where forces a
@@ -15,6 +16,15 @@
 // The sum runs in increasing expert id with a separate rounding of each
 // product, the order and rounding in which the reference's index_add_ loop
 // accumulates (model.py:455-460).  GELU is the exact erf form of nn.GELU().
+//
+// Storage is float32 or bfloat16 (weights, x, the GELU activations and the
+// output; the routing logits and weights are float32 in both, as the
+// reference keeps routing in float32, model.py:450-453).  Every product and
+// sum runs in float32.  For bfloat16 each result is rounded where the
+// reference's PyTorch path stores a bfloat16 tensor: the norm's output, each
+// Linear's output (its float32 sum plus bias, rounded once), GELU's, the
+// route weight, the weighted product and each partial sum of index_add_, and
+// the residual add.  For float32 none of these roundings changes a value.
 //
 // Expert weights live in four canonical contiguous storages - W1 [E, hidden,
 // dim], b1 [E, hidden], W2 [E, dim, hidden], b2 [E, dim] - so a selected
@@ -48,38 +58,71 @@ constexpr int kW2Chunks = K <= 2 ? 8 : (16 / K > 0 ? 16 / K : 1);
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef long long i64x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
+// Element storage: float32, or bfloat16 held as uint16_t.  A lane holds four
+// consecutive elements (16 bytes of float32, 8 of bfloat16) and works on them
+// in float32; R() rounds a float32 result to the storage type.
+template <typename T> struct Mem;
+template <> struct Mem<float> {
+  static __device__ __forceinline__ f32x4_t load4(const float* p) { return *reinterpret_cast<const f32x4_t*>(p); }
+  static __device__ __forceinline__ f32x4_t stream4(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
+  }
+  static __device__ __forceinline__ float get(const float* p) { return *p; }
+  static __device__ __forceinline__ void put(float* p, float v) { *p = v; }
+  static __device__ __forceinline__ float R(float v) { return v; }
+  static __device__ __forceinline__ f32x4_t R4(f32x4_t v) { return v; }
+};
+template <> struct Mem<uint16_t> {
+  static __device__ __forceinline__ f32x4_t widen(u32x2_t w) {
+    return f32x4_t{mie::bf16_lo(w.x), mie::bf16_hi(w.x), mie::bf16_lo(w.y), mie::bf16_hi(w.y)};
+  }
+  static __device__ __forceinline__ f32x4_t load4(const uint16_t* p) {
+    return widen(*reinterpret_cast<const u32x2_t*>(p));
+  }
+  static __device__ __forceinline__ f32x4_t stream4(const uint16_t* p) {
+    return widen(__builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p)));
+  }
+  static __device__ __forceinline__ float get(const uint16_t* p) {
+    return __uint_as_float(static_cast<uint32_t>(*p) << 16);
+  }
+  static __device__ __forceinline__ void put(uint16_t* p, float v) {
+    *p = static_cast<uint16_t>(mie::f32_to_bf16_bits(v));
+  }
+  static __device__ __forceinline__ float R(float v) { return __uint_as_float(mie::f32_to_bf16_bits(v) << 16); }
+  static __device__ __forceinline__ f32x4_t R4(f32x4_t v) { return f32x4_t{R(v.x), R(v.y), R(v.z), R(v.w)}; }
+};
+
+// Pointers marked T hold the storage type (float32 or bfloat16).
 struct MoeArgs {
-  const float* x;       // [dim]
-  const float* router;  // [E, dim]
-  const float* w1;      // [E, hidden, dim]
-  const float* b1;      // [E, hidden]
-  const float* w2;      // [E, dim, hidden]
-  const float* b2;      // [E, dim]
+  const void* x;       // T [dim]
+  const void* router;  // T [E, dim]
+  const void* w1;      // T [E, hidden, dim]
+  const void* b1;      // T [E, hidden]
+  const void* w2;      // T [E, dim, hidden]
+  const void* b2;      // T [E, dim]
   int32_t E, top_k, dim, hidden;
-  const float* ln_w;      // block form: norm weight [dim] (NULL: no norm)
-  const float* ln_b;      // block form: norm bias [dim] or NULL
+  const void* ln_w;      // T; block form: norm weight [dim] (NULL: no norm)
+  const void* ln_b;      // T; block form: norm bias [dim] or NULL
   float ln_eps;
-  const float* residual;  // block form: x, added to the output
+  const void* residual;  // T; block form: x, added to the output
   // Accumulator form (after mie_attn_out_acc): the block's input to the MoE
   // half is h = x + (acc * 2^-32 + b_out), formed in the W1 launch (h_out
   // written by workgroup (0, 0)); the W2 launch adds h_out as the residual
-  // and clears acc for the next token.
+  // and clears acc for the next token.  float32 storage only.
   const unsigned long long* acc;  // [dim + 1]; acc[dim] != 0: a partial was not representable
   const float* b_out;             // [dim] or NULL
   float* h_out;                   // [dim]
   unsigned long long* acc_clear;  // W2: acc to clear, or NULL
-  float* logits;   // [E]
+  float* logits;   // float32 [E]
   int32_t* ids;    // [top_k], largest logit first
-  float* weights;  // [top_k], same order
-  float* h;        // [top_k, hidden], same order
-  float* out;      // [dim]
+  float* weights;  // float32 [top_k], same order
+  void* h;         // T [top_k, hidden], same order
+  void* out;       // T [dim]
 };
 
 __device__ __forceinline__ f32x4_t load4(const float* p) { return *reinterpret_cast<const f32x4_t*>(p); }
-__device__ __forceinline__ f32x4_t stream4(const float* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
-}
 __device__ __forceinline__ float dot4(f32x4_t a, f32x4_t b, float s) {
   s = fmaf(a.x, b.x, s);
   s = fmaf(a.y, b.y, s);
@@ -87,10 +130,12 @@ __device__ __forceinline__ float dot4(f32x4_t a, f32x4_t b, float s) {
   return fmaf(a.w, b.w, s);
 }
 
-// Dot product of a row with a vector over one wavefront (16-byte slices per lane).
-__device__ __forceinline__ float wave_dot(const float* __restrict__ row, const float* __restrict__ v, int n, int lane) {
+// Dot product of a row with a vector over one wavefront (four elements per
+// lane per step), in float32.
+template <typename T>
+__device__ __forceinline__ float wave_dot(const T* __restrict__ row, const T* __restrict__ v, int n, int lane) {
   float s = 0.f;
-  for (int i = lane * 4; i < n; i += 256) s = dot4(load4(row + i), load4(v + i), s);
+  for (int i = lane * 4; i < n; i += 256) s = dot4(Mem<T>::load4(row + i), Mem<T>::load4(v + i), s);
   return mie::wave_sum(s);
 }
 
@@ -159,12 +204,14 @@ __device__ __forceinline__ void wave_topk(float logit, int top_k, int num_expert
 }
 
 // One workgroup: E router dot products, then top-k and softmax on wave 0.
+template <typename T>
 __global__ __launch_bounds__(256) void moe_route_kernel(MoeArgs a) {
   __shared__ float logits[kMaxExperts];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const T* router = static_cast<const T*>(a.router);
   for (int e = wave; e < a.E; e += 4) {
-    const float s = wave_dot(a.router + static_cast<int64_t>(e) * a.dim, a.x, a.dim, lane);
+    const float s = wave_dot(router + static_cast<int64_t>(e) * a.dim, static_cast<const T*>(a.x), a.dim, lane);
     if (lane == 0) {
       logits[e] = s;
       a.logits[e] = s;
@@ -204,9 +251,15 @@ __device__ __forceinline__ float wave_sum4(float r0, float r1, float r2, float r
 // behind the kernel's one barrier, every wave takes the top-k itself, then
 // computes 4 rows of slot blockIdx.y's expert.  hidden % 4 == 0, so a wave's
 // rows are all valid or all past the end.
-template <int NCH, bool NORM, bool ACC = false>
+template <typename T, int NCH, bool NORM, bool ACC = false>
 __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
+  static_assert(!ACC || sizeof(T) == 4, "the accumulator form is float32 only");
+  using M = Mem<T>;
   __shared__ float s_logits[kMaxExperts];
+  const T* __restrict__ xs = static_cast<const T*>(a.x);
+  const T* __restrict__ router = static_cast<const T*>(a.router);
+  const T* __restrict__ ln_w = static_cast<const T*>(a.ln_w);
+  const T* __restrict__ ln_b = static_cast<const T*>(a.ln_b);
   const int k = blockIdx.y;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -220,11 +273,11 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   for (int c = 0; c < NCH; ++c) {
     const int i = c * 256 + lane * 4;
     const bool valid = i < dim;
-    y[c] = valid ? load4(a.x + i) : zero;
-    gw[c] = NORM && valid ? load4(a.ln_w + i) : zero;
-    gb[c] = NORM && valid && a.ln_b ? load4(a.ln_b + i) : zero;
-    q0[c] = valid && e0 < a.E ? load4(a.router + static_cast<int64_t>(e0) * dim + i) : zero;
-    q1[c] = valid && e1 < a.E ? load4(a.router + static_cast<int64_t>(e1) * dim + i) : zero;
+    y[c] = valid ? M::load4(xs + i) : zero;
+    gw[c] = NORM && valid ? M::load4(ln_w + i) : zero;
+    gb[c] = NORM && valid && ln_b ? M::load4(ln_b + i) : zero;
+    q0[c] = valid && e0 < a.E ? M::load4(router + static_cast<int64_t>(e0) * dim + i) : zero;
+    q1[c] = valid && e1 < a.E ? M::load4(router + static_cast<int64_t>(e1) * dim + i) : zero;
   }
   // Accumulator form: the fixed-point sums, the output projection's bias and
   // the flag, loaded with the rest (unconditionally: lanes past dim re-read
@@ -234,7 +287,7 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   f32x4_t bo[NA];
   long long acc_flag = 0;
   if constexpr (ACC) {
-    const float* bsrc = a.b_out ? a.b_out : a.x;
+    const float* bsrc = a.b_out ? a.b_out : reinterpret_cast<const float*>(xs);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int i = c * 256 + lane * 4;
@@ -289,7 +342,9 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
     }
     const float rstd = rsqrtf(mie::wave_sum(q) / dim + a.ln_eps);
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) y[c] = (y[c] - mean) * rstd * gw[c] + gb[c];
+    // The norm's output is what the reference feeds the router and the
+    // experts: rounded to the storage type.
+    for (int c = 0; c < NCH; ++c) y[c] = M::R4((y[c] - mean) * rstd * gw[c] + gb[c]);
   }
 
   // 3. Router logits: experts wave and wave + 4 from registers, any others
@@ -312,7 +367,7 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const int i = c * 256 + lane * 4;
-        if (i < dim) l = dot4(load4(a.router + static_cast<int64_t>(e) * dim + i), y[c], l);
+        if (i < dim) l = dot4(M::load4(router + static_cast<int64_t>(e) * dim + i), y[c], l);
       }
       l = mie::wave_sum(l);
       if (lane == 0) s_logits[e] = l;
@@ -342,11 +397,13 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   // 5. Four rows of the selected expert's W1, GELU, into h[k].
   const int r0 = (blockIdx.x * 4 + wave) * 4;
   if (r0 >= a.hidden) return;
-  const float* __restrict__ w = a.w1 + (static_cast<int64_t>(e) * a.hidden + r0) * dim;
+  const T* __restrict__ w = static_cast<const T*>(a.w1) + (static_cast<int64_t>(e) * a.hidden + r0) * dim;
   // The bias of the row this lane stores, read with the weights rather than
   // after the reduction.
   const int r_out = r0 + (lane >> 4);
-  const float bias = (lane & 15) == 0 && r_out < a.hidden ? a.b1[static_cast<int64_t>(e) * a.hidden + r_out] : 0.f;
+  const float bias = (lane & 15) == 0 && r_out < a.hidden
+                         ? M::get(static_cast<const T*>(a.b1) + static_cast<int64_t>(e) * a.hidden + r_out)
+                         : 0.f;
   // All 4 x NCH row loads go out before the first multiply: unconditional,
   // with lanes past dim reading element 0 (y is zero there, and the product
   // is dropped below), since a load under a branch makes the compiler wait
@@ -357,7 +414,7 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
     const int i = c * 256 + lane * 4;
     const int ic = i < dim ? i : 0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wv[r][c] = stream4(w + r * dim + ic);
+    for (int r = 0; r < 4; ++r) wv[r][c] = M::stream4(w + r * dim + ic);
   }
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
@@ -371,34 +428,37 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   }
   const float t = wave_sum4(s0, s1, s2, s3, lane);
   if ((lane & 15) == 0) {
-    const float pre = t + bias;
-    a.h[static_cast<int64_t>(k) * a.hidden + r_out] = 0.5f * pre * (1.f + erff(pre * 0.70710678118654752440f));
+    const float pre = M::R(t + bias);  // the Linear's output
+    M::put(static_cast<T*>(a.h) + static_cast<int64_t>(k) * a.hidden + r_out,
+           0.5f * pre * (1.f + erff(pre * 0.70710678118654752440f)));
   }
 }
 
 // grid = ceil(dim / 4); each wave owns one output element and reads that row
 // of every selected expert's W2 at once.
-template <int K, bool RESID>
+template <typename T, int K, bool RESID>
 __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
+  using M = Mem<T>;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int j = blockIdx.x * 4 + wave;
   if (j >= a.dim) return;
   int e[K];
   float wt[K], bias[K];
-  const float* __restrict__ row[K];
+  const T* __restrict__ row[K];
+  const T* __restrict__ hs = static_cast<const T*>(a.h);
 #pragma unroll
   for (int s = 0; s < K; ++s) {
     e[s] = a.ids[s];
-    row[s] = a.w2 + (static_cast<int64_t>(e[s]) * a.dim + j) * a.hidden;
+    row[s] = static_cast<const T*>(a.w2) + (static_cast<int64_t>(e[s]) * a.dim + j) * a.hidden;
   }
   // The epilogue's reads go out with the row loads, not after the reduction.
 #pragma unroll
   for (int s = 0; s < K; ++s) {
     wt[s] = a.weights[s];
-    bias[s] = a.b2[static_cast<int64_t>(e[s]) * a.dim + j];
+    bias[s] = M::get(static_cast<const T*>(a.b2) + static_cast<int64_t>(e[s]) * a.dim + j);
   }
-  const float res = RESID ? a.residual[j] : 0.f;
+  const float res = RESID ? M::get(static_cast<const T*>(a.residual) + j) : 0.f;
   if (a.acc_clear && lane == 0) {
     // The attention's fixed-point sums were consumed by the W1 launch: ready
     // for the next token.
@@ -420,8 +480,8 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
       const bool valid = i < a.hidden;
 #pragma unroll
       for (int s = 0; s < K; ++s) {
-        q[s][u] = valid ? stream4(row[s] + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        hv[s][u] = valid ? load4(a.h + static_cast<int64_t>(s) * a.hidden + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        q[s][u] = valid ? M::stream4(row[s] + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        hv[s][u] = valid ? M::load4(hs + static_cast<int64_t>(s) * a.hidden + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
     }
 #pragma unroll
@@ -448,12 +508,15 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
 #pragma unroll
     for (int s = 0; s < K; ++s) {
       if (rank[s] == r) {
-        const float y = acc[s] + bias[s];
-        out = __fadd_rn(out, __fmul_rn(wt[s], y));
+        // The expert's output (its Linear's, rounded), the route weight in
+        // the storage type, their product, and the running sum, each rounded
+        // as index_add_ stores it.
+        const float y = M::R(acc[s] + bias[s]);
+        out = M::R(__fadd_rn(out, M::R(__fmul_rn(M::R(wt[s]), y))));
       }
     }
   }
-  a.out[j] = RESID ? __fadd_rn(res, out) : out;
+  M::put(static_cast<T*>(a.out) + j, RESID ? __fadd_rn(res, out) : out);
 }
 
 bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
@@ -461,7 +524,8 @@ bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0;
 int32_t check_route_args(const char* who, const void* x, const void* router_weight, int32_t num_experts,
                          int32_t top_k, int32_t dim, const void* logits, const void* ids, const void* weights,
                          int32_t dtype) {
-  if (dtype != MIE_DTYPE_F32) return mie::fail(MIE_ERR_UNSUPPORTED, "%s: float32 only", who);
+  if (dtype != MIE_DTYPE_F32 && dtype != MIE_DTYPE_BF16)
+    return mie::fail(MIE_ERR_UNSUPPORTED, "%s: float32 or bfloat16 only (dtype %d)", who, dtype);
   if (num_experts <= 0 || num_experts > kMaxExperts || top_k <= 0 || top_k > kMaxTopK || top_k > num_experts)
     return mie::fail(MIE_ERR_INVALID, "%s: experts=%d top_k=%d (at most %d and %d)", who, num_experts, top_k,
                      kMaxExperts, kMaxTopK);
@@ -475,8 +539,8 @@ int32_t check_route_args(const char* who, const void* x, const void* router_weig
 MoeArgs make_args(const void* x, const void* router_weight, int32_t num_experts, int32_t top_k, int32_t dim,
                   int32_t hidden, void* logits, void* ids, void* weights) {
   MoeArgs a{};
-  a.x = static_cast<const float*>(x);
-  a.router = static_cast<const float*>(router_weight);
+  a.x = x;
+  a.router = router_weight;
   a.E = num_experts;
   a.top_k = top_k;
   a.dim = dim;
@@ -487,12 +551,12 @@ MoeArgs make_args(const void* x, const void* router_weight, int32_t num_experts,
   return a;
 }
 
-template <int K>
+template <typename T, int K>
 void launch_w2(const MoeArgs& a, hipStream_t st) {
   if (a.residual) {
-    moe_w2_reduce_kernel<K, true><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
+    moe_w2_reduce_kernel<T, K, true><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
   } else {
-    moe_w2_reduce_kernel<K, false><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
+    moe_w2_reduce_kernel<T, K, false><<<(a.dim + 3) / 4, 256, 0, st>>>(a);
   }
 }
 
@@ -505,7 +569,11 @@ extern "C" int32_t mie_moe_route(const void* x, const void* router_weight, int32
                                 expert_ids, route_weights, dtype);
   if (rc != MIE_OK) return rc;
   const MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, 0, router_logits, expert_ids, route_weights);
-  moe_route_kernel<<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  if (dtype == MIE_DTYPE_F32) {
+    moe_route_kernel<float><<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  } else {
+    moe_route_kernel<uint16_t><<<1, 256, 0, static_cast<hipStream_t>(stream)>>>(a);
+  }
   return mie::check_launch("moe_route_kernel");
 }
 
@@ -522,46 +590,56 @@ int32_t check_expert_args(const char* who, int32_t hidden, int32_t dim, const vo
   return MIE_OK;
 }
 
-template <int NCH>
+template <typename T, int NCH>
 void launch_w1(const MoeArgs& a, hipStream_t st) {
   const dim3 grid((a.hidden + 15) / 16, a.top_k);
-  if (a.acc) {
-    if (a.ln_w) {
-      moe_w1_gelu_kernel<NCH, true, true><<<grid, 256, 0, st>>>(a);
-    } else {
-      moe_w1_gelu_kernel<NCH, false, true><<<grid, 256, 0, st>>>(a);
+  if constexpr (sizeof(T) == 4) {
+    if (a.acc) {
+      if (a.ln_w) {
+        moe_w1_gelu_kernel<T, NCH, true, true><<<grid, 256, 0, st>>>(a);
+      } else {
+        moe_w1_gelu_kernel<T, NCH, false, true><<<grid, 256, 0, st>>>(a);
+      }
+      return;
     }
-  } else if (a.ln_w) {
-    moe_w1_gelu_kernel<NCH, true><<<grid, 256, 0, st>>>(a);
+  }
+  if (a.ln_w) {
+    moe_w1_gelu_kernel<T, NCH, true><<<grid, 256, 0, st>>>(a);
   } else {
-    moe_w1_gelu_kernel<NCH, false><<<grid, 256, 0, st>>>(a);
+    moe_w1_gelu_kernel<T, NCH, false><<<grid, 256, 0, st>>>(a);
   }
 }
 
-int32_t launch_experts(MoeArgs& a, hipStream_t st) {
+template <typename T>
+int32_t launch_experts_as(const MoeArgs& a, hipStream_t st) {
   switch ((a.dim + 255) / 256) {
-    case 1: launch_w1<1>(a, st); break;
-    case 2: launch_w1<2>(a, st); break;
-    case 3: launch_w1<3>(a, st); break;
-    case 4: launch_w1<4>(a, st); break;
-    case 5: launch_w1<5>(a, st); break;
-    case 6: launch_w1<6>(a, st); break;
-    case 7: launch_w1<7>(a, st); break;
-    default: launch_w1<8>(a, st); break;
+    case 1: launch_w1<T, 1>(a, st); break;
+    case 2: launch_w1<T, 2>(a, st); break;
+    case 3: launch_w1<T, 3>(a, st); break;
+    case 4: launch_w1<T, 4>(a, st); break;
+    case 5: launch_w1<T, 5>(a, st); break;
+    case 6: launch_w1<T, 6>(a, st); break;
+    case 7: launch_w1<T, 7>(a, st); break;
+    default: launch_w1<T, 8>(a, st); break;
   }
   int32_t rc = mie::check_launch("moe_w1_gelu_kernel");
   if (rc != MIE_OK) return rc;
   switch (a.top_k) {
-    case 1: launch_w2<1>(a, st); break;
-    case 2: launch_w2<2>(a, st); break;
-    case 3: launch_w2<3>(a, st); break;
-    case 4: launch_w2<4>(a, st); break;
-    case 5: launch_w2<5>(a, st); break;
-    case 6: launch_w2<6>(a, st); break;
-    case 7: launch_w2<7>(a, st); break;
-    default: launch_w2<8>(a, st); break;
+    case 1: launch_w2<T, 1>(a, st); break;
+    case 2: launch_w2<T, 2>(a, st); break;
+    case 3: launch_w2<T, 3>(a, st); break;
+    case 4: launch_w2<T, 4>(a, st); break;
+    case 5: launch_w2<T, 5>(a, st); break;
+    case 6: launch_w2<T, 6>(a, st); break;
+    case 7: launch_w2<T, 7>(a, st); break;
+    default: launch_w2<T, 8>(a, st); break;
   }
   return mie::check_launch("moe_w2_reduce_kernel");
+}
+
+// dtype was checked: float32 or bfloat16 (the accumulator form float32 only).
+int32_t launch_experts(const MoeArgs& a, int32_t dtype, hipStream_t st) {
+  return dtype == MIE_DTYPE_F32 ? launch_experts_as<float>(a, st) : launch_experts_as<uint16_t>(a, st);
 }
 
 }  // namespace
@@ -576,13 +654,13 @@ extern "C" int32_t mie_moe_decode(const void* x, const void* router_weight, cons
   rc = check_expert_args("mie_moe_decode", hidden, dim, w1, b1, w2, b2, hidden_act, out);
   if (rc != MIE_OK) return rc;
   MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids, route_weights);
-  a.w1 = static_cast<const float*>(w1);
-  a.b1 = static_cast<const float*>(b1);
-  a.w2 = static_cast<const float*>(w2);
-  a.b2 = static_cast<const float*>(b2);
-  a.h = static_cast<float*>(hidden_act);
-  a.out = static_cast<float*>(out);
-  return launch_experts(a, static_cast<hipStream_t>(stream));
+  a.w1 = w1;
+  a.b1 = b1;
+  a.w2 = w2;
+  a.b2 = b2;
+  a.h = hidden_act;
+  a.out = out;
+  return launch_experts(a, dtype, static_cast<hipStream_t>(stream));
 }
 
 namespace mie {
@@ -611,6 +689,7 @@ int32_t moe_decode_block_acc_check(const void* x, const void* acc, const void* b
                                             top_k, dim, hidden, router_logits, expert_ids, route_weights,
                                             hidden_act, out, dtype);
   if (rc != MIE_OK) return rc;
+  if (dtype != MIE_DTYPE_F32) return mie::fail(MIE_ERR_UNSUPPORTED, "mie_moe_decode_block_acc: float32 only");
   if (!acc || !h_out || reinterpret_cast<uintptr_t>(acc) % 16 || !aligned16(h_out) || !aligned16(b_out))
     return mie::fail(MIE_ERR_INVALID, "mie_moe_decode_block_acc: acc and h_out (and b_out) must be non-NULL and "
                                       "16-byte aligned");
@@ -632,17 +711,17 @@ extern "C" int32_t mie_moe_decode_block(const void* x, const void* ln_weight, co
                                                  hidden_act, out, dtype);
   if (rc != MIE_OK) return rc;
   MoeArgs a = make_args(x, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids, route_weights);
-  a.ln_w = static_cast<const float*>(ln_weight);
-  a.ln_b = static_cast<const float*>(ln_bias);
+  a.ln_w = ln_weight;
+  a.ln_b = ln_bias;
   a.ln_eps = ln_eps;
-  a.residual = static_cast<const float*>(x);
-  a.w1 = static_cast<const float*>(w1);
-  a.b1 = static_cast<const float*>(b1);
-  a.w2 = static_cast<const float*>(w2);
-  a.b2 = static_cast<const float*>(b2);
-  a.h = static_cast<float*>(hidden_act);
-  a.out = static_cast<float*>(out);
-  return launch_experts(a, static_cast<hipStream_t>(stream));
+  a.residual = x;
+  a.w1 = w1;
+  a.b1 = b1;
+  a.w2 = w2;
+  a.b2 = b2;
+  a.h = hidden_act;
+  a.out = out;
+  return launch_experts(a, dtype, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_out, void* h_out,
@@ -658,20 +737,20 @@ extern "C" int32_t mie_moe_decode_block_acc(const void* x, const void* acc, cons
   if (rc != MIE_OK) return rc;
   MoeArgs a = make_args(h_out, router_weight, num_experts, top_k, dim, hidden, router_logits, expert_ids,
                         route_weights);
-  a.x = static_cast<const float*>(x);  // the W1 launch reads x and forms h_out
+  a.x = x;  // the W1 launch reads x and forms h_out
   a.acc = static_cast<const unsigned long long*>(acc);
   a.b_out = static_cast<const float*>(b_out);
   a.h_out = static_cast<float*>(h_out);
   a.acc_clear = static_cast<unsigned long long*>(const_cast<void*>(acc));
-  a.ln_w = static_cast<const float*>(ln_weight);
-  a.ln_b = static_cast<const float*>(ln_bias);
+  a.ln_w = ln_weight;
+  a.ln_b = ln_bias;
   a.ln_eps = ln_eps;
-  a.residual = static_cast<const float*>(h_out);
-  a.w1 = static_cast<const float*>(w1);
-  a.b1 = static_cast<const float*>(b1);
-  a.w2 = static_cast<const float*>(w2);
-  a.b2 = static_cast<const float*>(b2);
-  a.h = static_cast<float*>(hidden_act);
-  a.out = static_cast<float*>(out);
-  return launch_experts(a, static_cast<hipStream_t>(stream));
+  a.residual = h_out;
+  a.w1 = w1;
+  a.b1 = b1;
+  a.w2 = w2;
+  a.b2 = b2;
+  a.h = hidden_act;
+  a.out = out;
+  return launch_experts(a, dtype, static_cast<hipStream_t>(stream));
 }

@@ -1,4 +1,4 @@
-"""Fused batch-one float32 MoE decode on MI355X through hand-written HIP kernels.
+"""Fused batch-one MoE decode on MI355X through hand-written HIP kernels.
 
 Drop-in for the reference's src/moe_engine/fused_moe.py: the same functions
 (`is_configuration_supported`, `is_supported`, `has_canonical_layout`, `route`,
@@ -24,6 +24,12 @@ Semantics (fused_moe.py:119-262, model.py:443-461):
 The reference's Triton kernel sums the slots in route order; here they are
 summed in expert-id order with each product rounded, as the PyTorch path's
 index_add_ loop does, so the two paths differ only in their dot products.
+
+The reference's kernels are float32 only.  These also take bfloat16 weights
+and activations: the routing stays float32 (its logits and weights
+workspaces are float32 for either dtype), every sum runs in float32, and each
+bfloat16 value is rounded where the PyTorch path stores one (each Linear's
+output, GELU's, the route weight, the weighted product, each partial sum).
 """
 
 import torch
@@ -33,7 +39,8 @@ from moe_engine import _native
 HAS_HIP = _native.HAS_HIP
 MAX_EXPERTS = 64
 MAX_TOP_K = 8
-MAX_HIDDEN_DIM = 2048  # the W1 kernel holds x in 8 16-byte loads per lane
+MAX_HIDDEN_DIM = 2048  # the W1 kernel holds x in 8 loads per lane
+DTYPES = (torch.float32, torch.bfloat16)
 
 
 def is_configuration_supported(
@@ -52,7 +59,7 @@ def is_configuration_supported(
         HAS_HIP
         and torch.device(device).type == "cuda"
         and torch.version.hip is not None
-        and dtype == torch.float32
+        and dtype in DTYPES
         and batch_size == 1
         and 0 < num_experts <= MAX_EXPERTS
         and 0 < top_k <= min(MAX_TOP_K, num_experts)
@@ -83,28 +90,32 @@ def is_supported(x: torch.Tensor, *, num_experts: int, top_k: int, expert_hidden
 def has_canonical_layout(router_weight, w1, b1, w2, b2, router_logits, expert_ids, route_weights, hidden, out) -> bool:
     """Shapes, contiguity, dtypes and device of the direct-kernel weights and
     workspaces (reference fused_moe.py:77-114), for the shape the router
-    weight [E, dim] and w1 [E, expert_hidden, dim] describe."""
+    weight [E, dim] and w1 [E, expert_hidden, dim] describe: the weights and
+    the hidden and output workspaces in the router weight's dtype (float32 or
+    bfloat16), the routing workspaces in float32."""
     if router_weight.dim() != 2 or w1.dim() != 3:
         return False
     num_experts, dim = router_weight.shape
     expert_hidden = w1.shape[1]
     top_k = expert_ids.numel()
-    float_parts = (
-        (router_weight, (num_experts, dim)),
-        (w1, (num_experts, expert_hidden, dim)),
-        (b1, (num_experts, expert_hidden)),
-        (w2, (num_experts, dim, expert_hidden)),
-        (b2, (num_experts, dim)),
-        (router_logits, (num_experts,)),
-        (route_weights, (top_k,)),
-        (hidden, (top_k, expert_hidden)),
-        (out, (dim,)),
+    dtype = router_weight.dtype
+    parts = (
+        (router_weight, (num_experts, dim), dtype),
+        (w1, (num_experts, expert_hidden, dim), dtype),
+        (b1, (num_experts, expert_hidden), dtype),
+        (w2, (num_experts, dim, expert_hidden), dtype),
+        (b2, (num_experts, dim), dtype),
+        (router_logits, (num_experts,), torch.float32),
+        (route_weights, (top_k,), torch.float32),
+        (hidden, (top_k, expert_hidden), dtype),
+        (out, (dim,), dtype),
     )
     device = router_weight.device
     return (
-        all(
-            t.shape == shape and t.is_contiguous() and t.device == device and t.dtype == torch.float32
-            for t, shape in float_parts
+        dtype in DTYPES
+        and all(
+            t.shape == shape and t.is_contiguous() and t.device == device and t.dtype == want
+            for t, shape, want in parts
         )
         and expert_ids.shape == (top_k,)
         and expert_ids.is_contiguous()
@@ -113,20 +124,25 @@ def has_canonical_layout(router_weight, w1, b1, w2, b2, router_logits, expert_id
     )
 
 
-def _require_rocm_float32(*tensors: torch.Tensor) -> None:
-    """Errors of the reference's _require_cuda_float32 (fused_moe.py:265-271)."""
-    if not HAS_HIP or any(not _native.is_rocm_device(t) for t in tensors):
+def _require_rocm(tensors, routing=()) -> None:
+    """Errors of the reference's _require_cuda_float32 (fused_moe.py:265-271):
+    `tensors` (activations and parameters) in one dtype, float32 or bfloat16;
+    `routing` (the logits and weights workspaces) in float32."""
+    everything = (*tensors, *routing)
+    if not HAS_HIP or any(not _native.is_rocm_device(t) for t in everything):
         raise RuntimeError("direct MoE needs a ROCm device and the HIP library")
-    if any(t.dtype != torch.float32 for t in tensors):
-        raise RuntimeError("direct MoE needs float32 activations and parameters")
-    if any(t.device != tensors[0].device for t in tensors[1:]):
+    if tensors[0].dtype not in DTYPES or any(t.dtype != tensors[0].dtype for t in tensors[1:]):
+        raise RuntimeError("direct MoE needs float32 or bfloat16 activations and parameters, all of one dtype")
+    if any(t.dtype != torch.float32 for t in routing):
+        raise RuntimeError("direct MoE keeps its routing logits and weights in float32")
+    if any(t.device != everything[0].device for t in everything[1:]):
         raise ValueError("direct MoE tensors must be on the same ROCm device")
 
 
 def route(x, router_weight, router_logits, expert_ids, route_weights) -> None:
     """Router logits, top-k expert ids and their softmax weights, written into
     the three workspaces (reference fused_moe.py:274-309)."""
-    _require_rocm_float32(x, router_weight, router_logits, route_weights)
+    _require_rocm((x, router_weight), (router_logits, route_weights))
     if router_weight.dim() != 2 or not router_weight.is_contiguous():
         raise ValueError("direct MoE router weight must be a contiguous [experts, hidden] matrix")
     num_experts, dim = router_weight.shape
@@ -157,8 +173,8 @@ def decode(x, router_weight, w1_base, b1_base, w2_base, b2_base, *, router_logit
            hidden, out) -> torch.Tensor:
     """Router, the selected W1 + GELU rows and the weighted W2 sum for one
     token; returns `out` viewed as [1, 1, hidden] (reference fused_moe.py:312-380)."""
-    _require_rocm_float32(x, router_weight, w1_base, b1_base, w2_base, b2_base, router_logits, route_weights,
-                          hidden, out)
+    _require_rocm((x, router_weight, w1_base, b1_base, w2_base, b2_base, hidden, out),
+                  (router_logits, route_weights))
     if not has_canonical_layout(router_weight, w1_base, b1_base, w2_base, b2_base, router_logits, expert_ids,
                                 route_weights, hidden, out):
         raise ValueError("direct MoE weights and workspaces must use canonical layouts")
@@ -184,8 +200,8 @@ def decode_block(x, norm_weight, norm_bias, norm_eps, router_weight, w1_base, b1
     filled as decode() fills them.  norm_weight None skips the norm.  Returns
     `out` viewed as [1, 1, hidden]."""
     params = [t for t in (norm_weight, norm_bias) if t is not None]
-    _require_rocm_float32(x, router_weight, w1_base, b1_base, w2_base, b2_base, router_logits, route_weights,
-                          hidden, out, *params)
+    _require_rocm((x, router_weight, w1_base, b1_base, w2_base, b2_base, hidden, out, *params),
+                  (router_logits, route_weights))
     if not has_canonical_layout(router_weight, w1_base, b1_base, w2_base, b2_base, router_logits, expert_ids,
                                 route_weights, hidden, out):
         raise ValueError("direct MoE weights and workspaces must use canonical layouts")

@@ -18,7 +18,7 @@ replay it reserves the block the new token needs (one host-to-device copy of
 one block id every block_size tokens); the replay itself never allocates.
 
 Only greedy decoding (temperature 0) over a PagedKVCache whose attention can
-run the direct kernel, with the fused float32 MoE, is captured; everything
+run the direct kernel, with the fused MoE (float32 or bfloat16), is captured; everything
 else uses Model.generate.
 """
 
@@ -49,7 +49,8 @@ class GraphedDecoder:
             # host synchronization), which a graph cannot hold.
             moe = block.moe
             if moe.mode == "reference" or not moe.direct_configuration_supported(1):
-                raise RuntimeError("graph decode needs the fused MoE decode kernel (mode 'auto' or 'direct', float32)")
+                raise RuntimeError("graph decode needs the fused MoE decode kernel (mode 'auto' or 'direct', "
+                                   "float32 or bfloat16)")
         if not projection.supported(model.config.hidden_dim, weight.dtype):
             raise RuntimeError("graph decode needs the HIP LM head for this width and dtype")
         if cache.position <= 0:

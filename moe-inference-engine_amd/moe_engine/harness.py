@@ -140,11 +140,12 @@ def attention_micro(config=None, contexts=(16, 64, 256, 1024), device="cuda", dt
 def greedy_pick(logits):
     """The next token from [1, S, vocab] logits: the argmax of the last
     position, as the reference's timed loop takes it
-    (benchmarks/ab_compare.py:58,64).  On a ROCm device in float32 it is one
-    mie_argmax launch, the pick Model.generate makes at temperature 0; else
+    (benchmarks/ab_compare.py:58,64).  On a ROCm device it is one library
+    launch, the pick Model.generate makes at temperature 0 (the merge of the
+    LM head's kept picks, or mie_argmax over a float32 row); else
     torch.argmax.  Both give torch.argmax's index (first maximum, NaN largest)."""
     last = logits[:, -1, :]
-    if last.dtype == torch.float32 and last.is_contiguous() and _native.is_rocm_device(last):
+    if last.is_contiguous() and projection.can_argmax(last.reshape(-1)):
         return projection.argmax(last.reshape(-1)).view(1, 1)
     return last.argmax(dim=-1, keepdim=True)
 

@@ -480,7 +480,7 @@ class MoEFeedForward(_TracksReplacement, nn.Module):
     Mode 'reference' runs the reference's PyTorch path (model.py:443-461)
     everywhere.  In mode 'auto' or 'direct', one-token decode runs the fused
     HIP kernels (moe_engine.fused_moe) where they apply - a ROCm device, the
-    HIP library, float32, one token - and a float32 prefill of up to 512
+    HIP library, float32 or bfloat16, one token - and a float32 prefill of up to 512
     tokens on a ROCm device runs dense-masked (_forward_dense: the reference's
     result without its per-expert synchronisations).  'auto' falls back to the
     PyTorch path elsewhere; a forced 'direct' decode that cannot run raises
@@ -547,6 +547,12 @@ class MoEFeedForward(_TracksReplacement, nn.Module):
         # Device / dtype conversion replaces each parameter on its own.
         result = super()._apply(fn, recurse=recurse)
         self._pack_expert_parameters()
+        # The routing workspaces stay float32 whatever the model's dtype (the
+        # reference routes in float32); the others follow the conversion.
+        for name in ("_router_logits", "_route_weights"):
+            buf = getattr(self, name)
+            if buf.dtype != torch.float32:
+                setattr(self, name, buf.float())
         return result
 
     def set_mode(self, mode: str) -> None:
@@ -584,7 +590,7 @@ class MoEFeedForward(_TracksReplacement, nn.Module):
     @staticmethod
     def _raise_direct_unsupported() -> None:
         raise RuntimeError(
-            "MoE mode 'direct' needs one-token batch-one float32 decode on a ROCm device with the HIP "
+            "MoE mode 'direct' needs one-token batch-one float32 or bfloat16 decode on a ROCm device with the HIP "
             "library (at most 64 experts, top-k at most 8, dimensions multiples of 4); use 'auto' for "
             "automatic fallback or 'reference' for the PyTorch oracle"
         )
@@ -680,8 +686,8 @@ class MoEFeedForward(_TracksReplacement, nn.Module):
             self.mode == "reference"
             or not isinstance(norm, nn.LayerNorm)
             or norm.weight is None
-            or norm.weight.dtype != torch.float32
-            or (norm.bias is not None and norm.bias.dtype != torch.float32)
+            or norm.weight.dtype != x.dtype
+            or (norm.bias is not None and norm.bias.dtype != x.dtype)
             or tuple(norm.normalized_shape) != (self.dim,)
             or not self._direct_supported(x)
         )
@@ -691,7 +697,7 @@ class MoEFeedForward(_TracksReplacement, nn.Module):
         (mie_moe_decode_block: the norm and routing in the W1 launch, the
         residual add in the W2 launch), or None when the fused kernels do not
         apply - mode 'reference', an unsupported configuration, or a norm that
-        is not a float32 LayerNorm over the hidden size."""
+        is not a LayerNorm over the hidden size in x's dtype."""
         if not self.fused_block_supported(x, norm):
             return None
         s = self._expert_storage
@@ -1140,7 +1146,7 @@ class Model(nn.Module):
         for _ in range(max_new_tokens):
             logits = self(step_input, cache)[:, -1, :]
             if temperature == 0:
-                if logits.dtype == torch.float32 and logits.is_contiguous() and _native.is_rocm_device(logits):
+                if projection.can_argmax(logits.view(-1)):
                     next_token = projection.argmax(logits.view(-1)).view(1, 1)  # one launch, same pick
                 else:
                     next_token = torch.argmax(logits, dim=-1, keepdim=True)

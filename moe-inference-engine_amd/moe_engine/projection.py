@@ -88,9 +88,9 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     head_workspace_bytes(vocab)) holds the per-workgroup picks; it is
     allocated when None.  `advance` (a contiguous int32 device tensor, with
     token_out): every element is incremented by one after the pick, in the
-    same launch.  keep_pick (without token_out, float32): the launch leaves
-    its picks in a workspace of this module's, and argmax(out) merges them
-    while out is unmodified and no later keep_pick call replaced them.
+    same launch.  keep_pick (without token_out): the launch leaves its picks
+    in a workspace of this module's, and argmax(out) merges them while out is
+    unmodified and no later keep_pick call replaced them.
     Returns out."""
     global _last_pick
     weight, bias = linear.weight, linear.bias
@@ -118,7 +118,7 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     elif out.numel() != vocab or not out.is_contiguous():
         raise ValueError(f"out must hold {vocab} contiguous values")
     ws_ptr, ws_bytes = 0, 0
-    keep_pick = keep_pick and token_out is None and dtype == torch.float32 and not out.is_inference()
+    keep_pick = keep_pick and token_out is None and not out.is_inference()
     if keep_pick:
         key = (device, vocab)
         workspace = _pick_workspaces.get(key)
@@ -158,14 +158,24 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     return out
 
 
+def can_argmax(x) -> bool:
+    """Whether argmax(x) applies: a contiguous float32 vector on a ROCm
+    device, or the unmodified output of the last lm_head(keep_pick=True) in
+    either dtype."""
+    if not (_native.is_rocm_device(x) and x.is_contiguous()) or x.numel() == 0:
+        return False
+    return x.dtype == torch.float32 or _kept_picks(x) is not None
+
+
 def argmax(x, out=None):
-    """torch.argmax of the contiguous float32 device vector x (the first index
-    of the maximum, NaN counting as the largest), written to `out` (an int64
-    device tensor of one element, allocated when None): a merge of the head's
-    kept picks when x is the unmodified output of the last
-    lm_head(keep_pick=True), else one pass over x.  Returns out."""
-    if not (_native.is_rocm_device(x) and x.dtype == torch.float32 and x.is_contiguous()) or x.numel() == 0:
-        raise ValueError("mie_argmax takes a non-empty contiguous float32 vector on a ROCm device")
+    """torch.argmax of the contiguous device vector x (the first index of the
+    maximum, NaN counting as the largest), written to `out` (an int64 device
+    tensor of one element, allocated when None): a merge of the head's kept
+    picks when x is the unmodified output of the last lm_head(keep_pick=True)
+    (float32 or bfloat16), else one pass over x (float32).  Returns out."""
+    if not can_argmax(x):
+        raise ValueError("mie_argmax takes a non-empty contiguous float32 vector on a ROCm device, or the "
+                         "unmodified logits of the last lm_head(keep_pick=True)")
     if out is None:
         out = torch.empty(1, dtype=torch.int64, device=x.device)
     elif out.dtype != torch.int64 or out.numel() != 1 or out.device != x.device:

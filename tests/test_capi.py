@@ -160,7 +160,9 @@ def _valid_plan_args(**over):
 
 
 @pytest.mark.parametrize("change,code,message", [
-    (dict(dtype=1), 2, b"float32 only"),            # bf16 passes the attention half, the MoE half refuses it
+    (dict(dtype=1), 0, b""),                        # bf16: five launches (no fused attention + out_proj)
+    (dict(hidden=130), 1, b"hidden=130"),           # an expert width only the MoE half sees
+    (dict(dtype=3), 2, b""),                        # a dtype no launch is built for
     (dict(head_dim=48, heads=1, dim=48, sblk=16 * 48, shead=16 * 48), 2, b""),  # a head_dim the decode lacks
     (dict(table_len=0), 1, b"block table"),
     (dict(w1=(1 << 20) + 4), 1, b"aligned"),

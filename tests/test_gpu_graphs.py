@@ -176,9 +176,10 @@ def test_generate_graphed_matches_generate():
 
 
 def test_graph_decoder_needs_fused_moe():
-    """bf16 MoE and mode 'reference' run the PyTorch expert loop, which
-    synchronizes the host; the decoder refuses them before touching the cache."""
-    for dtype, mode in ((torch.bfloat16, "auto"), (torch.float32, "reference")):
+    """Mode 'reference' runs the PyTorch expert loop, which synchronizes the
+    host; the decoder refuses it, in either dtype, before touching the cache.
+    (bfloat16 models with the fused MoE are captured: test_gpu_moe_bf16.)"""
+    for dtype, mode in ((torch.bfloat16, "reference"), (torch.float32, "reference")):
         model = tiny_model(dtype).set_moe_mode(mode)
         cache = model.new_block_allocator(num_blocks=8, block_size=4, attention_mode="direct").new_cache()
         with torch.no_grad():

@@ -199,8 +199,11 @@ def test_canonical_storage_survives_device_apply():
 
 
 def test_forced_direct_preflight_preserves_paged_cache_at_block_boundary():
+    # The reference's case (tests/test_fused_moe.py:167-197) makes the direct
+    # MoE unavailable through bfloat16, which its kernels lack; these kernels
+    # take bfloat16, so float64 plays that part here.
     torch.manual_seed(0)
-    model = Model(ModelConfig(**TINY)).to("cuda").bfloat16().eval()
+    model = Model(ModelConfig(**TINY)).to("cuda").double().eval()
     allocator = model.new_block_allocator(num_blocks=4, block_size=4)
     cache = allocator.new_cache()
     ids = torch.randint(0, 96, (1, 4), device="cuda")
