@@ -465,3 +465,26 @@ def test_copies_leave_launch_plans_and_steps_behind():
             assert torch.equal(a, b)
     assert len(model._steps) == 1 and block._one_token is not None
 
+
+
+def test_bfloat16_layers_keep_float32_routing_workspaces():
+    """A dtype conversion follows the experts, the GELU activations and the
+    output workspace, but the routing logits and weights stay float32 (the
+    reference routes in float32); the canonical layout check accepts the
+    bfloat16 layer, and the fused kernels stay off away from a ROCm device."""
+    from moe_engine import fused_moe
+
+    layer = MoEFeedForward(32, 64, 4, 2).to(torch.bfloat16)
+    assert layer._router_logits.dtype == torch.float32 and layer._route_weights.dtype == torch.float32
+    assert layer._expert_hidden.dtype == torch.bfloat16 and layer._direct_out.dtype == torch.bfloat16
+    assert layer._expert_storage["w1"].dtype == torch.bfloat16
+    assert layer._has_direct_layout()
+    assert not layer.direct_configuration_supported(1)  # CPU
+    layer = layer.float()
+    assert layer._expert_hidden.dtype == torch.float32 and layer._has_direct_layout()
+    s = layer._expert_storage
+    # A routing workspace in the model dtype is not the canonical layout.
+    assert not fused_moe.has_canonical_layout(
+        layer.router.weight.bfloat16(), s["w1"].bfloat16(), s["b1"].bfloat16(), s["w2"].bfloat16(),
+        s["b2"].bfloat16(), layer._router_logits.bfloat16(), layer._expert_ids, layer._route_weights,
+        layer._expert_hidden.bfloat16(), layer._direct_out.bfloat16())
