@@ -438,13 +438,16 @@ int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_st
  *
  * and adds round(y_h[i] * 2^32) into acc[i] (int64, dim + 1 entries) with
  * integer atomics, so acc[i] = sum_h round(y_h[i] * 2^32) is exact and the
- * same whatever order the workgroups run in.  A y_h[i] of magnitude 2^31 or
- * more (or NaN) is not added: acc[dim] is set instead.  acc must hold zeros
+ * same whatever order the workgroups run in.  A y_h[i] of magnitude 2^31 / H
+ * or more (or NaN) is not added - the sum of H such partials could leave
+ * int64 - and acc[dim] is set instead.  acc must hold zeros
  * beforehand (mie_moe_decode_block_acc clears it after use).  ctx is *ctx_dev
  * when ctx_dev is non-NULL (device int32), else `ctx`; either is clamped to
  * max_ctx, and max_ctx spans at most 1024 blocks.  q [H * D], the pools (one
- * layer, element strides, as mie_paged_decode) and W_out are float32 and
- * 16-byte aligned; head_dim 32, 64 or 128; block_table holds block_table_len
+ * layer, element strides, as mie_paged_decode) and W_out are in `dtype`
+ * (float32 or bfloat16) and 16-byte aligned; every product and sum is float32,
+ * and in bfloat16 a_h is rounded to bfloat16 before the projection, as the
+ * decode stores it.  head_dim 32, 64 or 128; block_table holds block_table_len
  * entries (ids outside the pool are skipped, as in the decode).
  */
 int32_t mie_attn_out_acc(const void* q, const void* k_pool, const void* v_pool, int64_t pool_stride_block,
@@ -462,9 +465,10 @@ int32_t mie_attn_out_acc(const void* q, const void* k_pool, const void* v_pool, 
  * and acc cleared to zeros for the next token.  Two launches: h_out is formed
  * in the W1 launch (every workgroup forms it in registers, one stores it), the
  * W2 launch adds it and clears acc.  Arguments and limits as
- * mie_moe_decode_block, float32 only (mie_attn_out_acc's dtype); acc (int64
- * [dim + 1]), h_out and b_out (may be NULL) 16-byte aligned; h_out must not
- * alias x.
+ * mie_moe_decode_block; in bfloat16 the projection's output and the
+ * residual are each rounded to bfloat16 (as mie_linear_residual stores them).
+ * acc (int64 [dim + 1]), h_out and b_out (may be NULL) 16-byte aligned; h_out
+ * must not alias x.
  */
 int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_out, void* h_out,
                                  const void* ln_weight, const void* ln_bias, float ln_eps, const void* router_weight,
@@ -479,7 +483,7 @@ int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_o
  * mie_block_decode(plan, x, counters, position, stream) issues, on `stream`:
  *
  * with an accumulator (`acc` non-NULL, used when mie_attn_out_acc is built for
- * the shape - float32, head_dim 32, 64 or 128 - and ignored otherwise) and
+ * the shape - float32 or bfloat16, head_dim 32, 64 or 128 - and ignored otherwise) and
  * position + 1 <= 1024, four launches:
  *   mie_qkv_append(x, attn norm, in_proj, pools, block_table, position) -> q
  *   mie_attn_out_acc(q, pools, block_table, ctx = position + 1, out_proj) -> acc

@@ -38,9 +38,12 @@
 // workgroup's W_out slice - is read in the first memory round; the K/V tiles
 // in the second (one round per 32 tokens per wave).
 //
-// float32 pools, head_dim 32, 64 or 128, contexts up to kMaxTable blocks.  A
-// context block whose id lies outside the pool is never read; the head's
-// attention is then NaN (as the decode kernels write), which sets acc[dim].
+// float32 or bfloat16 (q, the pools and W_out in one dtype; every product and
+// sum in float32, the head's attention output rounded to the dtype before the
+// projection, as the decode kernels store it), head_dim 32, 64 or 128,
+// contexts up to kMaxTable blocks.  A context block whose id lies outside the
+// pool is never read; the head's attention is then NaN (as the decode kernels
+// write), which sets acc[dim].
 #include <math.h>
 
 #include "mie_common.h"
@@ -61,9 +64,9 @@ constexpr float kFix = 4294967296.0f;  // 2^32
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 struct AttnOutArgs {
-  const float* q;  // [H * D]
-  const float* k;  // one layer's pools
-  const float* v;
+  const void* q;  // T [H * D]
+  const void* k;  // T: one layer's pools
+  const void* v;
   int64_t sblk, shead;  // element strides
   int32_t num_blocks;
   const int32_t* bt;
@@ -75,7 +78,7 @@ struct AttnOutArgs {
   int32_t H;
   mie::FastDiv bs;
   float qk_scale;  // scale * log2(e)
-  const float* w;  // W_out [dim, dim] row-major
+  const void* w;  // T: W_out [dim, dim] row-major
   int32_t dim;
   int32_t R;  // row blocks per head
   int32_t rows_per_block;
@@ -107,8 +110,9 @@ __device__ __forceinline__ void merge_state(float& m, float& l, f32x4_t& o, floa
   m = mm;
 }
 
-template <int D>
+template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
+  using M = mie::Mem<T>;
   constexpr int LPT = Shape<D>::LPT;
   constexpr int TPL = Shape<D>::TPL;
   __shared__ int32_t s_bt[kMaxTable];
@@ -129,17 +133,16 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   // Round 1, all independent: this workgroup's W_out rows, q, the block
   // table up to the host's bound (nblk_max entries, at most 1024 = 4 per
   // thread), and the live length.
-  f32x4_t wv[kRowSteps];
+  typename M::raw4 wv[kRowSteps];
   const int row0 = rblk * a.rows_per_block;
   const int row_end = min(a.dim, row0 + a.rows_per_block);
 #pragma unroll
   for (int s = 0; s < kRowSteps; ++s) {
     int row = row0 + (s * kWaves + wave) * TPL + g;
     row = row < row_end ? row : row0;  // in bounds; the product is dropped below
-    wv[s] = __builtin_nontemporal_load(
-        reinterpret_cast<const f32x4_t*>(a.w + static_cast<int64_t>(row) * a.dim + h * D + c4));
+    wv[s] = M::stream_raw(static_cast<const T*>(a.w) + static_cast<int64_t>(row) * a.dim + h * D + c4);
   }
-  const f32x4_t qv = *reinterpret_cast<const f32x4_t*>(a.q + h * D + c4);
+  const typename M::raw4 qraw = M::load_raw(static_cast<const T*>(a.q) + h * D + c4);
   constexpr int kTablePerThread = kMaxTable / 256;
   int tb[kTablePerThread];
 #pragma unroll
@@ -166,13 +169,13 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
 
   // Round 2..: this wave's tokens t = (step * 4 + wave) * TPL + g, kBatch wave
   // loads of K and V per round; online softmax per TPL-row group.
-  const float* kh = a.k + static_cast<int64_t>(h) * a.shead + c4;
-  const float* vh = a.v + static_cast<int64_t>(h) * a.shead + c4;
+  const T* kh = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.shead + c4;
+  const T* vh = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.shead + c4;
   float m = -INFINITY, l = 0.f;
   f32x4_t o = {0.f, 0.f, 0.f, 0.f};
   const int steps = (ctx + kWaves * TPL - 1) / (kWaves * TPL);
   for (int s0 = 0; s0 < steps; s0 += kBatch) {
-    f32x4_t kv[kBatch], vv[kBatch];
+    typename M::raw4 kv[kBatch], vv[kBatch];
     bool valid[kBatch];
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
@@ -185,14 +188,14 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       const int64_t off = static_cast<int64_t>(blk) * a.sblk + static_cast<int64_t>(tc - lb * a.bs.d) * D;
       // Plain (temporal) loads: the R workgroups of this head run on one XCD
       // and read the same K/V, so all but the first hit its L2.
-      kv[b] = *reinterpret_cast<const f32x4_t*>(kh + off);
-      vv[b] = *reinterpret_cast<const f32x4_t*>(vh + off);
+      kv[b] = M::load_raw(kh + off);
+      vv[b] = M::load_raw(vh + off);
     }
     float sc[kBatch];
     float mb = m;
 #pragma unroll
     for (int b = 0; b < kBatch; ++b) {
-      sc[b] = mie::group_sum<LPT>(dot4(qv, kv[b], 0.f)) * a.qk_scale;
+      sc[b] = mie::group_sum<LPT>(dot4(M::widen(qraw), M::widen(kv[b]), 0.f)) * a.qk_scale;
       sc[b] = valid[b] ? sc[b] : -INFINITY;
       mb = fmaxf(mb, sc[b]);
     }
@@ -204,7 +207,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       for (int b = 0; b < kBatch; ++b) {
         const float p = valid[b] ? mie::fast_exp2(sc[b] - mb) : 0.f;
         l += p;
-        o += p * vv[b];
+        o += p * M::widen(vv[b]);
       }
       m = mb;
     }
@@ -237,7 +240,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       merge_state(mm, ll, oo, s_ml[w][0], s_ml[w][1], *reinterpret_cast<const f32x4_t*>(&s_o[w][c4]));
     // No key at all: scaled_dot_product_attention's zeros.  A context block
     // outside the pool gives NaN, as the decode kernels write.
-    f32x4_t r = ll > 0.f ? oo / ll : f32x4_t{0.f, 0.f, 0.f, 0.f};
+    f32x4_t r = M::R4(ll > 0.f ? oo / ll : f32x4_t{0.f, 0.f, 0.f, 0.f});
     if (any_bad) r = f32x4_t{NAN, NAN, NAN, NAN};
     *reinterpret_cast<f32x4_t*>(&s_attn[c4]) = r;
   }
@@ -248,7 +251,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
 #pragma unroll
   for (int s = 0; s < kRowSteps; ++s) {
     const int row = row0 + (s * kWaves + wave) * TPL + g;
-    const float y = mie::group_sum<LPT>(dot4(wv[s], av, 0.f));
+    const float y = mie::group_sum<LPT>(dot4(M::widen(wv[s]), av, 0.f));
     if (lane % LPT == 0 && row < row_end) {
       if (fabsf(y) < a.fix_limit) {
         const long long fx = llrintf(y * kFix);
@@ -268,7 +271,8 @@ int32_t attn_out_check(const void* q, const void* k_pool, const void* v_pool, in
                        int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
                        int32_t block_table_len, int32_t max_ctx, int32_t num_heads, int32_t head_dim,
                        int32_t block_size, const void* w_out, const void* acc, int32_t dtype) {
-  if (dtype != MIE_DTYPE_F32) return mie::fail(MIE_ERR_UNSUPPORTED, "mie_attn_out_acc: float32 only");
+  if (dtype != MIE_DTYPE_F32 && dtype != MIE_DTYPE_BF16)
+    return mie::fail(MIE_ERR_UNSUPPORTED, "mie_attn_out_acc: float32 or bfloat16 only (dtype %d)", dtype);
   if (head_dim != 32 && head_dim != 64 && head_dim != 128)
     return mie::fail(MIE_ERR_UNSUPPORTED, "mie_attn_out_acc: head_dim %d (32, 64 or 128)", head_dim);
   if (num_heads <= 0 || num_heads > 4096 || block_size <= 0 || num_blocks <= 0 || block_table_len <= 0)
@@ -293,11 +297,11 @@ int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, i
                         int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
                         int32_t block_table_len, const int32_t* ctx_dev, int32_t ctx, int32_t max_ctx,
                         int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, const void* w_out,
-                        void* acc, hipStream_t stream) {
+                        void* acc, int32_t dtype, hipStream_t stream) {
   AttnOutArgs a{};
-  a.q = static_cast<const float*>(q);
-  a.k = static_cast<const float*>(k_pool);
-  a.v = static_cast<const float*>(v_pool);
+  a.q = q;
+  a.k = k_pool;
+  a.v = v_pool;
   a.sblk = pool_stride_block;
   a.shead = pool_stride_head;
   a.num_blocks = num_blocks;
@@ -310,7 +314,7 @@ int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, i
   a.H = num_heads;
   a.bs = mie::FastDiv::make(static_cast<uint32_t>(block_size));
   a.qk_scale = scale * kLog2e;
-  a.w = static_cast<const float*>(w_out);
+  a.w = w_out;
   a.dim = num_heads * head_dim;
   a.acc = static_cast<unsigned long long*>(acc);
   a.fix_limit = 2147483648.0f / static_cast<float>(num_heads);  // H partials of |y| * 2^32 < 2^63 / H
@@ -318,10 +322,20 @@ int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, i
   a.rows_per_block = kWaves * tpl * kRowSteps;
   a.R = (a.dim + a.rows_per_block - 1) / a.rows_per_block;
   const dim3 grid(8 * a.R * ((num_heads + 7) / 8));
+  const bool f32 = dtype == MIE_DTYPE_F32;
   switch (head_dim) {
-    case 32: attn_out_kernel<32><<<grid, 256, 0, stream>>>(a); break;
-    case 64: attn_out_kernel<64><<<grid, 256, 0, stream>>>(a); break;
-    default: attn_out_kernel<128><<<grid, 256, 0, stream>>>(a); break;
+    case 32:
+      if (f32) attn_out_kernel<float, 32><<<grid, 256, 0, stream>>>(a);
+      else attn_out_kernel<uint16_t, 32><<<grid, 256, 0, stream>>>(a);
+      break;
+    case 64:
+      if (f32) attn_out_kernel<float, 64><<<grid, 256, 0, stream>>>(a);
+      else attn_out_kernel<uint16_t, 64><<<grid, 256, 0, stream>>>(a);
+      break;
+    default:
+      if (f32) attn_out_kernel<float, 128><<<grid, 256, 0, stream>>>(a);
+      else attn_out_kernel<uint16_t, 128><<<grid, 256, 0, stream>>>(a);
+      break;
   }
   return mie::check_launch("attn_out_kernel");
 }
@@ -341,5 +355,5 @@ extern "C" int32_t mie_attn_out_acc(const void* q, const void* k_pool, const voi
     return mie::fail(MIE_ERR_INVALID, "mie_attn_out_acc: ctx %d outside [0, max_ctx=%d]", ctx, max_ctx);
   return mie::attn_out_launch(q, k_pool, v_pool, pool_stride_block, pool_stride_head, num_blocks, block_table,
                               block_table_len, ctx_dev, ctx, max_ctx, num_heads, head_dim, block_size, scale, w_out,
-                              acc, static_cast<hipStream_t>(stream));
+                              acc, dtype, static_cast<hipStream_t>(stream));
 }

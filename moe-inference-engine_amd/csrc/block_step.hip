@@ -270,7 +270,7 @@ int32_t launch_call(const BlockCall& c, void* stream) {
     // summed into acc, then the MoE half forming x + out_proj(a) itself.
     rc = mie::attn_out_launch(p.q, p.k_pool, p.v_pool, p.pool_stride_block, p.pool_stride_head, p.num_blocks,
                               p.block_table, p.block_table_len, c.ctx_dev, c.max_ctx, c.max_ctx, p.num_heads,
-                              p.head_dim, p.block_size, p.scale, p.w_out, p.acc, st);
+                              p.head_dim, p.block_size, p.scale, p.w_out, p.acc, p.dtype, st);
     if (rc != MIE_OK) return rc;
     return mie_moe_decode_block_acc(c.x, p.acc, p.b_out, p.h, p.moe_ln_w, p.moe_ln_b, p.moe_ln_eps, p.router, p.w1,
                                     p.b1, p.w2, p.b2, p.num_experts, p.top_k, p.dim, p.hidden, p.router_logits,

@@ -77,6 +77,61 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
 }
 
+// ---- element storage: float32 or bfloat16 ----------------------------------
+// Kernels that take either dtype hold four consecutive elements per lane (16
+// bytes of float32, 8 of bfloat16, held as uint16_t) and work on them in
+// float32; R() rounds a float32 result to the storage type (the identity for
+// float32).  raw4 is the loaded form: a kernel that wants many loads in
+// flight keeps raw words and widens them where it uses them, since a widen
+// right after each load makes the compiler wait for that load first.
+typedef float mem_f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int mem_u32x2 __attribute__((ext_vector_type(2)));
+template <typename T> struct Mem;
+template <> struct Mem<float> {
+  typedef mem_f32x4 raw4;
+  static __device__ __forceinline__ raw4 load_raw(const float* p) { return *reinterpret_cast<const raw4*>(p); }
+  static __device__ __forceinline__ raw4 stream_raw(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const raw4*>(p));
+  }
+  static __device__ __forceinline__ raw4 zero_raw() { return raw4{0.f, 0.f, 0.f, 0.f}; }
+  static __device__ __forceinline__ mem_f32x4 widen(raw4 r) { return r; }
+  static __device__ __forceinline__ mem_f32x4 load4(const float* p) { return *reinterpret_cast<const mem_f32x4*>(p); }
+  static __device__ __forceinline__ mem_f32x4 stream4(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const mem_f32x4*>(p));
+  }
+  static __device__ __forceinline__ float get(const float* p) { return *p; }
+  static __device__ __forceinline__ void put(float* p, float v) { *p = v; }
+  static __device__ __forceinline__ void put4(float* p, mem_f32x4 v) { *reinterpret_cast<mem_f32x4*>(p) = v; }
+  static __device__ __forceinline__ float R(float v) { return v; }
+  static __device__ __forceinline__ mem_f32x4 R4(mem_f32x4 v) { return v; }
+};
+template <> struct Mem<uint16_t> {
+  typedef mem_u32x2 raw4;
+  static __device__ __forceinline__ raw4 load_raw(const uint16_t* p) { return *reinterpret_cast<const raw4*>(p); }
+  static __device__ __forceinline__ raw4 stream_raw(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const raw4*>(p));
+  }
+  static __device__ __forceinline__ raw4 zero_raw() { return raw4{0u, 0u}; }
+  static __device__ __forceinline__ mem_f32x4 widen(mem_u32x2 w) {
+    return mem_f32x4{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+  }
+  static __device__ __forceinline__ mem_f32x4 load4(const uint16_t* p) {
+    return widen(*reinterpret_cast<const mem_u32x2*>(p));
+  }
+  static __device__ __forceinline__ mem_f32x4 stream4(const uint16_t* p) {
+    return widen(__builtin_nontemporal_load(reinterpret_cast<const mem_u32x2*>(p)));
+  }
+  static __device__ __forceinline__ float get(const uint16_t* p) {
+    return __uint_as_float(static_cast<uint32_t>(*p) << 16);
+  }
+  static __device__ __forceinline__ void put(uint16_t* p, float v) { *p = static_cast<uint16_t>(f32_to_bf16_bits(v)); }
+  static __device__ __forceinline__ void put4(uint16_t* p, mem_f32x4 v) {
+    *reinterpret_cast<mem_u32x2*>(p) = mem_u32x2{pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w)};
+  }
+  static __device__ __forceinline__ float R(float v) { return __uint_as_float(f32_to_bf16_bits(v) << 16); }
+  static __device__ __forceinline__ mem_f32x4 R4(mem_f32x4 v) { return mem_f32x4{R(v.x), R(v.y), R(v.z), R(v.w)}; }
+};
+
 // ---- wavefront reductions -------------------------------------------------
 // DPP controls (CDNA3/4 ISA): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E,
 // row_half_mirror = 0x141 (lane i <-> 7-i within 8), row_mirror = 0x140
@@ -191,7 +246,7 @@ int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, i
                         int64_t pool_stride_head, int32_t num_blocks, const int32_t* block_table,
                         int32_t block_table_len, const int32_t* ctx_dev, int32_t ctx, int32_t max_ctx,
                         int32_t num_heads, int32_t head_dim, int32_t block_size, float scale, const void* w_out,
-                        void* acc, hipStream_t stream);
+                        void* acc, int32_t dtype, hipStream_t stream);
 int32_t moe_decode_block_acc_check(const void* x, const void* acc, const void* b_out, const void* h_out,
                                    const void* ln_weight, const void* ln_bias, const void* router_weight,
                                    const void* w1, const void* b1, const void* w2, const void* b2,

@@ -50,49 +50,16 @@ namespace {
 
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
-constexpr int kMaxDim = 2048;  // the W1 kernel holds x in 8 16-byte loads per lane
-// W2 kernel: 16-byte loads per lane per slot per round, 8 for top-1 and
+constexpr int kMaxDim = 2048;  // the W1 kernel holds x in 8 four-element loads per lane
+// W2 kernel: four-element loads per lane per slot per round, 8 for top-1 and
 // top-2 and 16 / K beyond, so a round holds 16 weight and 16 hidden loads.
 template <int K>
 constexpr int kW2Chunks = K <= 2 ? 8 : (16 / K > 0 ? 16 / K : 1);
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef long long i64x2_t __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
-// Element storage: float32, or bfloat16 held as uint16_t.  A lane holds four
-// consecutive elements (16 bytes of float32, 8 of bfloat16) and works on them
-// in float32; R() rounds a float32 result to the storage type.
-template <typename T> struct Mem;
-template <> struct Mem<float> {
-  static __device__ __forceinline__ f32x4_t load4(const float* p) { return *reinterpret_cast<const f32x4_t*>(p); }
-  static __device__ __forceinline__ f32x4_t stream4(const float* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(p));
-  }
-  static __device__ __forceinline__ float get(const float* p) { return *p; }
-  static __device__ __forceinline__ void put(float* p, float v) { *p = v; }
-  static __device__ __forceinline__ float R(float v) { return v; }
-  static __device__ __forceinline__ f32x4_t R4(f32x4_t v) { return v; }
-};
-template <> struct Mem<uint16_t> {
-  static __device__ __forceinline__ f32x4_t widen(u32x2_t w) {
-    return f32x4_t{mie::bf16_lo(w.x), mie::bf16_hi(w.x), mie::bf16_lo(w.y), mie::bf16_hi(w.y)};
-  }
-  static __device__ __forceinline__ f32x4_t load4(const uint16_t* p) {
-    return widen(*reinterpret_cast<const u32x2_t*>(p));
-  }
-  static __device__ __forceinline__ f32x4_t stream4(const uint16_t* p) {
-    return widen(__builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(p)));
-  }
-  static __device__ __forceinline__ float get(const uint16_t* p) {
-    return __uint_as_float(static_cast<uint32_t>(*p) << 16);
-  }
-  static __device__ __forceinline__ void put(uint16_t* p, float v) {
-    *p = static_cast<uint16_t>(mie::f32_to_bf16_bits(v));
-  }
-  static __device__ __forceinline__ float R(float v) { return __uint_as_float(mie::f32_to_bf16_bits(v) << 16); }
-  static __device__ __forceinline__ f32x4_t R4(f32x4_t v) { return f32x4_t{R(v.x), R(v.y), R(v.z), R(v.w)}; }
-};
+using mie::Mem;
 
 // Pointers marked T hold the storage type (float32 or bfloat16).
 struct MoeArgs {
@@ -110,10 +77,10 @@ struct MoeArgs {
   // Accumulator form (after mie_attn_out_acc): the block's input to the MoE
   // half is h = x + (acc * 2^-32 + b_out), formed in the W1 launch (h_out
   // written by workgroup (0, 0)); the W2 launch adds h_out as the residual
-  // and clears acc for the next token.  float32 storage only.
+  // and clears acc for the next token.
   const unsigned long long* acc;  // [dim + 1]; acc[dim] != 0: a partial was not representable
-  const float* b_out;             // [dim] or NULL
-  float* h_out;                   // [dim]
+  const void* b_out;              // T [dim] or NULL
+  void* h_out;                    // T [dim]
   unsigned long long* acc_clear;  // W2: acc to clear, or NULL
   float* logits;   // float32 [E]
   int32_t* ids;    // [top_k], largest logit first
@@ -122,7 +89,6 @@ struct MoeArgs {
   void* out;       // T [dim]
 };
 
-__device__ __forceinline__ f32x4_t load4(const float* p) { return *reinterpret_cast<const f32x4_t*>(p); }
 __device__ __forceinline__ float dot4(f32x4_t a, f32x4_t b, float s) {
   s = fmaf(a.x, b.x, s);
   s = fmaf(a.y, b.y, s);
@@ -253,7 +219,6 @@ __device__ __forceinline__ float wave_sum4(float r0, float r1, float r2, float r
 // rows are all valid or all past the end.
 template <typename T, int NCH, bool NORM, bool ACC = false>
 __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
-  static_assert(!ACC || sizeof(T) == 4, "the accumulator form is float32 only");
   using M = Mem<T>;
   __shared__ float s_logits[kMaxExperts];
   const T* __restrict__ xs = static_cast<const T*>(a.x);
@@ -266,33 +231,46 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   const int dim = a.dim;
   const int e0 = wave, e1 = wave + 4;
 
-  // 1. All global reads that do not depend on the routing.
+  // 1. All global reads that do not depend on the routing, kept as loaded
+  //    and widened after the last one is issued.
   f32x4_t y[NCH], gw[NCH], gb[NCH], q0[NCH], q1[NCH];
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  {
+    typename M::raw4 ry[NCH], rgw[NCH], rgb[NCH], rq0[NCH], rq1[NCH];
+    const typename M::raw4 zr = M::zero_raw();
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int i = c * 256 + lane * 4;
-    const bool valid = i < dim;
-    y[c] = valid ? M::load4(xs + i) : zero;
-    gw[c] = NORM && valid ? M::load4(ln_w + i) : zero;
-    gb[c] = NORM && valid && ln_b ? M::load4(ln_b + i) : zero;
-    q0[c] = valid && e0 < a.E ? M::load4(router + static_cast<int64_t>(e0) * dim + i) : zero;
-    q1[c] = valid && e1 < a.E ? M::load4(router + static_cast<int64_t>(e1) * dim + i) : zero;
+    for (int c = 0; c < NCH; ++c) {
+      const int i = c * 256 + lane * 4;
+      const bool valid = i < dim;
+      ry[c] = valid ? M::load_raw(xs + i) : zr;
+      rgw[c] = NORM && valid ? M::load_raw(ln_w + i) : zr;
+      rgb[c] = NORM && valid && ln_b ? M::load_raw(ln_b + i) : zr;
+      rq0[c] = valid && e0 < a.E ? M::load_raw(router + static_cast<int64_t>(e0) * dim + i) : zr;
+      rq1[c] = valid && e1 < a.E ? M::load_raw(router + static_cast<int64_t>(e1) * dim + i) : zr;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      y[c] = M::widen(ry[c]);
+      gw[c] = M::widen(rgw[c]);
+      gb[c] = M::widen(rgb[c]);
+      q0[c] = M::widen(rq0[c]);
+      q1[c] = M::widen(rq1[c]);
+    }
   }
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
   // Accumulator form: the fixed-point sums, the output projection's bias and
   // the flag, loaded with the rest (unconditionally: lanes past dim re-read
   // element 0 and drop it), so they add no memory round.
   constexpr int NA = ACC ? NCH : 1;
   i64x2_t acc_lo[NA], acc_hi[NA];
-  f32x4_t bo[NA];
+  typename M::raw4 bo[NA];
   long long acc_flag = 0;
   if constexpr (ACC) {
-    const float* bsrc = a.b_out ? a.b_out : reinterpret_cast<const float*>(xs);
+    const T* bsrc = a.b_out ? static_cast<const T*>(a.b_out) : xs;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int i = c * 256 + lane * 4;
       const int ic = i < dim ? i : 0;
-      bo[c] = load4(bsrc + ic);
+      bo[c] = M::load_raw(bsrc + ic);
       acc_lo[c] = *reinterpret_cast<const i64x2_t*>(a.acc + ic);
       acc_hi[c] = *reinterpret_cast<const i64x2_t*>(a.acc + ic + 2);
     }
@@ -305,15 +283,16 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
     // h = x + (acc * 2^-32 + b_out): the attention output projection summed
     // over heads in fixed point (int64 -> float is one rounding, the power of
     // two scale is exact), its bias, then the residual - the rounding points
-    // of x + out_proj(a).
+    // of x + out_proj(a): the projection's output, then the sum, each rounded
+    // to the storage type.
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int i = c * 256 + lane * 4;
       f32x4_t o = {static_cast<float>(acc_lo[c].x), static_cast<float>(acc_lo[c].y),
                    static_cast<float>(acc_hi[c].x), static_cast<float>(acc_hi[c].y)};
       o *= 2.3283064365386963e-10f;  // 2^-32
-      if (a.b_out) o += bo[c];
-      f32x4_t hv = y[c] + o;
+      if (a.b_out) o += M::widen(bo[c]);
+      f32x4_t hv = M::R4(y[c] + M::R4(o));
       if (acc_flag != 0) hv = f32x4_t{NAN, NAN, NAN, NAN};
       y[c] = i < dim ? hv : zero;
     }
@@ -321,7 +300,7 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
 #pragma unroll
       for (int c = 0; c < NCH; ++c) {
         const int i = c * 256 + lane * 4;
-        if (i < dim) *reinterpret_cast<f32x4_t*>(a.h_out + i) = y[c];
+        if (i < dim) M::put4(static_cast<T*>(a.h_out) + i, y[c]);
       }
     }
   }
@@ -408,22 +387,22 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   // with lanes past dim reading element 0 (y is zero there, and the product
   // is dropped below), since a load under a branch makes the compiler wait
   // for it before the next one.
-  f32x4_t wv[4][NCH];
+  typename M::raw4 wv[4][NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int i = c * 256 + lane * 4;
     const int ic = i < dim ? i : 0;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) wv[r][c] = M::stream4(w + r * dim + ic);
+    for (int r = 0; r < 4; ++r) wv[r][c] = M::stream_raw(w + r * dim + ic);
   }
   float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     if (c * 256 + lane * 4 < dim) {
-      s0 = dot4(wv[0][c], y[c], s0);
-      s1 = dot4(wv[1][c], y[c], s1);
-      s2 = dot4(wv[2][c], y[c], s2);
-      s3 = dot4(wv[3][c], y[c], s3);
+      s0 = dot4(M::widen(wv[0][c]), y[c], s0);
+      s1 = dot4(M::widen(wv[1][c]), y[c], s1);
+      s2 = dot4(M::widen(wv[2][c]), y[c], s2);
+      s3 = dot4(M::widen(wv[3][c]), y[c], s3);
     }
   }
   const float t = wave_sum4(s0, s1, s2, s3, lane);
@@ -473,22 +452,22 @@ __global__ __launch_bounds__(256) void moe_w2_reduce_kernel(MoeArgs a) {
   // values (one round at FFN width 2048).  Each lane still accumulates its
   // chunks in increasing order.
   for (int i0 = lane * 4; i0 < a.hidden; i0 += 256 * kW2Chunks<K>) {
-    f32x4_t q[K][kW2Chunks<K>], hv[K][kW2Chunks<K>];
+    typename M::raw4 q[K][kW2Chunks<K>], hv[K][kW2Chunks<K>];
 #pragma unroll
     for (int u = 0; u < kW2Chunks<K>; ++u) {
       const int i = i0 + u * 256;
       const bool valid = i < a.hidden;
 #pragma unroll
       for (int s = 0; s < K; ++s) {
-        q[s][u] = valid ? M::stream4(row[s] + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
-        hv[s][u] = valid ? M::load4(hs + static_cast<int64_t>(s) * a.hidden + i) : f32x4_t{0.f, 0.f, 0.f, 0.f};
+        q[s][u] = valid ? M::stream_raw(row[s] + i) : M::zero_raw();
+        hv[s][u] = valid ? M::load_raw(hs + static_cast<int64_t>(s) * a.hidden + i) : M::zero_raw();
       }
     }
 #pragma unroll
     for (int u = 0; u < kW2Chunks<K>; ++u) {
       if (i0 + u * 256 >= a.hidden) break;
 #pragma unroll
-      for (int s = 0; s < K; ++s) acc[s] = dot4(q[s][u], hv[s][u], acc[s]);
+      for (int s = 0; s < K; ++s) acc[s] = dot4(M::widen(q[s][u]), M::widen(hv[s][u]), acc[s]);
     }
   }
 #pragma unroll
@@ -593,15 +572,13 @@ int32_t check_expert_args(const char* who, int32_t hidden, int32_t dim, const vo
 template <typename T, int NCH>
 void launch_w1(const MoeArgs& a, hipStream_t st) {
   const dim3 grid((a.hidden + 15) / 16, a.top_k);
-  if constexpr (sizeof(T) == 4) {
-    if (a.acc) {
-      if (a.ln_w) {
-        moe_w1_gelu_kernel<T, NCH, true, true><<<grid, 256, 0, st>>>(a);
-      } else {
-        moe_w1_gelu_kernel<T, NCH, false, true><<<grid, 256, 0, st>>>(a);
-      }
-      return;
+  if (a.acc) {
+    if (a.ln_w) {
+      moe_w1_gelu_kernel<T, NCH, true, true><<<grid, 256, 0, st>>>(a);
+    } else {
+      moe_w1_gelu_kernel<T, NCH, false, true><<<grid, 256, 0, st>>>(a);
     }
+    return;
   }
   if (a.ln_w) {
     moe_w1_gelu_kernel<T, NCH, true><<<grid, 256, 0, st>>>(a);
@@ -637,7 +614,7 @@ int32_t launch_experts_as(const MoeArgs& a, hipStream_t st) {
   return mie::check_launch("moe_w2_reduce_kernel");
 }
 
-// dtype was checked: float32 or bfloat16 (the accumulator form float32 only).
+// dtype was checked: float32 or bfloat16.
 int32_t launch_experts(const MoeArgs& a, int32_t dtype, hipStream_t st) {
   return dtype == MIE_DTYPE_F32 ? launch_experts_as<float>(a, st) : launch_experts_as<uint16_t>(a, st);
 }
@@ -689,7 +666,6 @@ int32_t moe_decode_block_acc_check(const void* x, const void* acc, const void* b
                                             top_k, dim, hidden, router_logits, expert_ids, route_weights,
                                             hidden_act, out, dtype);
   if (rc != MIE_OK) return rc;
-  if (dtype != MIE_DTYPE_F32) return mie::fail(MIE_ERR_UNSUPPORTED, "mie_moe_decode_block_acc: float32 only");
   if (!acc || !h_out || reinterpret_cast<uintptr_t>(acc) % 16 || !aligned16(h_out) || !aligned16(b_out))
     return mie::fail(MIE_ERR_INVALID, "mie_moe_decode_block_acc: acc and h_out (and b_out) must be non-NULL and "
                                       "16-byte aligned");
@@ -739,8 +715,8 @@ extern "C" int32_t mie_moe_decode_block_acc(const void* x, const void* acc, cons
                         route_weights);
   a.x = x;  // the W1 launch reads x and forms h_out
   a.acc = static_cast<const unsigned long long*>(acc);
-  a.b_out = static_cast<const float*>(b_out);
-  a.h_out = static_cast<float*>(h_out);
+  a.b_out = b_out;
+  a.h_out = h_out;
   a.acc_clear = static_cast<unsigned long long*>(const_cast<void*>(acc));
   a.ln_w = ln_weight;
   a.ln_b = ln_bias;

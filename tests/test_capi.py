@@ -160,7 +160,7 @@ def _valid_plan_args(**over):
 
 
 @pytest.mark.parametrize("change,code,message", [
-    (dict(dtype=1), 0, b""),                        # bf16: five launches (no fused attention + out_proj)
+    (dict(dtype=1), 0, b""),                        # bf16 passes every check
     (dict(hidden=130), 1, b"hidden=130"),           # an expert width only the MoE half sees
     (dict(dtype=3), 2, b""),                        # a dtype no launch is built for
     (dict(head_dim=48, heads=1, dim=48, sblk=16 * 48, shead=16 * 48), 2, b""),  # a head_dim the decode lacks
@@ -226,7 +226,7 @@ def test_block_plan_launch_count_follows_the_form():
 
 
 @pytest.mark.parametrize("change,code,message", [
-    (dict(dtype=1), 2, b"float32 only"),
+    (dict(dtype=3), 2, b"float32 or bfloat16 only"),
     (dict(head_dim=96), 2, b"head_dim 96"),
     (dict(max_ctx=1025 * 16), 2, b"contexts up to 1024 blocks"),
     (dict(acc=(1 << 20) + 4), 1, b"aligned"),

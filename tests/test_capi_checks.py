@@ -162,7 +162,7 @@ CASES = [
     ("mie_moe_decode", moe_args(experts=65), INVALID, b"experts=65"),
     ("mie_moe_decode_block", moe_block_args(ln_w=None), INVALID, b"needs a weight"),
     ("mie_moe_decode_block", moe_block_args(dtype=3), UNSUPPORTED, b"float32 or bfloat16 only"),
-    ("mie_moe_decode_block_acc", moe_block_acc_args(dtype=BF16), UNSUPPORTED, b"float32 only"),
+    ("mie_moe_decode_block_acc", moe_block_acc_args(dtype=3), UNSUPPORTED, b"float32 or bfloat16 only"),
     ("mie_moe_decode_block_acc", moe_block_acc_args(acc=None), INVALID, b"16-byte aligned"),
     ("mie_paged_decode", decode_args(head_dim=48, q_sh=48), UNSUPPORTED, b"not built"),
     ("mie_paged_decode", decode_args(partition=3), INVALID, b"partition_tokens 3"),

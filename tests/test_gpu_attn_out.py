@@ -37,7 +37,7 @@ def stream():
     return torch.cuda.current_stream().cuda_stream
 
 
-def attn_out(w, b, w_out, acc, ctx=None, ctx_dev=None, max_ctx=None):
+def attn_out(w, b, w_out, acc, ctx=None, ctx_dev=None, max_ctx=None, dtype=0):
     kp, vp = w.k_pool[w.layer], w.v_pool[w.layer]
     heads, bs, head_dim = kp.shape[1], kp.shape[2], kp.shape[3]
     table = w.block_tables[b]
@@ -46,7 +46,7 @@ def attn_out(w, b, w_out, acc, ctx=None, ctx_dev=None, max_ctx=None):
     rc = _native.lib().mie_attn_out_acc(
         w.q[b].data_ptr(), kp.data_ptr(), vp.data_ptr(), kp.stride(0), kp.stride(1), kp.shape[0],
         table.data_ptr(), table.numel(), None if ctx_dev is None else ctx_dev.data_ptr(), ctx, max_ctx,
-        heads, head_dim, bs, 1.0 / math.sqrt(head_dim), w_out.data_ptr(), acc.data_ptr(), 0, stream())
+        heads, head_dim, bs, 1.0 / math.sqrt(head_dim), w_out.data_ptr(), acc.data_ptr(), dtype, stream())
     _native.check(rc, "mie_attn_out_acc")
 
 
@@ -222,3 +222,79 @@ def test_moe_block_acc_writes_nan_when_the_flag_is_set():
     torch.cuda.synchronize()
     assert torch.isnan(h_out).all() and torch.isnan(out).all()
     assert not acc.any()
+
+
+@pytest.mark.parametrize("heads,head_dim,block_size,lens", [CASES[0], CASES[3], CASES[5]])
+def test_attn_out_bf16_matches_float64_on_rounded_head_outputs(heads, head_dim, block_size, lens):
+    """bfloat16 q, pools and W_out: each head's attention output is rounded
+    to bfloat16 before the projection (as the decode kernels store it), then
+    projected and summed in fixed point.  Against float64 attention on the
+    same bfloat16 values, rounded the same way: a float32 softmax can put a
+    head output on the other side of a bfloat16 rounding boundary, so at
+    least 98 % of rows meet the float32 bound and every row a bound one
+    bfloat16 ulp of the row's scale wider."""
+    print_case("attn_out bf16", heads, head_dim, block_size, lens)
+    w = make_workload(lens, num_heads=heads, head_dim=head_dim, block_size=block_size, dtype=torch.bfloat16,
+                      seed=heads + head_dim + block_size, heavy_fraction=0.02)
+    dim = heads * head_dim
+    g = torch.Generator(device="cuda").manual_seed(7)
+    w_out = (torch.randn(dim, dim, generator=g, device="cuda") / math.sqrt(dim)).to(torch.bfloat16)
+    w64 = ref.to_f64(w_out)
+    for b in range(len(lens)):
+        acc = torch.zeros(dim + 1, dtype=torch.int64, device="cuda")
+        attn_out(w, b, w_out, acc, dtype=1)
+        k, v = sequence_kv(w, b)
+        a = ref.attention_fp64(ref.to_f64(w.q[b]), ref.to_f64(k), ref.to_f64(v)).reshape(-1)
+        a = torch.from_numpy(a).to(torch.bfloat16).double().numpy()
+        want, scale = w64 @ a, np.abs(w64) @ np.abs(a)
+        got = acc[:dim].cpu().numpy().astype(np.float64) * FIX
+        assert int(acc[dim]) == 0
+        err = np.abs(got - want)
+        tight = err <= 2e-5 * scale + 1e-6
+        assert tight.mean() >= 0.98, f"only {tight.mean():.1%} of rows within the float32 bound"
+        assert (err <= (2e-5 + 2.0 ** -7) * scale + 1e-6).all(), f"max error {err.max():.3e}"
+        again = torch.zeros_like(acc)
+        attn_out(w, b, w_out, again, dtype=1)
+        assert torch.equal(acc, again), "the fixed-point sums differ between runs"
+
+
+def test_moe_block_acc_bf16_forms_the_rounded_residual():
+    """bfloat16: h_out = round(x + round(acc * 2^-32 + b_out)) - the
+    projection's output, then the residual, each rounded to bfloat16 as
+    mie_linear_residual stores them - bit for bit against torch's float32
+    arithmetic and rounding, then the MoE half exactly as mie_moe_decode_block
+    computes it on h_out."""
+    print_case("moe_decode_block_acc bf16")
+    lib = _native.lib()
+    dim, hidden, experts, top_k = 768, 2048, 8, 2
+    t = {k: v.to(torch.bfloat16) for k, v in moe_inputs(dim, hidden, experts, seed=11).items()}
+    acc = torch.zeros(dim + 1, dtype=torch.int64, device="cuda")
+    acc[:dim] = torch.round(t["o"].double() / FIX).long()
+    proj = (acc[:dim].float() * FIX + t["b_out"].float()).to(torch.bfloat16)
+    h_want = (t["x"].float() + proj.float()).to(torch.bfloat16)
+    h_out = torch.empty(dim, dtype=torch.bfloat16, device="cuda")
+    z = lambda *shape, dtype=torch.float32: torch.zeros(*shape, dtype=dtype, device="cuda")  # noqa: E731
+
+    def scratch():
+        return z(experts), z(top_k, dtype=torch.int32), z(top_k), z(top_k, hidden, dtype=torch.bfloat16), \
+            z(dim, dtype=torch.bfloat16)
+
+    logits, ids, weights, hid, out = scratch()
+    rc = lib.mie_moe_decode_block_acc(
+        t["x"].data_ptr(), acc.data_ptr(), t["b_out"].data_ptr(), h_out.data_ptr(), t["ln_w"].data_ptr(),
+        t["ln_b"].data_ptr(), 1e-5, t["router"].data_ptr(), t["w1"].data_ptr(), t["b1"].data_ptr(),
+        t["w2"].data_ptr(), t["b2"].data_ptr(), experts, top_k, dim, hidden, logits.data_ptr(), ids.data_ptr(),
+        weights.data_ptr(), hid.data_ptr(), out.data_ptr(), 1, stream())
+    _native.check(rc, "mie_moe_decode_block_acc")
+    torch.cuda.synchronize()
+    assert torch.equal(h_out, h_want)
+    assert not acc.any(), "the accumulator is not cleared"
+    logits2, ids2, weights2, hid2, out2 = scratch()
+    rc = lib.mie_moe_decode_block(
+        h_want.data_ptr(), t["ln_w"].data_ptr(), t["ln_b"].data_ptr(), 1e-5, t["router"].data_ptr(),
+        t["w1"].data_ptr(), t["b1"].data_ptr(), t["w2"].data_ptr(), t["b2"].data_ptr(), experts, top_k, dim, hidden,
+        logits2.data_ptr(), ids2.data_ptr(), weights2.data_ptr(), hid2.data_ptr(), out2.data_ptr(), 1, stream())
+    _native.check(rc, "mie_moe_decode_block")
+    assert torch.equal(ids, ids2) and torch.equal(weights, weights2) and torch.equal(hid, hid2)
+    assert torch.equal(out, out2)
+

@@ -139,7 +139,8 @@ def _bf16_model(seed, cfg):
 @pytest.mark.parametrize("seed", range(4))
 def test_bf16_model_decodes_through_the_fused_moe(seed):
     """A bfloat16 model on a paged-direct cache: the decode steps take the
-    fused MoE (no per-expert synchronisation), the greedy tokens equal the
+    fused MoE (no per-expert synchronisation) and the four-launch block, the
+    greedy tokens equal the
     PyTorch MoE's up to the first near-tie of its logits, and the whole step
     replayed from a HIP graph gives the eager tokens exactly."""
     cfg = dict(max_seq_length=96, vocab_size=512, num_layers=2, hidden_dim=128, num_heads=2, num_experts=8,
@@ -147,6 +148,7 @@ def test_bf16_model_decodes_through_the_fused_moe(seed):
     print_case("bf16 model", seed, cfg)
     model = _bf16_model(seed, cfg)
     assert all(block.moe.direct_configuration_supported(1) for block in model.MoEBlocks)
+    head_dim = cfg["hidden_dim"] // cfg["num_heads"]
     prompt = torch.randint(0, cfg["vocab_size"], (12,), generator=torch.Generator().manual_seed(seed)).cuda()
     alloc = model.new_block_allocator(num_blocks=8, block_size=16, attention_mode="direct")
 
@@ -183,6 +185,15 @@ def test_bf16_model_decodes_through_the_fused_moe(seed):
         lib.mie_blocks_decode = real
         model.set_moe_mode("auto")
     assert torch.equal(fused, eager_again) and torch.equal(graphed, fused)
+    # The bfloat16 block takes the four-launch form (attention fused with
+    # out_proj) at these contexts.
+    cache = alloc.new_cache()
+    with torch.no_grad():
+        model(prompt[None, :4], cache)
+        model(prompt[None, 4:5], cache)
+    plan = model.MoEBlocks[0]._one_token[2].plan
+    assert head_dim == 64 and lib.mie_block_plan_launches(plan, 40) == 4
+    cache.free()
     # Teacher-forced logits of the reference MoE's sequence decide where the
     # two may part: up to the first step whose top two logits lie within
     # 4 bf16 ulps of the larger, the tokens must agree.
