@@ -14,22 +14,33 @@
 float32 or bfloat16.
 """
 
+import threading
+
 import torch
 
 from moe_engine import _native
 
-# The logits of the last lm_head(keep_pick=True) call, with the picks its
-# workgroups left: (logits, their version counter then, picks).  Holding the
+# Per host thread: the logits of its last lm_head(keep_pick=True) call, with
+# the picks its workgroups left - last_pick = (logits, their version counter
+# then, picks) - and the picks' workspaces by (device, vocab).  Holding the
 # logits keeps their memory from being reused, so a tensor at their address
 # is one of their views, and views share the version counter, which counts
-# every in-place write.
-_last_pick = None
-_pick_workspaces = {}  # (device, vocab) -> the picks' workspace
+# every in-place write.  Threads keep their own workspaces, so one thread's
+# head never overwrites picks another thread is about to merge.
+_pick_state = threading.local()
+
+
+def _state():
+    st = _pick_state
+    if not hasattr(st, "workspaces"):
+        st.last_pick = None
+        st.workspaces = {}
+    return st
 
 
 def _kept_picks(x):
     """The workspace of picks that describe x, or None."""
-    rec = _last_pick
+    rec = _state().last_pick
     if rec is None or x.is_inference():
         return None
     logits, version, workspace = rec
@@ -92,7 +103,7 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     in a workspace of this module's, and argmax(out) merges them while out is
     unmodified and no later keep_pick call replaced them.
     Returns out."""
-    global _last_pick
+    st = _state()
     weight, bias = linear.weight, linear.bias
     if weight.dim() != 2 or not weight.is_contiguous():
         raise ValueError("weight must be a contiguous [vocab, dim] matrix")
@@ -121,14 +132,14 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
     keep_pick = keep_pick and token_out is None and not out.is_inference()
     if keep_pick:
         key = (device, vocab)
-        workspace = _pick_workspaces.get(key)
+        workspace = st.workspaces.get(key)
         if workspace is None:
-            workspace = _pick_workspaces[key] = torch.empty(head_workspace_bytes(vocab), dtype=torch.uint8,
-                                                            device=device)
+            workspace = st.workspaces[key] = torch.empty(head_workspace_bytes(vocab), dtype=torch.uint8,
+                                                         device=device)
         ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel()
-        _last_pick = None  # the picks are overwritten from here on
-    elif _last_pick is not None and out.data_ptr() == _last_pick[0].data_ptr():
-        _last_pick = None  # the kernel rewrites the recorded logits without counting a version
+        st.last_pick = None  # the picks are overwritten from here on
+    elif st.last_pick is not None and out.data_ptr() == st.last_pick[0].data_ptr():
+        st.last_pick = None  # the kernel rewrites the recorded logits without counting a version
     if not keep_pick and token_out is not None:
         if token_out.dtype != torch.int64 or token_out.numel() != 1 or token_out.device != device:
             raise ValueError("token_out must be one int64 value on the weight's device")
@@ -154,7 +165,7 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
         "mie_lm_head",
     )
     if keep_pick:
-        _last_pick = (out, out._version, workspace)
+        st.last_pick = (out, out._version, workspace)
     return out
 
 

@@ -179,6 +179,22 @@ def test_argmax_of_fresh_head_logits_merges_the_kept_picks(monkeypatch):
     projection.lm_head(x, ln, linear, out=kept)
     assert int(projection.argmax(kept)) == pick(kept) and counted.calls["mie_argmax"] == 3
 
+    # Each host thread keeps its own picks: another thread's head (same device
+    # and vocabulary) neither replaces nor overwrites this thread's.
+    import threading
+
+    mine = projection.lm_head(x, ln, linear, keep_pick=True)
+    theirs = {}
+    worker = threading.Thread(target=lambda: theirs.update(
+        logits=projection.lm_head(x2, None, tied, keep_pick=True)))
+    worker.start()
+    worker.join()
+    torch.cuda.synchronize()
+    merges = counted.calls["mie_argmax_pairs"]
+    assert int(projection.argmax(mine)) == pick(mine)
+    assert counted.calls["mie_argmax_pairs"] == merges + 1 and counted.calls["mie_argmax"] == 3
+    assert not projection.can_argmax(theirs["logits"].bfloat16())  # not this thread's logits, not float32
+
 
 def test_lm_head_advances_counters_after_the_pick():
     x, ln, linear = make_head(700, 64, torch.float32, True, True, seed=2)
