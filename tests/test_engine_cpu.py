@@ -488,3 +488,55 @@ def test_bfloat16_layers_keep_float32_routing_workspaces():
         layer.router.weight.bfloat16(), s["w1"].bfloat16(), s["b1"].bfloat16(), s["w2"].bfloat16(),
         s["b2"].bfloat16(), layer._router_logits.bfloat16(), layer._expert_ids, layer._route_weights,
         layer._expert_hidden.bfloat16(), layer._direct_out.bfloat16())
+
+
+def _bf16_moe_path(layer, x, keep_gelu_float=False, reverse_sums=False):
+    """The reference's bfloat16 MoE (model.py:443-461) written out with its
+    rounding points: each Linear's float32 sum plus bias rounded once, GELU
+    rounded, the route weight and the weighted product rounded, index_add_
+    rounding each partial sum.  keep_gelu_float drops one rounding point;
+    reverse_sums keeps them all and reverses the dot products' order."""
+    import torch.nn.functional as F
+
+    flat = x.reshape(-1, layer.dim)
+    logits = F.linear(flat.float(), layer.router.weight.float())
+    top_logits, top_ids = torch.topk(logits, layer.top_k)
+    weights = F.softmax(top_logits, dim=-1)
+    out = torch.zeros_like(flat)
+
+    def linear(v, w, b):
+        if reverse_sums:
+            v, w = v.flip(-1), w.flip(-1)
+        return (v.float() @ w.float().t() + b.float()).to(torch.bfloat16)
+
+    for e, expert in enumerate(layer.experts):
+        tok, slot = torch.where(top_ids == e)
+        if tok.numel() == 0:
+            continue
+        first, second = expert.net[0], expert.net[2]
+        h = F.gelu(linear(flat[tok], first.weight, first.bias).float())
+        h = h if keep_gelu_float else h.to(torch.bfloat16)
+        y = linear(h, second.weight, second.bias)
+        out.index_add_(0, tok, weights[tok, slot].unsqueeze(-1).to(torch.bfloat16) * y)
+    return out
+
+
+def test_bf16_moe_identity_bar_separates_reordering_from_a_dropped_rounding():
+    """The GPU bfloat16 MoE tests require at least 90 % of the outputs to be
+    bit-identical to the PyTorch path's.  This pins what that bar can tell
+    apart, on the CPU: summing the dot products in another order (what the
+    fused kernels legitimately do) leaves nearly every output identical,
+    while dropping one rounding point (GELU's) leaves well under 90 %."""
+    torch.manual_seed(50)
+    for dim, hidden, experts, top_k in ((256, 200, 17, 4), (128, 512, 8, 2)):
+        layer = MoEFeedForward(dim, hidden, experts, top_k).to(torch.bfloat16).eval()
+        x = torch.randn(16, 1, dim).to(torch.bfloat16)
+        with torch.no_grad():
+            base = _bf16_moe_path(layer, x)
+            reference = layer._forward_reference(x).reshape(base.shape)
+            reordered = _bf16_moe_path(layer, x, reverse_sums=True)
+            dropped = _bf16_moe_path(layer, x, keep_gelu_float=True)
+        same = lambda a, b: (a.float() == b.float()).float().mean().item()  # noqa: E731
+        assert same(base, reference) >= 0.97  # the restatement has the reference path's rounding points
+        assert same(base, reordered) >= 0.97
+        assert same(base, dropped) < 0.75

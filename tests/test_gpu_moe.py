@@ -13,6 +13,8 @@ the reference engine runs through tests/test_gpu_golden.py, where 'auto'
 selects these kernels for decode steps.
 """
 
+import os
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -58,7 +60,7 @@ def test_fused_decode_matches_pytorch_path(dim, hidden, experts, top_k):
         assert_output_close(got, want)
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("MIE_MOE_RANDOM_CASES", "16"))))
 def test_random_fused_decode_and_block_match_pytorch_path(seed):
     """Drawn widths (multiples of 4 up to 2048), hidden sizes, expert counts
     (up to 64) and top-k (up to 8): the fused decode and the block form

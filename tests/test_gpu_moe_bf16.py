@@ -7,15 +7,20 @@ weight cast to bfloat16, the weighted product and each index_add_ partial
 sum.  The fused kernels round at the same points and sum in float32, so the
 two paths differ only where a different float32 summation order inside a dot
 product moves a value across a bfloat16 rounding boundary - about 2e-6 / 2^-7
-per value.  Required here: at least 98 % of the outputs bit-identical to the
-PyTorch path's and every output within 2^-6 of the output scale (a missing or
-extra rounding would leave a large share of outputs off by an ulp); expert
+per value; over a layer's several roundings, up to a few percent of the
+outputs (2.2 % for a 2048-wide top-4 layer).  Required here: at least 90 %
+of the outputs bit-identical to the PyTorch path's and every output within
+2^-6 of the output scale.  A dropped rounding point leaves only 58-60 % of
+the outputs identical, while reordering the sums leaves 99.9 %
+(tests/test_engine_cpu.py, test_bf16_moe_identity_bar_separates_reordering_from_a_dropped_rounding);
+expert
 ids equal to torch.topk over the float32 logits, route weights within 2e-6.
 End to end, a bfloat16 model decodes through the fused MoE (eagerly and from
 a HIP graph) with the same greedy tokens as through the PyTorch MoE, up to
 the first near-tie.
 """
 
+import os
 import random
 
 import pytest
@@ -41,7 +46,7 @@ def assert_bf16_close(got, want, what):
     same = (g == w).float().mean().item()
     scale = max(w.abs().max().item(), 2.0**-4)
     err = (g - w).abs().max().item()
-    assert same >= 0.98, f"{what}: only {same:.1%} of the outputs are bit-identical"
+    assert same >= 0.90, f"{what}: only {same:.1%} of the outputs are bit-identical"
     assert err <= 2.0**-6 * scale, f"{what}: max error {err:.3e} at output scale {scale:.3e}"
 
 
@@ -70,7 +75,7 @@ def test_fused_bf16_decode_matches_pytorch_path(dim, hidden, experts, top_k):
     assert_bf16_close(torch.cat(got), torch.cat(want), f"moe {dim}x{hidden} E{experts} k{top_k}")
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(int(os.environ.get("MIE_MOE_RANDOM_CASES", "12"))))
 def test_random_bf16_decode_and_block_match_pytorch_path(seed):
     """Drawn widths, hidden sizes, expert counts and top-k: the fused decode
     and the block form x + MoE(LayerNorm(x)) against the module's PyTorch
