@@ -20,8 +20,9 @@ stream: one event pair around the timed loop of back-to-back fused launches
 (region / steps), or events around every attention call with `--unfused`.
 `cpu_baseline` times the oracle's gather + scaled_dot_product_attention path
 (the reference's CPU path) on a bounded sample of the same workload.
-`secondary` carries the per-token end-to-end decode latency (config 1) and the
-single-layer, append/gather and long-context figures (configs 2, 3, 5).
+`secondary` carries the per-token end-to-end decode latency (config 1, and
+its shape in bfloat16) and the single-layer, append/gather and long-context
+figures (configs 2, 3, 5).
 """
 
 import argparse
@@ -38,8 +39,8 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
-                   "fused_moe_decode", "config1_e2e_decode", "read_ceilings", "grid_sync", "l2_reuse",
-                   "decode_timeline", "atomic_sum")
+                   "fused_moe_decode", "config1_e2e_decode", "config1_bf16_decode", "read_ceilings", "grid_sync",
+                   "l2_reuse", "decode_timeline", "atomic_sum")
 PROBES = ROOT / "moe-inference-engine_amd" / "moe_engine" / "libmie_probes.so"
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
@@ -838,6 +839,28 @@ def secondary_e2e(torch, rounds=5, new_tokens=64, cpu_rounds=2):
     return report
 
 
+def secondary_e2e_bf16(torch, rounds=3, new_tokens=32):
+    """Config 1's model in bfloat16 (not a BASELINE config): per-token greedy
+    decode of paged-direct, eagerly and replayed from a graph, interleaved
+    rounds as in config1_e2e_decode, and the same cache system with the
+    PyTorch MoE (moe_ab_compare), which the reference's bfloat16 models take
+    because its fused MoE is float32 only."""
+    from moe_engine import harness
+
+    model = harness.make_model(harness.CONFIG1, seed=0, device="cuda", dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(0)
+    prompt = torch.randint(0, harness.CONFIG1["vocab_size"], (32,), generator=gen).cuda()
+    rep = harness.ab_compare(model, prompt, ("paged-direct", harness.GRAPH_SYSTEM), rounds=rounds,
+                             new_tokens=new_tokens)
+    ab = harness.moe_ab_compare(model, prompt, rounds=2, new_tokens=8, system="paged-direct")
+    return {
+        "decode_median_ms": {s: v["decode_median_ms"] for s, v in rep["summary"].items()},
+        "pytorch_moe_decode_median_ms": ab["summary"]["reference"]["decode_median_ms"],
+        "tokens_identical": rep["tokens_identical"] and ab["tokens_identical"],
+        "note": "config 1's shape in bfloat16, random init seed 0; the reference's fused MoE is float32 only",
+    }
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -882,6 +905,7 @@ def main():
             ("config5_long_context", secondary_config5),
             ("fused_moe_decode", secondary_moe),
             ("config1_e2e_decode", secondary_e2e),
+            ("config1_bf16_decode", secondary_e2e_bf16),
             ("read_ceilings", secondary_read_ceilings),
             ("grid_sync", secondary_grid_sync),
             ("l2_reuse", secondary_l2_reuse),
