@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   const int g = lane / LPT;          // row within a wave load
   const int c4 = (lane % LPT) * 4;   // this lane's 4 columns of a row
 
-  // Round 1, all independent: this workgroup's W_out rows, q, the block
+  // First memory round, all loads independent: this workgroup's W_out rows, q, the block
   // table up to the host's bound (nblk_max entries, at most 1024 = 4 per
   // thread), and the live length.
   typename M::raw4 wv[kRowSteps];
@@ -167,7 +167,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   // A context block outside the pool (never read) makes the head's attention NaN.
   const bool any_bad = __syncthreads_or(bad) != 0;
 
-  // Round 2..: this wave's tokens t = (step * 4 + wave) * TPL + g, kBatch wave
+  // Later memory rounds: this wave's tokens t = (step * 4 + wave) * TPL + g, kBatch wave
   // loads of K and V per round; online softmax per TPL-row group.
   const T* kh = static_cast<const T*>(a.k) + static_cast<int64_t>(h) * a.shead + c4;
   const T* vh = static_cast<const T*>(a.v) + static_cast<int64_t>(h) * a.shead + c4;
