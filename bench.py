@@ -39,9 +39,7 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
 SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
-                   "fused_moe_decode", "config1_e2e_decode", "config1_bf16_decode", "read_ceilings", "grid_sync",
-                   "l2_reuse", "decode_timeline", "atomic_sum")
-PROBES = ROOT / "moe-inference-engine_amd" / "moe_engine" / "libmie_probes.so"
+                   "fused_moe_decode", "config1_e2e_decode", "config1_bf16_decode")
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
 
@@ -446,299 +444,23 @@ def secondary_config5(torch):
     return res
 
 
-def probes_lib():
-    """libmie_probes.so (csrc/probes): measurement kernels only."""
-    import ctypes
-
-    lib = ctypes.CDLL(str(PROBES))
-    c = ctypes
-    lib.mie_probe_read_chunks.argtypes = [c.c_int32, c.c_int32, c.c_void_p, c.c_int64, c.c_void_p, c.c_int32,
-                                          c.c_int32, c.c_void_p, c.c_void_p]
-    lib.mie_probe_read_chunks.restype = c.c_int32
-    lib.mie_probe_noop.argtypes = [c.c_int32, c.c_void_p]
-    lib.mie_probe_noop.restype = c.c_int32
-    lib.mie_probe_grid_barrier.argtypes = [c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_void_p, c.c_void_p,
-                                           c.c_void_p, c.c_void_p, c.c_int64, c.c_void_p]
-    lib.mie_probe_grid_barrier.restype = c.c_int32
-    lib.mie_probe_read_regions.argtypes = [c.c_void_p, c.c_int64, c.c_int32, c.c_int32, c.c_int32, c.c_void_p,
-                                           c.c_void_p]
-    lib.mie_probe_read_regions.restype = c.c_int32
-    lib.mie_probe_atomic_sum.argtypes = [c.c_int32, c.c_int32, c.c_int32, c.c_int32, c.c_void_p, c.c_void_p]
-    lib.mie_probe_atomic_sum.restype = c.c_int32
-    return lib
-
-
-def secondary_decode_timeline(torch, launches=3):
-    """Where config 4's decode time goes: the fused step launched from the
-    probe library's copy of the decode kernels, built with per-workgroup
-    timestamps (MIE_DECODE_TIMELINE: start and end on the 100 MHz real-time
-    clock, XCD and hardware id per workgroup).  Per launch: the kernel span,
-    how many workgroups each CU ran and when each CU finished, and each
-    workgroup's read rate (its sequence's K and V bytes for one head over
-    its duration); and, over the workgroups of sequences longer than 4096
-    tokens, when each of the 16 waves finished its slice as a fraction of its
-    workgroup's duration (mean per wave index, and the median spread between
-    the first and the last wave)."""
-    import ctypes
-
-    from moe_engine import _native, workloads
-
-    probe = ctypes.CDLL(str(PROBES))
-    fn = probe.mie_paged_decode_append
-    fn.restype, fn.argtypes = _native._SIGNATURES["mie_paged_decode_append"]
-    probe.mie_probe_decode_timeline.argtypes = [ctypes.c_void_p]
-    probe.mie_probe_decode_timeline.restype = ctypes.c_int32
-
-    class ProbeDecode:  # the probe's decode, every other entry point the product's
-        def __init__(self, product):
-            self._product = product
-            self.mie_paged_decode_append = fn
-
-        def __getattr__(self, name):
-            return getattr(self._product, name)
-
-    step = workloads.config4_step()
-    w = step.w
-    heads, head_dim = w.k_pool.shape[2], w.k_pool.shape[4]
-    n_wg = heads * len(w.lens)
-    words = 20  # the probe build's record: 4 words, then 16 wave end times
-    buf = torch.zeros(n_wg * words, dtype=torch.int64, device="cuda")
-    product = _native._LIB
-    _native._LIB = ProbeDecode(product)
-    try:
-        for _ in range(3):
-            step.fused()
-        if probe.mie_probe_decode_timeline(buf.data_ptr()):
-            raise RuntimeError("mie_probe_decode_timeline failed")
-        runs = []
-        for _ in range(launches):
-            buf.zero_()
-            torch.cuda.synchronize()
-            step.fused()
-            torch.cuda.synchronize()
-            runs.append(buf.view(n_wg, words).cpu().numpy().astype("uint64"))
-        probe.mie_probe_decode_timeline(None)
-    finally:
-        _native._LIB = product
-    import numpy as np
-
-    res = []
-    for rec in runs:
-        t0, t1 = rec[:, 0].astype(np.int64), rec[:, 1].astype(np.int64)
-        base = t0.min()
-        xcd = (rec[:, 2] >> np.uint64(32)) & np.uint64(0xF)
-        hw = rec[:, 2] & np.uint64(0xFFFFFFFF)
-        cu = xcd * np.uint64(1 << 16) + ((hw >> np.uint64(8)) & np.uint64(0xFF))  # XCD, then SE/SH/CU bits
-        ctx = (rec[:, 3] & np.uint64(0xFFFFFFFF)).astype(np.int64)
-        dur_us = (t1 - t0) / 100.0
-        kv_bytes = ctx * head_dim * 2 * 2  # K and V rows of one head, bf16
-        wave_rel = (rec[:, 4:].astype(np.int64) - t0[:, None]) / np.maximum(t1 - t0, 1)[:, None]
-        long_seq = ctx > 4096
-        rate = kv_bytes / np.maximum(dur_us, 1e-3) / 1e3  # GB/s
-        ends = {}
-        counts = {}
-        for c, e in zip(cu.tolist(), ((t1 - base) / 100.0).tolist()):
-            ends[c] = max(ends.get(c, 0.0), e)
-            counts[c] = counts.get(c, 0) + 1
-        cu_end = np.array(sorted(ends.values()))
-        res.append({
-            "span_us": round(float((t1.max() - base) / 100.0), 2),
-            "workgroups": int(n_wg),
-            "cus_used": len(ends),
-            "xcds_used": int(len(set(xcd.tolist()))),
-            "workgroups_per_cu": {str(k): v for k, v in sorted(
-                {n: list(counts.values()).count(n) for n in set(counts.values())}.items())},
-            "cu_finish_us_min_median_max": [round(float(cu_end[0]), 2), round(float(np.median(cu_end)), 2),
-                                            round(float(cu_end[-1]), 2)],
-            "workgroup_gbs_p10_median_p90": [round(float(np.percentile(rate, q)), 1) for q in (10, 50, 90)],
-            "sum_over_cus_of_median_rate_tbs": round(float(np.median(rate)) * len(ends) / 1e3, 2),
-            "wave_end_fraction_by_wave": [round(float(v), 3) for v in wave_rel[long_seq].mean(0)],
-            "wave_end_spread_median": round(float(np.median(wave_rel[long_seq].max(1) - wave_rel[long_seq].min(1))), 3),
-        })
-    return {"launches": res, "note": "config 4 fused step (workgroup form), probe build of the decode kernels"}
-
-
-def secondary_l2_reuse(torch, reps=5):
-    """Whether one launch finds what the previous launch read in L2: 256
-    workgroups each read 48 KiB (12 MiB, 1.5 MiB per XCD) after a 1 GiB read
-    has flushed the caches, then again.  Workgroup w reads region (w + shift)
-    mod 256; read first with shift 8 (the same XCD, another workgroup), 1 (a
-    neighbouring XCD) or not at all, the second read (shift 0) then hits the
-    XCD's L2, the last-level cache only, or HBM.  Best of `reps`, microseconds
-    per launch from events around it (launch overhead included)."""
-    lib = probes_lib()
-    stream = torch.cuda.current_stream().cuda_stream
-    groups, per = 256, 48 * 1024
-    buf = torch.zeros(groups * per, dtype=torch.uint8, device="cuda")
-    flush = torch.zeros(1 << 30, dtype=torch.uint8, device="cuda")
-    out = torch.empty(max(groups, (1 << 30) // per) * 256, dtype=torch.int32, device="cuda")
-
-    def read(t, shift, n=groups):
-        if lib.mie_probe_read_regions(t.data_ptr(), t.numel(), n, per, shift, out.data_ptr(), stream):
-            raise RuntimeError("mie_probe_read_regions failed")
-
-    res = {}
-    for name, shift in (("hbm", None), ("other_xcd_l2_last_level_cache", 1), ("same_xcd_l2", 8)):
-        best = None
-        for _ in range(reps):
-            read(flush, 0, (1 << 30) // per)
-            if shift is not None:
-                read(buf, shift)
-            torch.cuda.synchronize()
-            start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            start.record()
-            read(buf, 0)
-            stop.record()
-            torch.cuda.synchronize()
-            us = start.elapsed_time(stop) * 1e3
-            best = us if best is None else min(best, us)
-        res[f"{name}_us"] = round(best, 2)
-    del buf, flush
-    return res
-
-
-def secondary_grid_sync(torch, iters=2000):
-    """What a grid-wide wait inside one launch costs, against a kernel
-    boundary in a graph (launch_floor): a cooperative launch of 256 or 512
-    workgroups meeting at a device counter `iters` times, in three memory
-    disciplines (csrc/probes/grid_sync.hip): device-scope relaxed data
-    (mode 1: no L2 writeback), one agent release/acquire per workgroup
-    (mode 2), both (mode 3: the release has no dirty L2 lines to write
-    back), and __threadfence in every thread (mode 0).  Best of five
-    launches, microseconds per barrier, with the count of stale reads seen
-    by the checks."""
-    lib = probes_lib()
-    stream = torch.cuda.current_stream().cuda_stream
-    res = {}
-    for groups in (256, 512):
-        counter = torch.zeros(1, dtype=torch.int32, device="cuda")
-        flags = torch.zeros(2, dtype=torch.int32, device="cuda")
-        vec = torch.zeros(2 * groups * 256, dtype=torch.float32, device="cuda")
-        for mode, name in ((1, "device_scope_data"), (2, "release_acquire_per_group"),
-                           (3, "device_scope_data_release_acquire"), (0, "threadfence_all")):
-            best, bad = None, 0
-            for _ in range(5):
-                counter.zero_()
-                flags.zero_()
-                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                start.record()
-                rc = lib.mie_probe_grid_barrier(mode, groups, iters, 256, counter.data_ptr(), vec.data_ptr(),
-                                                flags[0:1].data_ptr(), flags[1:2].data_ptr(), 1 << 20, stream)
-                stop.record()
-                torch.cuda.synchronize()
-                if rc:
-                    raise RuntimeError(f"mie_probe_grid_barrier returned {rc}")
-                err, wrong = flags.tolist()
-                if err:
-                    raise RuntimeError("a grid barrier wait hit its spin limit")
-                bad += wrong
-                us = start.elapsed_time(stop) * 1e3 / iters
-                best = us if best is None else min(best, us)
-            res[f"g{groups}_{name}"] = {"us_per_barrier": round(best, 3), "stale_reads": bad}
-    return res
-
-
-def secondary_atomic_sum(torch, outputs=768):
-    """What summing every workgroup's partial vector (768 values, config 1's
-    width) across workgroups costs with device-scope atomics
-    (csrc/probes/atomic_sum.hip): 128-512 workgroups adding into 1-16 copies
-    of the vector (workgroup g into copy g % copies) as exact int64
-    fixed-point or float32 sums, against plain stores of the partials.
-    Device time per launch (best of five runs of 300 back-to-back launches),
-    each sum checked against the exact total."""
-    import numpy as np
-
-    lib = probes_lib()
-    stream = torch.cuda.current_stream().cuda_stream
-
-    def expected(groups):
-        g = np.arange(groups)[:, None]
-        i = np.arange(outputs)[None, :]
-        return (((((g * 131 + i * 7) & 255) - 128) / 256.0) * 2.0 ** 32).astype(np.int64).sum(0)
-
-    res = {}
-    for groups in (128, 256, 512):
-        for mode, name, copies_list in ((3, "stores", (1,)), (0, "int64", (1, 2, 4, 8, 16)), (2, "f32", (1, 4))):
-            for copies in copies_list:
-                rows = groups if mode == 3 else copies
-                acc = torch.zeros(rows * outputs, dtype=torch.float32 if mode == 2 else torch.int64, device="cuda")
-
-                def call(mode=mode, groups=groups, copies=copies, acc=acc):
-                    if lib.mie_probe_atomic_sum(mode, groups, outputs, copies, acc.data_ptr(), stream):
-                        raise RuntimeError("mie_probe_atomic_sum failed")
-
-                call()
-                torch.cuda.synchronize()
-                host = acc.view(rows, outputs).cpu()
-                if mode == 2:  # multiples of 2^-8 summed exactly in float32
-                    exact = np.array_equal(host.double().numpy().sum(0) * 2.0 ** 32, expected(groups))
-                else:
-                    exact = np.array_equal(host.numpy().sum(0), expected(groups))
-                best = None
-                for _ in range(5):
-                    us = timed_us(torch, call, iters=300, warmup=20)
-                    best = us if best is None else min(best, us)
-                key = f"g{groups}_{name}" + ("" if mode == 3 else f"_copies{copies}")
-                res[key] = {"us": round(best, 3), "exact": bool(exact)}
-    return res
-
-
 def secondary_launch_floor(torch):
     """The floor a launch-bound call cannot go under on this box: device time
     per call of 64 calls replayed from one HIP graph, each call one or two
     launches of an empty kernel (256 workgroups) - the same way the config 2,
     3 and 5 figures are timed."""
-    lib = probes_lib()
+    from moe_engine import _native
+
+    lib = _native.lib()
 
     def noop():
-        if lib.mie_probe_noop(256, torch.cuda.current_stream().cuda_stream):
-            raise RuntimeError("mie_probe_noop failed")
+        if lib.mie_empty_launch(256, torch.cuda.current_stream().cuda_stream):
+            raise RuntimeError("mie_empty_launch failed")
 
     one = graph_replay_us(torch, [noop] * 64)
     two = graph_replay_us(torch, [lambda: (noop(), noop())] * 64)
     return {"one_launch_us": round(one, 3), "two_launch_us": round(two, 3),
             "note": "empty kernel, 256 workgroups x 256 threads; 64 calls per graph, device time per call"}
-
-
-def secondary_read_ceilings(torch):
-    """Read ceilings of the decode's access pattern: 768 MiB per call (about
-    config 4's 785 MB) in 2 KiB chunks - one bf16 (block, head) tile - at
-    random chunk ids of a 4 GiB buffer, in runs of 12 consecutive chunks at
-    random places (a block's 12 heads, 24 KiB: the read unit of a workgroup
-    that took all heads of a sequence) and in order, read into registers with
-    non-temporal loads (the decode kernels' way) or staged through LDS with
-    global_load_lds, with 1-8 chunks in flight per wave (csrc/probes)."""
-    lib = probes_lib()
-    chunks = (4 << 30) // 2048
-    n = (768 << 20) // 2048
-    buf = torch.empty(chunks * 2048, dtype=torch.uint8, device="cuda")
-    gen = torch.Generator().manual_seed(0)
-    random_ids = torch.randperm(chunks, generator=gen)[:n].to(torch.int32).cuda()
-    run = 12
-    starts = torch.randperm(chunks // run, generator=gen)[: n // run].to(torch.int64) * run
-    orders = {"random": random_ids,
-              "runs_of_12": (starts[:, None] + torch.arange(run)).reshape(-1).to(torch.int32).cuda(),
-              "in_order": torch.arange(n, dtype=torch.int32, device="cuda")}
-    groups = 2048
-    out = torch.empty(groups * 256, dtype=torch.int32, device="cuda")
-    res = {}
-    for order, ids in orders.items():
-        for kind, name, depths in ((0, "registers", (1, 2, 4, 8)), (1, "global_load_lds", (1, 2, 4))):
-            for depth in depths:
-                def call(kind=kind, depth=depth, ids=ids):
-                    rc = lib.mie_probe_read_chunks(kind, depth, buf.data_ptr(), chunks, ids.data_ptr(), n, groups,
-                                                   out.data_ptr(), torch.cuda.current_stream().cuda_stream)
-                    if rc:
-                        raise RuntimeError(f"mie_probe_read_chunks returned {rc}")
-
-                us = timed_us(torch, call, iters=20, warmup=3)
-                res[f"{order}_{name}_depth{depth}"] = {"us": round(us, 1), "gbs": round(n * 2048 / us / 1e3, 1)}
-    for order in orders:
-        for name in ("registers", "global_load_lds"):
-            res[f"best_{order}_{name}_gbs"] = max(v["gbs"] for k, v in res.items()
-                                                   if isinstance(v, dict) and k.startswith(f"{order}_{name}_"))
-    del buf
-    return res
 
 
 def add_floor_fractions(secondary):
@@ -906,11 +628,6 @@ def main():
             ("fused_moe_decode", secondary_moe),
             ("config1_e2e_decode", secondary_e2e),
             ("config1_bf16_decode", secondary_e2e_bf16),
-            ("read_ceilings", secondary_read_ceilings),
-            ("grid_sync", secondary_grid_sync),
-            ("l2_reuse", secondary_l2_reuse),
-            ("decode_timeline", secondary_decode_timeline),
-            ("atomic_sum", secondary_atomic_sum),
         ):
             if name not in chosen:
                 continue

@@ -10,13 +10,13 @@
  *   mie_paged_decode  <- paged_attention.decode src/moe_engine/paged_attention.py:113-154
  *                        and _paged_decode_kernel src/moe_engine/paged_attention.py:46-110
  *   mie_paged_decode_append <- cache.write then paged_attention.decode for a
- *                        decode token (model.py:247 then :263), in one launch
+ *                        decode token (model.py:247 then :260), in one launch
  *   mie_qkv_append    <- CachedAttention.forward's QKV projection and
  *                        cache.write for one decode token  src/moe_engine/model.py:228-247
- *   mie_linear_residual <- out_proj + the block's residual add  src/moe_engine/model.py:268, :447
+ *   mie_linear_residual <- out_proj + the block's residual add  src/moe_engine/model.py:269, :495
  *   mie_moe_route     <- fused_moe.route         src/moe_engine/fused_moe.py:274-309
  *   mie_moe_decode    <- fused_moe.decode        src/moe_engine/fused_moe.py:312-380
- *   mie_moe_decode_block <- the block's x + moe(moe_norm(x)) for one token  src/moe_engine/model.py:446-449
+ *   mie_moe_decode_block <- the block's x + moe(moe_norm(x)) for one token  src/moe_engine/model.py:496-497
  *   mie_argmax        <- Model.generate's greedy torch.argmax   src/moe_engine/model.py:603
  *   mie_lm_head       <- final_norm + output_projection (model.py:564-565) and,
  *                        optionally, the greedy argmax (:603) for one token
@@ -24,12 +24,12 @@
  *                        logits mie_lm_head just wrote, from its per-workgroup picks
  *   mie_embed         <- token_embedding(ids) + positional_embedding(pos)  src/moe_engine/model.py:558
  *   mie_attn_out_acc  <- paged_attention.decode then out_proj for one decode
- *                        token (model.py:263 then :268), per head, summed into
+ *                        token (model.py:260 then :269), per head, summed into
  *                        a fixed-point accumulator row: one launch
- *   mie_moe_decode_block_acc <- the block's x + out_proj(a) (model.py:447) and
- *                        x + moe(moe_norm(x)) (:448-449) after mie_attn_out_acc
+ *   mie_moe_decode_block_acc <- the block's x + out_proj(a) (model.py:495) and
+ *                        x + moe(moe_norm(x)) (:496-497) after mie_attn_out_acc
  *   mie_block_plan_init, mie_block_decode <- one TransformerMoEBlock.forward for one
- *                        decode token (model.py:446-449 with :226-269): four or
+ *                        decode token (model.py:494-498 with :226-269): four or
  *                        five launches above from a stored plan, one call per token
  *   mie_block_plan_set_embedding, mie_block_decode_embed <- the embedding (model.py:558)
  *                        and the first block, the embedding inside the QKV launch
@@ -88,10 +88,17 @@ enum mie_status {
 
 /* Library ABI version (MIE_ABI_VERSION below). */
 int32_t mie_abi_version(void);
-#define MIE_ABI_VERSION 15
+#define MIE_ABI_VERSION 16
 
 /* Message for the last non-zero status returned on this thread ("" if none). */
 const char* mie_last_error(void);
+
+/*
+ * Measurement only, no counterpart in the reference: launches `workgroups`
+ * (1 .. 2^20) workgroups of 256 threads of an empty kernel on `stream`, so a
+ * caller can time the launch floor that a latency-bound call cannot go under.
+ */
+int32_t mie_empty_launch(int32_t workgroups, void* stream);
 
 /*
  * KV append: scatter new K/V rows into the pool through block tables.
@@ -178,7 +185,7 @@ int32_t mie_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                          int32_t dtype, void* stream);
 
 /*
- * A decode step's append and attention together (model.py:247 then :263 for
+ * A decode step's append and attention together (model.py:247 then :260 for
  * B sequences): each sequence's new token is its LAST context token, so
  * k_new[b] / v_new[b] ([B, H, D] rows, element strides new_stride_b /
  * new_stride_h, inner axis contiguous, `dtype`) are stored at position
@@ -255,7 +262,7 @@ int32_t mie_qkv_append_supported(int32_t dim, int32_t dtype);
 
 /*
  * One-token linear layer with a residual add (the attention's out_proj and the
- * block's `x + attention(...)`, model.py:268 and :447, in one launch):
+ * block's `x + attention(...)`, model.py:269 and :495, in one launch):
  *
  *   out[r] = residual[r] + round(weight[r, :] . x + bias[r])     r < rows
  *
@@ -308,7 +315,7 @@ int32_t mie_moe_route(const void* x, const void* router_weight, int32_t num_expe
  *
  * dtype (float32 or bfloat16) is that of x, the weights, hidden_act and out;
  * router_logits and route_weights are float32 either way, the routing the
- * reference keeps in float32 (model.py:450-453).  Sums run in float32.  In
+ * reference keeps in float32 (model.py:448-452).  Sums run in float32.  In
  * bfloat16 each value is rounded where the reference's PyTorch path stores
  * one: each Linear's output (sum plus bias, rounded once), GELU's, the route
  * weight, the weighted product and each partial sum of the expert-id-ordered
@@ -321,7 +328,7 @@ int32_t mie_moe_decode(const void* x, const void* router_weight, const void* w1,
                        int32_t dtype, void* stream);
 
 /*
- * The MoE half of a decoder block for ONE token (model.py:446-449):
+ * The MoE half of a decoder block for ONE token (model.py:496-497):
  *
  *   out = x + MoE(LayerNorm(x; ln_weight, ln_bias, ln_eps))
  *
@@ -431,7 +438,7 @@ int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_st
 /*
  * Decode attention of ONE token fused with the attention's output projection
  * (paged_attention.decode, paged_attention.py:113-154, then out_proj,
- * model.py:268), one launch.  For each head h the launch computes
+ * model.py:269), one launch.  For each head h the launch computes
  *
  *   a_h = softmax(scale * q_h . K_h^T) . V_h   over tokens [0, ctx)   (as mie_paged_decode)
  *   y_h = W_out[:, h*D : (h+1)*D] . a_h        (W_out [dim, dim] row-major, dim = H * D)
@@ -457,7 +464,7 @@ int32_t mie_attn_out_acc(const void* q, const void* k_pool, const void* v_pool, 
                          void* acc, int32_t dtype, void* stream);
 
 /*
- * The rest of a decoder block after mie_attn_out_acc (model.py:447-449):
+ * The rest of a decoder block after mie_attn_out_acc (model.py:495-497):
  *
  *   h_out = x + round(acc * 2^-32 + b_out)          (NaN everywhere when acc[dim] != 0)
  *   out   = h_out + MoE(LayerNorm(h_out))           (as mie_moe_decode_block)
@@ -478,7 +485,7 @@ int32_t mie_moe_decode_block_acc(const void* x, const void* acc, const void* b_o
 
 /*
  * One decoder block for ONE decode token (TransformerMoEBlock.forward,
- * model.py:446-449, with the attention half model.py:226-269) from a launch
+ * model.py:494-498, with the attention half model.py:226-269) from a launch
  * plan stored in caller-owned host memory of mie_block_plan_bytes() bytes.
  * mie_block_decode(plan, x, counters, position, stream) issues, on `stream`:
  *

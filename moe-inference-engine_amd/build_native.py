@@ -5,11 +5,7 @@
 compiles each csrc/*.hip with hipcc (in parallel, one object per source) and
 links the objects into moe_engine/libmie_paged.so.  The library is written to
 a temporary name first and renamed, so a process that already mapped the old
-file keeps a consistent copy.  The measurement probes bench.py runs
-(csrc/probes/*.hip: read ceilings, launch floor, grid waits, L2 reuse) go into
-their own moe_engine/libmie_probes.so, apart from the product library, with a
-copy of the decode kernels built with MIE_DECODE_TIMELINE (per-workgroup
-timestamps).
+file keeps a consistent copy.
 """
 
 import os
@@ -25,7 +21,6 @@ REPO_ROOT = PKG_ROOT.parent
 CSRC = PKG_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 OUTPUT = PKG_ROOT / "moe_engine" / "libmie_paged.so"
-PROBE_OUTPUT = PKG_ROOT / "moe_engine" / "libmie_probes.so"
 ARCH = os.environ.get("MIE_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32.
@@ -53,15 +48,8 @@ def _run(cmd, verbose):
     return proc.returncode, stderr
 
 
-# The probe library also carries an instrumented copy of the decode kernels
-# (with what they call), built with MIE_DECODE_TIMELINE.
-PROBE_PRODUCT_SOURCES = ("paged_decode.hip", "kv_copy.hip", "capi.hip")
-
-
 def build(verbose: bool = True) -> Path:
     _link(sorted(CSRC.glob("*.hip")), OUTPUT, verbose)
-    probe_sources = sorted((CSRC / "probes").glob("*.hip")) + [CSRC / n for n in PROBE_PRODUCT_SOURCES]
-    _link(probe_sources, PROBE_OUTPUT, verbose, ["-DMIE_DECODE_TIMELINE"])
     return OUTPUT
 
 

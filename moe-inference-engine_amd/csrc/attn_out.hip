@@ -1,7 +1,7 @@
 // Decode attention of one token fused with the attention's output projection.
 //
 // The reference's attention half of a decoder block for one decode token
-// (src/moe_engine/model.py:226-269 and :447) is, after the QKV projection and
+// (src/moe_engine/model.py:226-269 and :495) is, after the QKV projection and
 // the cache write:
 //
 //   a_h  = softmax(scale * q_h . K_h^T) . V_h          for each head h

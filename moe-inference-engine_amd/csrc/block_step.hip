@@ -1,6 +1,6 @@
 // One decoder block for one decode token from a stored launch plan.
 //
-// The block of the reference (src/moe_engine/model.py:446-449, attention half
+// The block of the reference (src/moe_engine/model.py:494-498, attention half
 // :226-269) for a single new token is, with a plan that holds an accumulator
 // row and a context of at most kFusedMaxCtx tokens, four launches of this
 // library: the QKV projection into the pool (mie_qkv_append), the attention

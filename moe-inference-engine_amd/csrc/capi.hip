@@ -31,3 +31,17 @@ int32_t check_launch(const char* what) {
 extern "C" int32_t mie_abi_version(void) { return MIE_ABI_VERSION; }
 
 extern "C" const char* mie_last_error(void) { return mie::g_last_error; }
+
+namespace {
+__global__ __launch_bounds__(256) void empty_kernel() {}
+}  // namespace
+
+// Measurement only: `workgroups` workgroups of 256 threads of an empty
+// kernel, so a caller can time the launch floor that latency-bound calls
+// cannot go under.
+extern "C" int32_t mie_empty_launch(int32_t workgroups, void* stream) {
+  if (workgroups < 1 || workgroups > (1 << 20)) return mie::fail(MIE_ERR_INVALID, "mie_empty_launch: workgroups %d", workgroups);
+  mie::clear_error();
+  hipLaunchKernelGGL(empty_kernel, dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream));
+  return mie::check_launch("mie_empty_launch");
+}

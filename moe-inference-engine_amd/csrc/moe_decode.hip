@@ -19,7 +19,7 @@
 //
 // Storage is float32 or bfloat16 (weights, x, the GELU activations and the
 // output; the routing logits and weights are float32 in both, as the
-// reference keeps routing in float32, model.py:450-453).  Every product and
+// reference keeps routing in float32, model.py:448-452).  Every product and
 // sum runs in float32.  For bfloat16 each result is rounded where the
 // reference's PyTorch path stores a bfloat16 tensor: the norm's output, each
 // Linear's output (its float32 sum plus bias, rounded once), GELU's, the
@@ -35,7 +35,7 @@
 // and stays in L2 - so no launch waits on a separate route kernel; workgroup
 // (0, 0) writes the routing outputs, which the W2 launch reads.  The block
 // form also folds in the block's norm (out = x + MoE(LayerNorm(x)),
-// model.py:446-449): the norm goes into W1's LDS staging and the residual add
+// model.py:494-498): the norm goes into W1's LDS staging and the residual add
 // into W2's store.
 //
 // The GEMVs are HBM-bound (2 * top_k * dim * hidden * 4 bytes per token,

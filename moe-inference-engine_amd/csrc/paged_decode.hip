@@ -565,22 +565,9 @@ struct WgOrder {
   uint16_t seq[kWgOrderMax];
 };
 
-#ifdef MIE_DECODE_TIMELINE
-// Measurement build only (libmie_probes.so, bench.py's decode_timeline): when
-// set, each workgroup of the workgroup form records its start and end on the
-// 100 MHz real-time clock, its XCD and hardware id, its sequence and length,
-// then the time each of its waves finished its slice: kTimelineWords words
-// per workgroup in grid order.  The product library is built without it.
-constexpr int kTimelineWords = 4 + kSplitWaves;
-__device__ uint64_t* g_decode_timeline;
-#endif
-
 template <int DT, int D, bool FAST>
 __global__ __launch_bounds__(64 * kSplitWaves) __attribute__((amdgpu_waves_per_eu(kMinWaves, 8)))
 void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
-#ifdef MIE_DECODE_TIMELINE
-  const uint64_t tl_start = wall_clock64();
-#endif
   using G = Geometry<DT, D, kWgTileWords>;
   constexpr int VEC = G::VEC, NW = G::NW, LPT = G::LPT, ELT = G::ELT;
   constexpr int kStates = kSplitWaves + 1;  // the waves' slices, then a fused append's new token
@@ -619,11 +606,6 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
   bool bad = false;
   if (t_begin < t_end)
     attend_range<DT, D, FAST, kWgTileWords, true>(a, b, h, t_begin, t_end, lane, m, l, acc, bad, win_ids);
-#ifdef MIE_DECODE_TIMELINE
-  if (lane == 0 && g_decode_timeline)
-    g_decode_timeline[kTimelineWords * (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x) + 4 + wave] =
-        wall_clock64();
-#endif
   __syncthreads();  // s_bad is cleared
   const int g = lane / LPT;
   const int jl = lane % LPT;
@@ -693,17 +675,6 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
     }
   }
   __syncthreads();
-#ifdef MIE_DECODE_TIMELINE
-  if (threadIdx.x == 0 && g_decode_timeline) {
-    uint64_t* r = g_decode_timeline + kTimelineWords * (static_cast<int64_t>(blockIdx.y) * gridDim.x + blockIdx.x);
-    r[0] = tl_start;
-    r[1] = wall_clock64();
-    // HW_REG_XCC_ID (bits 3:0) and HW_REG_HW_ID (all 32 bits).
-    r[2] = (static_cast<uint64_t>(__builtin_amdgcn_s_getreg((3 << 11) | 20)) << 32) |
-           static_cast<uint32_t>(__builtin_amdgcn_s_getreg((31 << 11) | 4));
-    r[3] = (static_cast<uint64_t>(b) << 32) | static_cast<uint32_t>(ctx);
-  }
-#endif
   // Threads 0 .. D/4-1 merge four output elements each.
   const int col = threadIdx.x * 4;
   if (col >= D) return;
@@ -1241,12 +1212,3 @@ extern "C" int32_t mie_paged_decode_noalloc(const void* q, int64_t q_stride_b, i
                      MIE_PAGED_DECODE_NOALLOC_MAX_WORKSPACE, partition_tokens, nullptr, nullptr, 0, 0, dtype, stream);
 }
 
-#ifdef MIE_DECODE_TIMELINE
-// Measurement build only: sets (or, with NULL, clears) the buffer the
-// workgroup form records into, kTimelineWords (20) uint64 per workgroup of the
-// next launches.
-extern "C" int32_t mie_probe_decode_timeline(void* buffer) {
-  const hipError_t e = hipMemcpyToSymbol(HIP_SYMBOL(g_decode_timeline), &buffer, sizeof(buffer));
-  return e == hipSuccess ? 0 : 2;
-}
-#endif

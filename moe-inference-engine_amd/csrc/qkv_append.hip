@@ -20,7 +20,7 @@
 //
 // The same body, with a residual epilogue instead of the pool stores, is the
 // attention's output projection plus the block's residual add
-// (model.py:268 and the block's `x + attention(...)`): out = residual +
+// (model.py:269 and the block's `x + attention(...)`): out = residual +
 // round(W @ x + b) - one launch in place of a GEMM and an add.
 //
 // With the norm and a pick epilogue it is the decode step's head

@@ -17,7 +17,7 @@ import torch
 
 LIB_NAME = "libmie_paged.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 # enum mie_dtype
 DTYPE_CODES = {
@@ -39,6 +39,7 @@ _f32 = ctypes.c_float
 _SIGNATURES = {
     "mie_abi_version": (_i32, []),
     "mie_last_error": (ctypes.c_char_p, []),
+    "mie_empty_launch": (_i32, [_i32, _c_void_p]),
     "mie_kv_append": (
         _i32,
         [_c_void_p, _c_void_p, _i64, _i64, _i32,  # pools, strides, num_blocks

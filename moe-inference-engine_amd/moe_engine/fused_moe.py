@@ -196,7 +196,7 @@ def decode(x, router_weight, w1_base, b1_base, w2_base, b2_base, *, router_logit
 def decode_block(x, norm_weight, norm_bias, norm_eps, router_weight, w1_base, b1_base, w2_base, b2_base, *,
                  router_logits, expert_ids, route_weights, hidden, out) -> torch.Tensor:
     """The MoE half of a decoder block for one token, out = x + MoE(LayerNorm(x))
-    (reference model.py:446-449), in two launches; the routing workspaces are
+    (reference model.py:494-498), in two launches; the routing workspaces are
     filled as decode() fills them.  norm_weight None skips the norm.  Returns
     `out` viewed as [1, 1, hidden]."""
     params = [t for t in (norm_weight, norm_bias) if t is not None]

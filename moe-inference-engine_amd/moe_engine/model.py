@@ -383,7 +383,7 @@ class CachedAttention(_TracksReplacement, nn.Module):
 
     def fused_decode(self, x, norm, cache, layer_idx, position: int):
         """x + attention(norm(x)) for one decode token - the attention half of
-        the block (reference model.py:447) - in three launches: the QKV
+        the block (reference model.py:495) - in three launches: the QKV
         projection stored straight into the paged pools (mie_qkv_append), the
         paged decode, and out_proj with the residual add (mie_linear_residual).
         Returns None when that path does not apply; the caller then runs
@@ -755,7 +755,7 @@ class TransformerMoEBlock(nn.Module):
         # plan (eagerly, or recorded into a graph with device positions);
         # otherwise each half takes its fused path where it applies (same
         # results to float32 rounding), else the reference's block
-        # (model.py:446-449).
+        # (model.py:494-498).
         if position > 0 and x.shape[1] == 1:
             out = self._decode_one_token(x, cache, layer_idx, position)
             if out is not None:

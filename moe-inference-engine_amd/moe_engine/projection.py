@@ -1,7 +1,7 @@
 """One-token linear layers through the HIP library.
 
 - linear_residual (mie_linear_residual): the attention's output projection and
-  the block's residual add (reference src/moe_engine/model.py:268 and :447,
+  the block's residual add (reference src/moe_engine/model.py:269 and :495,
   `x + out_proj(attn)`) as one launch: out = residual + round(weight @ x + bias).
 - lm_head (mie_lm_head): the decode step's head, final_norm + output_projection
   (model.py:564-565), optionally with generate's greedy torch.argmax (:603)
@@ -22,11 +22,13 @@ from moe_engine import _native
 
 # Per host thread: the logits of its last lm_head(keep_pick=True) call, with
 # the picks its workgroups left - last_pick = (logits, their version counter
-# then, picks) - and the picks' workspaces by (device, vocab).  Holding the
-# logits keeps their memory from being reused, so a tensor at their address
-# is one of their views, and views share the version counter, which counts
-# every in-place write.  Threads keep their own workspaces, so one thread's
-# head never overwrites picks another thread is about to merge.
+# then, picks, the stream the head ran on) - and the picks' workspaces by
+# (device, vocab, stream).  Holding the logits keeps their memory from being
+# reused, so a tensor at their address is one of their views, and views share
+# the version counter, which counts every in-place write.  Threads keep their
+# own workspaces, and so does each stream, so a head queued on one thread or
+# stream never overwrites picks that an argmax queued on another is about to
+# merge; the picks are merged only on the stream that wrote them.
 _pick_state = threading.local()
 
 
@@ -43,8 +45,10 @@ def _kept_picks(x):
     rec = _state().last_pick
     if rec is None or x.is_inference():
         return None
-    logits, version, workspace = rec
+    logits, version, workspace, stream = rec
     if x.data_ptr() != logits.data_ptr() or x.numel() != logits.numel() or x.device != logits.device:
+        return None
+    if _native.stream_of(x) != stream:
         return None
     return workspace if x._version == version else None
 
@@ -130,8 +134,9 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
         raise ValueError(f"out must hold {vocab} contiguous values")
     ws_ptr, ws_bytes = 0, 0
     keep_pick = keep_pick and token_out is None and not out.is_inference()
+    stream = _native.stream_of(weight)
     if keep_pick:
-        key = (device, vocab)
+        key = (device, vocab, stream)
         workspace = st.workspaces.get(key)
         if workspace is None:
             workspace = st.workspaces[key] = torch.empty(head_workspace_bytes(vocab), dtype=torch.uint8,
@@ -160,12 +165,12 @@ def lm_head(x, norm, linear, out=None, token_out=None, workspace=None, advance=N
             x.data_ptr(), _native.ptr(ln_w), _native.ptr(ln_b), eps, weight.data_ptr(), _native.ptr(bias),
             vocab, dim, out.data_ptr(), _native.ptr(token_out), ws_ptr, ws_bytes,
             _native.ptr(advance), 0 if advance is None else advance.numel(),
-            _native.dtype_code(dtype), _native.stream_of(weight),
+            _native.dtype_code(dtype), stream,
         ),
         "mie_lm_head",
     )
     if keep_pick:
-        st.last_pick = (out, out._version, workspace)
+        st.last_pick = (out, out._version, workspace, stream)
     return out
 
 

@@ -142,7 +142,7 @@ def qkv_project_fp64(x, in_proj_weight, in_proj_bias, heads, norm_weight=None, n
     return q, k, v
 
 
-# ---- the attention half of a block for one decode token (model.py:263-268, :447)
+# ---- the attention half of a block for one decode token (model.py:260-269, :495)
 
 
 def attention_half_fp64(q, k, v, out_proj_weight, out_proj_bias, x, scale=None):
@@ -152,8 +152,8 @@ def attention_half_fp64(q, k, v, out_proj_weight, out_proj_bias, x, scale=None):
     out_proj_bias [dim] or None; x [dim] (the block's input, the residual).
     The per-head attention outputs are concatenated head by head - the
     [1, H, 1, D] -> [1, 1, dim] reshape of CachedAttention.forward
-    (model.py:267) - and projected (model.py:268), then added to x
-    (model.py:447).  Returns (out_proj output, x + it).
+    (model.py:269) - and projected (model.py:269), then added to x
+    (model.py:495).  Returns (out_proj output, x + it).
     """
     a = attention_fp64(q, k, v, scale).reshape(-1)
     o = to_f64(out_proj_weight) @ a

@@ -157,7 +157,7 @@ def test_generate_validates_arguments():
 
 def test_cache_follows_model_dtype():
     """The contiguous cache (the comparator) takes the model's dtype too.
-    Routing stays in float32 for every model dtype (model.py:446-449), and a
+    Routing stays in float32 for every model dtype (model.py:448-452), and a
     one-row router product can differ from the batched one in its last float32
     bits, so float64 logits agree to float32 rounding, not float64's."""
     engine = make_engine().double()

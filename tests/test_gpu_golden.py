@@ -5,8 +5,8 @@ whole decode step replayed from a HIP graph (moe_engine.graphs).
 
 Tokens must be identical.  Logits differ from the reference CPU run only by
 GPU rounding (hipBLASLt and the HIP GEMVs against the CPU BLAS); they are
-checked within a bound far below the logit scale (|logit| ~ 28 at d 768),
-with identical argmax at every step.
+checked within 2e-3 at config 1's shape (about six times the measured
+difference; |logit| ~ 28 at d 768), with identical argmax at every step.
 """
 
 import pytest
@@ -18,7 +18,11 @@ from test_golden import FIXTURES, build, check_logits, load, step_logits
 
 pytestmark = pytest.mark.gpu
 
-ATOL = {"tiny": 1e-4, "config1_ffn3072": 2e-2, "config1": 2e-2}
+# The measured GPU-against-CPU difference at config 1 is 3.4e-4 (hipBLASLt
+# and the HIP GEMVs against the CPU BLAS, |logit| ~ 28); the bound is about 6x
+# that, so a drift of the fused attention / out_proj path far below the argmax
+# margin still fails.
+ATOL = {"tiny": 1e-4, "config1_ffn3072": 2e-3, "config1": 2e-3}
 
 
 def paged_cache(model, fixture, mode):

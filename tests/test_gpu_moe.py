@@ -255,7 +255,7 @@ def test_auto_uses_fused_kernel_for_decode_and_pytorch_for_prefill():
 @pytest.mark.parametrize("norm", [True, False])
 def test_block_decode_matches_norm_then_pytorch_path(dim, hidden, experts, top_k, norm):
     """decode_block: out = x + MoE(LayerNorm(x)) against the reference block's
-    own sequence (model.py:446-449) with the PyTorch MoE path; routing outputs
+    own sequence (model.py:494-498) with the PyTorch MoE path; routing outputs
     against torch.topk / softmax of the normalised token's router logits."""
     print_case("moe block", dim, hidden, experts, top_k, norm)
     layer = moe(dim, hidden, experts, top_k)

@@ -1,7 +1,7 @@
 """Fused MoE decode in bfloat16 against the reference's PyTorch path in
 bfloat16 (src/moe_engine/model.py:443-461 on a bfloat16 module).
 
-The reference keeps routing in float32 (model.py:450-453) and runs the
+The reference keeps routing in float32 (model.py:448-452) and runs the
 experts in bfloat16: each Linear's output rounded once, GELU's, the route
 weight cast to bfloat16, the weighted product and each index_add_ partial
 sum.  The fused kernels round at the same points and sum in float32, so the
