@@ -38,8 +38,9 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
-SECONDARY_NAMES = ("launch_floor", "config2_single_layer", "config3_append_gather", "config5_long_context",
-                   "fused_moe_decode", "config1_e2e_decode", "config1_bf16_decode")
+SECONDARY_NAMES = ("launch_floor", "north_star_64x8192", "config2_single_layer", "config3_append_gather",
+                   "config5_long_context", "fused_moe_decode", "config1_e2e_decode", "config1_context_sweep",
+                   "config1_attention_micro", "config1_bf16_decode")
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
 
 
@@ -444,6 +445,35 @@ def secondary_config5(torch):
     return res
 
 
+def secondary_north_star(torch, launches=100):
+    """The north star's literal target shape: 64 sequences x 8192 tokens,
+    12 x 64, block 16, bf16 (workloads.north_star_step, the object
+    tests/test_gpu_decode.py checks): the same one-launch decode step as the
+    headline, timed the same way (one HIP event pair around `launches`
+    back-to-back launches), as GB/s of its algorithmic bytes and a fraction
+    of HBM peak."""
+    from moe_engine import workloads
+
+    step = workloads.north_star_step()
+    w = step.w
+    nbytes = workloads.attention_bytes(w.lens, 12, 64, 16, 2) + workloads.append_bytes(len(w.lens), 12, 64, 2)
+    for _ in range(10):
+        step.fused()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(launches):
+        step.fused()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / launches * 1e3
+    del step, w
+    return {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1), "hbm_fraction": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4),
+            "bytes": nbytes, "launches": launches,
+            "note": "64 x 8192 uniform, bf16, shuffled tables over a 40000-block pool; mie_paged_decode_append "
+            "(append fused), average of back-to-back launches between one HIP event pair"}
+
+
 def secondary_launch_floor(torch):
     """The floor a launch-bound call cannot go under on this box: device time
     per call of 64 calls replayed from one HIP graph, each call one or two
@@ -492,7 +522,32 @@ def add_floor_fractions(secondary):
                 cell["hbm_fraction"] = round(cell["gbs"] / PEAK_HBM_GBS, 3)
 
 
-def secondary_e2e(torch, rounds=5, new_tokens=64, cpu_rounds=2):
+def secondary_context_sweep(torch, rounds=21):
+    """BASELINE config 1's model: decode step latency at contexts 16, 64, 256
+    and 1024 (benchmarks/context_sweep.py:50-126) for contiguous,
+    paged-gather, paged-direct, contiguous-direct and the two graph systems,
+    `rounds` interleaved rounds, each system on a fresh cache behind a
+    random pad in every round (moe_engine.harness.context_sweep), with
+    paired paging-cost intervals per context."""
+    from moe_engine import harness
+
+    model = harness.make_model(harness.CONFIG1, seed=0, device="cuda")
+    return harness.context_sweep(model, contexts=(16, 64, 256, 1024), rounds=rounds)
+
+
+def secondary_attention_micro(torch, rounds=21):
+    """One layer's decode attention at config 1's shape (12 x 64, fp32,
+    block 16; benchmarks/attention_micro.py:27-85): us per call for
+    contiguous read + SDPA, paged gather + SDPA, the paged direct kernel and
+    the same kernel on the contiguous layout, `rounds` rounds on freshly
+    placed caches, with device time (graph replays) and paired paging costs
+    for the direct kernel (moe_engine.harness.attention_micro)."""
+    from moe_engine import harness
+
+    return harness.attention_micro(harness.CONFIG1, contexts=(16, 64, 256, 1024), rounds=rounds)
+
+
+def secondary_e2e(torch, rounds=21, new_tokens=64, cpu_rounds=2):
     """BASELINE config 1 (random init from seed 0, fp32, block 16, 32-token
     prompt, 64 greedy tokens).
 
@@ -622,11 +677,14 @@ def main():
         chosen = [n for n in args.secondary.split(",") if n] or list(SECONDARY_NAMES)
         for name, fn in (
             ("launch_floor", secondary_launch_floor),
+            ("north_star_64x8192", secondary_north_star),
             ("config2_single_layer", secondary_config2),
             ("config3_append_gather", secondary_config3),
             ("config5_long_context", secondary_config5),
             ("fused_moe_decode", secondary_moe),
             ("config1_e2e_decode", secondary_e2e),
+            ("config1_context_sweep", secondary_context_sweep),
+            ("config1_attention_micro", secondary_attention_micro),
             ("config1_bf16_decode", secondary_e2e_bf16),
         ):
             if name not in chosen:
@@ -668,16 +726,18 @@ def main():
         },
         "roofline": main_res["roofline"],
         "cpu_baseline": cpu,
-        "per_token_decode_ms": per_token_decode_ms(secondary.get("config1_e2e_decode")),
+        "per_token_decode_ms": per_token_decode_ms(secondary.get("config1_e2e_decode"),
+                                                   secondary.get("config1_context_sweep")),
         "secondary": secondary,
     }
     print(json.dumps(line), flush=True)
 
 
-def per_token_decode_ms(e2e):
+def per_token_decode_ms(e2e, sweep=None):
     """The metric's second half: BASELINE config 1's median greedy decode
     latency per token for each system, from the config1_e2e_decode secondary
-    (None when it did not run)."""
+    (None when it did not run), with the paging-cost intervals of the e2e
+    rounds and of the context sweep at every context."""
     if not e2e or "summary" not in e2e:
         return None
     out = {system: s["decode_median_ms"] for system, s in e2e["summary"].items()}
@@ -699,6 +759,15 @@ def per_token_decode_ms(e2e):
         out["parity"] = {k: parity[k] for k in ("engine_cache", "max_abs_logit_diff", "max_rel_logit_diff",
                                                 "greedy_tokens_compared", "first_greedy_mismatch",
                                                 "tokens_equal_reference_engine") if k in parity}
+    if sweep and "paging_cost_ms" in sweep:
+        out["context_sweep"] = {
+            "median_step_ms": sweep["median_step_ms"],
+            "paging_cost_ms": sweep["paging_cost_ms"],
+            "rounds": sweep["rounds"],
+            "placement_sampled": sweep["placement_sampled"],
+        }
+    out["rounds"] = e2e.get("rounds")
+    out["placement_sampled"] = e2e.get("placement_sampled")
     out["workload"] = ("BASELINE config 1: 12 layers, d 768, 12 x 64 heads, top-2 of 8, FFN 2048, vocab 50257, "
                        "fp32, random init seed 0, 32-token prompt, 64 greedy tokens, block 16")
     return out

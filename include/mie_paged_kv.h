@@ -144,6 +144,19 @@ int32_t mie_kv_gather(const void* k_pool, const void* v_pool, int64_t pool_strid
                       int32_t dtype, void* stream);
 
 /*
+ * Block-table mirror append: table[start + i] = ids[i] for i < count, where
+ * `table` is a device int32 table of `table_len` entries and `ids` is HOST
+ * memory, read before the call returns (the ids travel in the launch's
+ * arguments).  Replaces the device-mirror update of PagedKVCache._reserve
+ * (model.py:135-143), block_table_device[start:start + n] =
+ * torch.tensor(taken), which is a pageable host-to-device copy the host waits
+ * for plus an indexing launch.  0 <= count <= 16; the entries must lie inside
+ * the table.  One launch, queued on `stream`; the host does not wait.
+ */
+int32_t mie_block_table_append(int32_t* table, int32_t table_len, int32_t start, const int32_t* ids,
+                               int32_t count, void* stream);
+
+/*
  * Direct paged decode attention for `batch` sequences with one query token
  * each.  Replaces paged_attention.decode (paged_attention.py:113-154) and
  * _paged_decode_kernel (paged_attention.py:46-110), which computes for one

@@ -259,3 +259,48 @@ extern "C" int32_t mie_kv_gather(const void* k_pool, const void* v_pool, int64_t
   }
   return mie::check_launch("mie_kv_gather");
 }
+
+// ---- block-table mirror append ------------------------------------------------
+//
+// The host allocator takes a new block once every block_size tokens and
+// appends its id to the sequence's device table.  A torch copy of a host list
+// is a pageable host-to-device transfer (a staging copy the host waits for)
+// plus an indexing launch; here the ids travel in the kernel arguments, so the
+// host only queues one small launch and never waits.
+
+namespace {
+
+constexpr int kTableAppendMax = 16;
+
+struct TableAppend {
+  int32_t* table;
+  int32_t start;
+  int32_t count;
+  int32_t ids[kTableAppendMax];
+};
+
+__global__ __launch_bounds__(64) void block_table_append_kernel(TableAppend a) {
+  const int i = threadIdx.x;
+  if (i < a.count) a.table[a.start + i] = a.ids[i];
+}
+
+}  // namespace
+
+extern "C" int32_t mie_block_table_append(int32_t* table, int32_t table_len, int32_t start, const int32_t* ids,
+                                          int32_t count, void* stream) {
+  if (count < 0 || count > kTableAppendMax)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_table_append: count %d outside [0, %d]", count, kTableAppendMax);
+  if (count == 0) return MIE_OK;
+  if (!table || !ids) return mie::fail(MIE_ERR_INVALID, "mie_block_table_append: null pointer");
+  if (start < 0 || table_len < 0 || static_cast<int64_t>(start) + count > table_len)
+    return mie::fail(MIE_ERR_INVALID, "mie_block_table_append: entries [%d, %d) outside a table of %d", start,
+                     start + count, table_len);
+  TableAppend a;
+  a.table = table;
+  a.start = start;
+  a.count = count;
+  for (int i = 0; i < kTableAppendMax; ++i) a.ids[i] = i < count ? ids[i] : 0;
+  mie::clear_error();
+  block_table_append_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(a);
+  return mie::check_launch("mie_block_table_append");
+}

@@ -56,6 +56,7 @@ _SIGNATURES = {
          _c_void_p, _c_void_p, _i64, _i64,  # outputs, strides h/t
          _i32, _i32, _i32, _i32, _c_void_p],  # heads, head_dim, block_size, dtype, stream
     ),
+    "mie_block_table_append": (_i32, [_c_void_p, _i32, _i32, ctypes.POINTER(_i32), _i32, _c_void_p]),
     "mie_paged_decode": (
         _i32,
         [_c_void_p, _i64, _i64,  # q, strides b/h

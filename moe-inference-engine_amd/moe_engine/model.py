@@ -39,6 +39,8 @@ from moe_engine import _native, embedding, fused_moe, kv_ops, paged_attention, p
 
 EOS_TOKEN_ID = 50256
 ATTENTION_MODES = ("auto", "direct", "gather")
+# Block ids one mie_block_table_append launch carries in its arguments.
+_TABLE_APPEND_MAX = 16
 MOE_MODES = ("auto", "direct", "reference")
 
 # A block's one-token launch plan (TransformerMoEBlock._decode_one_token) and a
@@ -224,8 +226,9 @@ class PagedKVCache:
         self.position = 0
         # Device mirror of block_table for the kernels.  Only the first
         # len(block_table) entries are meaningful; new entries are appended as
-        # blocks are reserved (one small host-to-device copy per block_size
-        # tokens), never rebuilt.
+        # blocks are reserved (once per block_size tokens: on a ROCm device one
+        # small launch carrying the ids, on the CPU an indexed copy), never
+        # rebuilt.
         self.block_table_device = torch.zeros(
             allocator.num_blocks, dtype=torch.int32, device=allocator.k_pool.device
         )
@@ -254,9 +257,20 @@ class PagedKVCache:
         if taken:
             start = len(self.block_table)
             self.block_table.extend(taken)
-            self.block_table_device[start : start + len(taken)] = torch.tensor(
-                taken, dtype=torch.int32, device=self.block_table_device.device
-            )
+            if self.allocator.on_device and len(taken) <= _TABLE_APPEND_MAX:
+                # The ids go in the arguments of one small launch on the
+                # current stream: no staging copy for the host to wait on.
+                ids = (ctypes.c_int32 * len(taken))(*taken)
+                table = self.block_table_device
+                _native.check(
+                    _native.lib().mie_block_table_append(table.data_ptr(), table.numel(), start, ids, len(taken),
+                                                         _native.stream_of(table)),
+                    "mie_block_table_append",
+                )
+            else:
+                self.block_table_device[start : start + len(taken)] = torch.tensor(
+                    taken, dtype=torch.int32, device=self.block_table_device.device
+                )
 
     def _block_for(self, token_pos: int):
         size = self.allocator.block_size

@@ -220,3 +220,18 @@ def config4_step(out_dtype=torch.bfloat16, partition_tokens=0, device="cuda"):
     k_new, v_new = take_last_tokens(w)
     out = torch.empty(len(lens), 12, 64, dtype=out_dtype, device=device)
     return DecodeStep(w, k_new, v_new, out, partition_tokens)
+
+
+NORTH_STAR_BATCH, NORTH_STAR_CONTEXT = 64, 8192
+
+
+def north_star_step(out_dtype=torch.bfloat16, partition_tokens=0, device="cuda"):
+    """The north star's literal target shape: 64 sequences of 8192 tokens
+    each, 12 x 64, block 16, bf16, tables shuffled over a shared 40000-block
+    pool (32768 blocks used), seed 3; the decode step as config4_step builds
+    it (new rows taken out of the pool).  Output [64, 12, 64] in out_dtype."""
+    lens = [NORTH_STAR_CONTEXT] * NORTH_STAR_BATCH
+    w = make_workload(lens, block_size=16, num_blocks=40000, dtype=torch.bfloat16, seed=3, device=device)
+    k_new, v_new = take_last_tokens(w)
+    out = torch.empty(len(lens), 12, 64, dtype=out_dtype, device=device)
+    return DecodeStep(w, k_new, v_new, out, partition_tokens)

@@ -224,3 +224,19 @@ def test_embedding_plan_entries_fail_on_the_host():
     assert rc == INVALID and b"null token id" in lib.mie_last_error()
     rc = lib.mie_block_decode_embed(raw, ptr(), None, 3, None)
     assert rc == INVALID and b"not initialised" in lib.mie_last_error()
+
+
+def test_block_table_append_and_empty_launch_fail_on_the_host():
+    lib = _native.lib()
+    ids = (ctypes.c_int32 * 17)(*range(17))
+    rc = lib.mie_block_table_append(ptr(), 64, 0, ids, 17, None)
+    assert rc == INVALID and b"count 17" in lib.mie_last_error()
+    rc = lib.mie_block_table_append(ptr(), 64, -1, ids, 1, None)
+    assert rc == INVALID and b"outside a table" in lib.mie_last_error()
+    rc = lib.mie_block_table_append(ptr(), 64, 60, ids, 5, None)
+    assert rc == INVALID and b"outside a table" in lib.mie_last_error()
+    rc = lib.mie_block_table_append(None, 64, 0, ids, 1, None)
+    assert rc == INVALID and b"null pointer" in lib.mie_last_error()
+    assert lib.mie_block_table_append(None, 0, 0, ids, 0, None) == 0  # nothing to append: no launch
+    rc = lib.mie_empty_launch(0, None)
+    assert rc == INVALID and b"workgroups 0" in lib.mie_last_error()

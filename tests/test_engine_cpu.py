@@ -1,12 +1,14 @@
 """Host-side engine semantics on the CPU (no GPU needed).
 
-Mirrors the reference's CPU-runnable tests of the paged path
-(tests/test_parity.py, tests/test_paged_attention.py:188-282,
-tests/test_fused_moe.py:167-197): allocator reclaim and rollback, batch
-rejection, dtype following, generate() validation, the prefill fast path,
-fail-before-mutate for a forced 'direct' that cannot run, and the device
-mirror of the block table.  The product's CPU paged cache is also compared
-with the oracle's closed forms.
+Covers the behaviour the reference's CPU-runnable tests of the paged path
+check (tests/test_parity.py, tests/test_paged_attention.py:188-282,
+tests/test_fused_moe.py:167-197) with cases drawn here: decode through
+either cache against one forward pass, sequences sharing a pool, allocation
+against the oracle's LIFO allocator with rollback and reuse, batch refusal,
+generate()'s contract, dtype following, the prefill fast path and
+fail-before-mutate for a forced 'direct' that cannot run (one snapshot of
+every cache and allocator field).  The product's CPU paged cache is also
+compared with the oracle's closed forms.
 """
 
 import random
@@ -19,13 +21,15 @@ from moe_engine import paged_attention
 from moe_engine.model import BlockAllocator, KVCache, Model, ModelConfig, MoEFeedForward, PagedKVCache
 from oracle import paged_ref as ref
 
-TINY = dict(max_seq_length=32, vocab_size=96, num_layers=2, hidden_dim=32, num_experts=4, top_k=2)
-TINY128 = dict(TINY, max_seq_length=128)
+# A small model of this file's own: 6 heads of 8, five experts.
+SMALL = dict(max_seq_length=40, vocab_size=88, num_layers=2, hidden_dim=48, num_heads=6, num_experts=5, top_k=2)
+SMALL128 = dict(SMALL, max_seq_length=128)
+VOCAB, WIDTH = SMALL["vocab_size"], SMALL["hidden_dim"]
 
 
 def make_engine(**overrides):
     torch.manual_seed(0)
-    return Model(ModelConfig(**dict(TINY, **overrides))).eval()
+    return Model(ModelConfig(**dict(SMALL, **overrides))).eval()
 
 
 def stepwise(engine, ids, cache, prefill):
@@ -36,238 +40,252 @@ def stepwise(engine, ids, cache, prefill):
     return torch.stack(steps, dim=1)
 
 
-def test_cached_decode_matches_full_forward():
-    engine = make_engine()
-    ids = torch.randint(0, TINY["vocab_size"], (1, 16))
+# ---- drawn engine cases --------------------------------------------------------------
+#
+# Each case below draws its own pool size, block size and sequence lengths from
+# a seeded generator, so one test covers partial and full last blocks, block
+# sizes from one token up, and several sequences on one pool.
+
+
+def draw_case(seed):
+    """(block_size, prompt_len, total_len) with prompt_len < total_len <=
+    SMALL128's max_seq_length, prompt and total not tied to block edges."""
+    rng = random.Random(seed)
+    block_size = rng.choice([1, 2, 3, 5, 7, 12])
+    prompt_len = rng.randint(1, 30)
+    total = rng.randint(prompt_len + 2, min(SMALL128["max_seq_length"], prompt_len + 40))
+    return block_size, prompt_len, total
+
+
+def one_pass_logits(engine, ids):
     with torch.no_grad():
-        full = engine(ids, engine.new_cache())
-    torch.testing.assert_close(stepwise(engine, ids, engine.new_cache(), 4), full[:, 3:], atol=1e-4, rtol=1e-4)
+        return engine(ids, engine.new_cache())
 
 
-@pytest.mark.parametrize("mode", ["gather", "auto"])
-def test_paged_decode_matches_full_forward(mode):
-    engine = make_engine()
-    ids = torch.randint(0, TINY["vocab_size"], (1, 16))
-    with torch.no_grad():
-        full = engine(ids, engine.new_cache())
-    cache = engine.new_block_allocator(num_blocks=8, block_size=4, attention_mode=mode).new_cache()
-    torch.testing.assert_close(stepwise(engine, ids, cache, 4), full[:, 3:], atol=1e-4, rtol=1e-4)
+def snapshot(cache):
+    """Every piece of state a failed call must leave as it was: the cache's
+    position, table, device mirror and write-index key, the allocator's free
+    list and both pools."""
+    alloc = cache.allocator
+    return dict(position=cache.position, table=list(cache.block_table), free=list(alloc.free_blocks),
+                key=cache._write_index_key, mirror=cache.block_table_device.clone(),
+                k=alloc.k_pool.clone(), v=alloc.v_pool.clone())
 
 
-def test_paged_cache_shares_pool_without_leaking():
-    engine = make_engine()
-    ids_a = torch.randint(0, TINY["vocab_size"], (1, 16))
-    ids_b = torch.randint(0, TINY["vocab_size"], (1, 16))
-    allocator = engine.new_block_allocator(num_blocks=8, block_size=4)
-    cache_a, cache_b = allocator.new_cache(), allocator.new_cache()
-    with torch.no_grad():
-        full_a = engine(ids_a, engine.new_cache())
-        full_b = engine(ids_b, engine.new_cache())
-        engine(ids_a[:, :4], cache_a)
-        engine(ids_b[:, :4], cache_b)
-        for t in range(4, 16):  # interleaved, so the two tables alternate in the pool
-            logits_a = engine(ids_a[:, t : t + 1], cache_a)
-            logits_b = engine(ids_b[:, t : t + 1], cache_b)
-    assert not set(cache_a.block_table) & set(cache_b.block_table)
-    torch.testing.assert_close(logits_a[:, -1], full_a[:, -1], atol=1e-4, rtol=1e-4)
-    torch.testing.assert_close(logits_b[:, -1], full_b[:, -1], atol=1e-4, rtol=1e-4)
+def assert_unchanged(cache, before):
+    """The free list is compared as a set of blocks: a rolled-back
+    reservation hands its blocks back with free(taken), in the order they
+    were popped (model.py:131-134), so their order in the list reverses; the
+    exact order is checked against the oracle allocator where it matters."""
+    after = snapshot(cache)
+    for name in ("position", "table", "key"):
+        assert after[name] == before[name], name
+    assert sorted(after["free"]) == sorted(before["free"])
+    for name in ("mirror", "k", "v"):
+        assert torch.equal(after[name], before[name]), name
 
 
-def test_block_allocator_reclaims_freed_blocks():
-    engine = make_engine()
-    ids = torch.randint(0, TINY["vocab_size"], (1, 8))
-    allocator = engine.new_block_allocator(num_blocks=2, block_size=4)
-    cache_a, cache_b = allocator.new_cache(), allocator.new_cache()
-    with torch.no_grad():
-        engine(ids, cache_a)
-        with pytest.raises(RuntimeError, match="no free KV cache blocks left"):
-            engine(ids[:, :1], cache_b)
-        cache_a.free()
-        engine(ids[:, :1], cache_b)
-
-
-def test_failed_allocation_rolls_back():
-    engine = make_engine()
-    allocator = engine.new_block_allocator(num_blocks=1, block_size=4)
-    cache = allocator.new_cache()
-    ids = torch.randint(0, TINY["vocab_size"], (1, 8))  # needs two blocks
-    with torch.no_grad():
-        with pytest.raises(RuntimeError, match="no free KV cache blocks left"):
-            engine(ids, cache)
-        assert cache.block_table == [] and cache.position == 0 and allocator.free_blocks == [0]
-        engine(ids[:, :4], cache)  # still usable
-
-
-def test_allocation_order_matches_oracle_lifo():
-    engine = make_engine()
-    allocator = engine.new_block_allocator(num_blocks=9, block_size=4)
-    random.Random(5).shuffle(allocator.free_blocks)
-    oracle_alloc = ref.LifoAllocator(9)
-    oracle_alloc.free_blocks = list(allocator.free_blocks)
-    cache = allocator.new_cache()
-    table = []
-    with torch.no_grad():
-        engine(torch.randint(0, 96, (1, 7)), cache)
-        ref.reserve(table, oracle_alloc, 7, 4)
-        for n in range(8, 20):
-            engine(torch.randint(0, 96, (1, 1)), cache)
-            ref.reserve(table, oracle_alloc, n, 4)
-    assert cache.block_table == table
-    assert allocator.free_blocks == oracle_alloc.free_blocks
-    assert cache.block_table_device[: len(table)].tolist() == table
-
-
-def test_paged_cache_rejects_batches():
-    engine = make_engine()
-    allocator = engine.new_block_allocator(num_blocks=8, block_size=4)
-    with torch.no_grad(), pytest.raises(ValueError, match="batch size 1"):
-        engine(torch.randint(0, 96, (2, 4)), allocator.new_cache())
-
-
-def test_generate_stops_at_context_limit():
-    engine = make_engine()
-    prompt = torch.randint(0, TINY["vocab_size"], (TINY["max_seq_length"] - 2,))
-    out = engine.generate(prompt, max_new_tokens=10, temperature=0)
-    assert out.shape[1] == TINY["max_seq_length"] + 1  # the last token never enters the cache
-
-
-def test_generate_validates_prompt_and_cache():
-    engine = make_engine()
-    with pytest.raises(ValueError, match="max_seq_length"):
-        engine.generate(torch.randint(0, 96, (TINY["max_seq_length"] + 1,)), max_new_tokens=1)
-    allocator = engine.new_block_allocator(num_blocks=8, block_size=4)
-    used = allocator.new_cache()
-    prompt = torch.randint(0, 96, (1, 4))
-    with torch.no_grad():
-        engine(prompt, used)
-    before = list(used.block_table)
-    with pytest.raises(ValueError, match="fresh cache"):
-        engine.generate(prompt, max_new_tokens=1, cache=used)
-    assert used.block_table == before
-
-
-def test_generate_validates_arguments():
-    engine = make_engine()
-    prompt = torch.randint(0, 96, (4,))
-    for kwargs in (dict(temperature=-1), dict(temperature=float("nan")), dict(top_k=0), dict(max_new_tokens=0)):
-        args = {"max_new_tokens": 4, **kwargs}
-        with pytest.raises(ValueError):
-            engine.generate(prompt, **args)
-
-
-def test_cache_follows_model_dtype():
-    """The contiguous cache (the comparator) takes the model's dtype too.
-    Routing stays in float32 for every model dtype (model.py:448-452), and a
-    one-row router product can differ from the batched one in its last float32
-    bits, so float64 logits agree to float32 rounding, not float64's."""
-    engine = make_engine().double()
-    ids = torch.randint(0, 96, (1, 8))
-    with torch.no_grad():
-        full = engine(ids, engine.new_cache())
-        cache = engine.new_cache()
-        engine(ids[:, :4], cache)
-        step = engine(ids[:, 4:5], cache)
-    assert full.dtype == torch.float64 and step.dtype == torch.float64
-    assert cache.k.dtype == torch.float64
-    torch.testing.assert_close(step[:, -1], full[:, 4], atol=1e-5, rtol=1e-5)
-
-
-def test_paged_cache_follows_model_dtype():
-    engine = make_engine().double()
-    ids = torch.randint(0, 96, (1, 8))
-    with torch.no_grad():
-        full = engine(ids, engine.new_cache())
-        cache = engine.new_block_allocator(num_blocks=2, block_size=4).new_cache()
-        engine(ids[:, :4], cache)
-        step = engine(ids[:, 4:5], cache)
-    assert step.dtype == torch.float64 and cache.allocator.k_pool.dtype == torch.float64
-    torch.testing.assert_close(step[:, -1], full[:, 4], atol=1e-4, rtol=1e-4)
-
-
-def test_auto_mode_matches_gather_mode_on_cpu():
+@pytest.mark.parametrize("seed", range(6))
+def test_teacher_forced_decode_equals_one_pass_forward(seed):
+    """A prompt, then one token per step, through the contiguous cache and the
+    paged cache in 'gather' and 'auto' mode: the logits at every position equal
+    one forward pass over the whole sequence (1e-4), and 'auto' (the gather
+    path on the CPU) equals 'gather' (1e-5)."""
+    block_size, prompt_len, total = draw_case(seed)
     engine = make_engine(max_seq_length=128)
-    ids = torch.randint(0, 96, (1, 16))
-    logits = {}
+    ids = torch.randint(0, VOCAB, (1, total), generator=torch.Generator().manual_seed(100 + seed))
+    want = one_pass_logits(engine, ids)[:, prompt_len - 1 :]
+    blocks = -(-total // block_size)
+    got = {"contiguous": stepwise(engine, ids, engine.new_cache(), prompt_len)}
     for mode in ("gather", "auto"):
-        cache = engine.new_block_allocator(num_blocks=16, block_size=4, attention_mode=mode).new_cache()
-        logits[mode] = stepwise(engine, ids, cache, 8)
-    torch.testing.assert_close(logits["auto"], logits["gather"], atol=1e-5, rtol=1e-5)
+        cache = engine.new_block_allocator(num_blocks=blocks + 3, block_size=block_size,
+                                           attention_mode=mode).new_cache()
+        got[mode] = stepwise(engine, ids, cache, prompt_len)
+        assert len(cache.block_table) == blocks and cache.position == total
+    for name, logits in got.items():
+        torch.testing.assert_close(logits, want, atol=1e-4, rtol=1e-4, msg=name)
+    torch.testing.assert_close(got["auto"], got["gather"], atol=1e-5, rtol=1e-5)
 
 
-def test_prefill_fast_path_matches_contiguous():
+@pytest.mark.parametrize("seed", range(4))
+def test_sequences_sharing_a_pool_stay_apart(seed):
+    """Two to four sequences of drawn lengths decode on one pool in a drawn
+    interleaving.  Their tables never share a block, tables plus free list
+    always partition the pool, and each sequence's last logits equal its own
+    one-pass forward."""
+    rng = random.Random(seed)
+    block_size = rng.choice([2, 3, 4, 6])
+    n_seq = rng.randint(2, 4)
+    lens = [rng.randint(3, 24) for _ in range(n_seq)]
+    prompts = [rng.randint(1, n - 1) for n in lens]
+    num_blocks = sum(-(-n // block_size) for n in lens) + rng.randint(0, 3)
     engine = make_engine(max_seq_length=128)
-    ids = torch.randint(0, 96, (1, 19))  # partial last block
+    alloc = engine.new_block_allocator(num_blocks=num_blocks, block_size=block_size)
+    rng.shuffle(alloc.free_blocks)
+    seqs = [torch.randint(0, VOCAB, (1, n), generator=torch.Generator().manual_seed(seed * 10 + i))
+            for i, n in enumerate(lens)]
+    caches = [alloc.new_cache() for _ in seqs]
+    last = [None] * n_seq
     with torch.no_grad():
-        contiguous = engine(ids, engine.new_cache())
-        paged = engine(ids, engine.new_block_allocator(num_blocks=16, block_size=4).new_cache())
-    torch.testing.assert_close(paged, contiguous, atol=1e-5, rtol=1e-5)
+        for i, (ids, cache) in enumerate(zip(seqs, caches)):
+            last[i] = engine(ids[:, : prompts[i]], cache)[:, -1]
+        pending = [i for i in range(n_seq) for _ in range(lens[i] - prompts[i])]
+        rng.shuffle(pending)
+        for i in pending:  # each sequence's own tokens stay in order
+            t = caches[i].position
+            last[i] = engine(seqs[i][:, t : t + 1], caches[i])[:, -1]
+            held = [b for c in caches for b in c.block_table]
+            assert len(held) == len(set(held))
+            assert sorted(held + alloc.free_blocks) == list(range(num_blocks))
+    for i, ids in enumerate(seqs):
+        torch.testing.assert_close(last[i], one_pass_logits(engine, ids)[:, -1], atol=1e-4, rtol=1e-4)
 
 
-def assert_cache_untouched(cache, allocator, num_blocks):
-    assert cache.position == 0
-    assert cache.block_table == []
-    assert sorted(allocator.free_blocks) == list(range(num_blocks))
-    assert (cache.block_table_device == 0).all()
-    assert cache._write_index_key is None
-
-
-def test_direct_mode_raises_without_rocm_before_mutating():
+@pytest.mark.parametrize("seed", range(5))
+def test_pool_exhaustion_rolls_back_and_freed_blocks_come_back_lifo(seed):
+    """Sequences of drawn lengths are prefilled into a drawn pool until one no
+    longer fits.  Every table and the free list follow the oracle's LIFO
+    allocator step for step; the one that does not fit raises the reference's
+    message and changes nothing (not even its partly reservable blocks); once
+    an earlier sequence is freed the same request succeeds and takes the freed
+    blocks, last freed first."""
+    rng = random.Random(seed)
+    block_size = rng.choice([1, 2, 4, 5])
+    num_blocks = rng.randint(3, 11)
     engine = make_engine()
-    allocator = engine.new_block_allocator(num_blocks=8, block_size=4, attention_mode="direct")
-    cache = allocator.new_cache()
+    alloc = engine.new_block_allocator(num_blocks=num_blocks, block_size=block_size)
+    rng.shuffle(alloc.free_blocks)
+    shadow = ref.LifoAllocator(0)
+    shadow.free_blocks = list(alloc.free_blocks)
+    caches, tables = [], []
+    with torch.no_grad():
+        while True:
+            length = rng.randint(1, min(SMALL["max_seq_length"], 3 * block_size + 1))
+            cache = alloc.new_cache()
+            ids = torch.randint(0, VOCAB, (1, length), generator=torch.Generator().manual_seed(len(caches)))
+            if -(-length // block_size) > len(alloc.free_blocks):
+                before = snapshot(cache)
+                with pytest.raises(RuntimeError, match="no free KV cache blocks left"):
+                    engine(ids, cache)
+                assert_unchanged(cache, before)
+                with pytest.raises(RuntimeError):
+                    ref.reserve([], shadow, length, block_size)
+                assert alloc.free_blocks == shadow.free_blocks
+                break
+            engine(ids, cache)
+            table = []
+            ref.reserve(table, shadow, length, block_size)
+            assert cache.block_table == table and alloc.free_blocks == shadow.free_blocks
+            assert cache.block_table_device[: len(table)].tolist() == table
+            caches.append(cache)
+            tables.append(table)
+        freed = caches[0].block_table[:]
+        caches[0].free()
+        shadow.free(tables[0])
+        assert caches[0].block_table == [] and caches[0].position == 0
+        if -(-length // block_size) <= len(alloc.free_blocks):
+            engine(ids, cache)
+            table = []
+            ref.reserve(table, shadow, length, block_size)
+            assert cache.block_table == table
+            assert cache.block_table[: len(freed)] == freed[::-1][: len(cache.block_table)]
+
+
+@pytest.mark.parametrize("batch", [2, 5])
+def test_more_than_one_sequence_per_paged_cache_is_refused(batch):
+    engine = make_engine()
+    cache = engine.new_block_allocator(num_blocks=6, block_size=3).new_cache()
+    before = snapshot(cache)
+    with torch.no_grad(), pytest.raises(ValueError, match="batch size 1"):
+        engine(torch.randint(0, VOCAB, (batch, 5)), cache)
+    assert_unchanged(cache, before)
+
+
+def test_generate_refuses_bad_requests_and_stops_at_the_context():
+    """generate's contract: bad sampling arguments, an over-long prompt and a
+    cache that already holds tokens raise ValueError without touching the
+    cache; greedy decoding that reaches max_seq_length stops there, returning
+    one token past the cache (it is never fed back)."""
+    engine = make_engine()
+    limit = SMALL["max_seq_length"]
+    prompt = torch.randint(0, VOCAB, (6,), generator=torch.Generator().manual_seed(9))
+    for kwargs in (dict(temperature=-0.5), dict(temperature=float("inf")), dict(top_k=-3),
+                   dict(max_new_tokens=-2)):
+        with pytest.raises(ValueError):
+            engine.generate(prompt, **{"max_new_tokens": 3, **kwargs})
+    with pytest.raises(ValueError, match="max_seq_length"):
+        engine.generate(torch.zeros(limit + 3, dtype=torch.long), max_new_tokens=2)
+    cache = engine.new_block_allocator(num_blocks=12, block_size=3).new_cache()
+    with torch.no_grad():
+        engine(prompt[None, :2], cache)
+    before = snapshot(cache)
+    with pytest.raises(ValueError, match="fresh cache"):
+        engine.generate(prompt, max_new_tokens=2, cache=cache)
+    assert_unchanged(cache, before)
+    for start in (limit - 5, limit - 1):
+        out = engine.generate(torch.randint(0, VOCAB, (start,)), max_new_tokens=limit, temperature=0)
+        assert out.shape[1] == limit + 1
+
+
+@pytest.mark.parametrize("paged", [False, True])
+def test_float64_models_keep_float64_caches(paged):
+    """The caches take the model's dtype; decode in float64 agrees with one
+    float64 pass to float32 rounding (routing runs in float32,
+    model.py:448-452, and a one-row router product may round differently
+    from the batched one)."""
+    engine = make_engine().double()
+    ids = torch.randint(0, VOCAB, (1, 11), generator=torch.Generator().manual_seed(21))
+    cache = engine.new_block_allocator(num_blocks=5, block_size=3).new_cache() if paged else engine.new_cache()
+    got = stepwise(engine, ids, cache, 6)
+    pool = cache.allocator.k_pool if paged else cache.k
+    assert got.dtype == pool.dtype == torch.float64
+    torch.testing.assert_close(got, one_pass_logits(engine, ids)[:, 5:], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("length", [1, 5, 9, 22])
+def test_paged_prefill_at_position_zero_equals_contiguous(length):
+    """The prefill fast path (attention over the fresh K/V at position 0):
+    block size 4 leaves the last block partly filled for most lengths."""
+    engine = make_engine(max_seq_length=128)
+    ids = torch.randint(0, VOCAB, (1, length), generator=torch.Generator().manual_seed(length))
+    with torch.no_grad():
+        paged = engine(ids, engine.new_block_allocator(num_blocks=7, block_size=4).new_cache())
+    torch.testing.assert_close(paged, one_pass_logits(engine, ids), atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("block_size,filled", [(3, 6), (5, 5), (2, 2)])
+def test_forced_direct_that_cannot_run_leaves_everything_as_it_was(block_size, filled):
+    """Forced 'direct' attention (no ROCm device here) and forced 'direct' MoE
+    both raise a message naming 'direct' before the step touches anything:
+    with the cache full up to a block edge, the refused token would have
+    taken a new block."""
+    engine = make_engine()
+    ids = torch.randint(0, VOCAB, (1, filled + 1), generator=torch.Generator().manual_seed(filled))
+    fresh = engine.new_block_allocator(num_blocks=6, block_size=block_size, attention_mode="direct").new_cache()
+    before = snapshot(fresh)
     with torch.no_grad(), pytest.raises(RuntimeError, match="direct"):
-        engine(torch.randint(0, 96, (1, 5)), cache)
-    assert_cache_untouched(cache, allocator, 8)
-
-
-def test_invalid_attention_mode_rejected():
-    with pytest.raises(ValueError, match="attention_mode"):
-        make_engine().new_block_allocator(num_blocks=4, block_size=4, attention_mode="turbo")
-
-
-def test_device_block_table_mirrors_python_table():
-    engine = make_engine()
-    allocator = engine.new_block_allocator(num_blocks=16, block_size=4)
-    random.Random(1).shuffle(allocator.free_blocks)
-    cache = allocator.new_cache()
-    ids = torch.randint(0, 96, (1, 10))
+        engine(ids, fresh)
+    assert_unchanged(fresh, before)
+    cache = engine.new_block_allocator(num_blocks=6, block_size=block_size).new_cache()
     with torch.no_grad():
-        engine(ids, cache)  # 10 tokens -> 3 blocks
-        for t in range(3):  # crosses into a 4th block
-            engine(ids[:, t : t + 1], cache)
-    assert len(cache.block_table) == 4
-    assert cache.block_table_device[:4].tolist() == cache.block_table
-
-
-def test_forced_direct_moe_preflight_preserves_paged_cache_at_block_boundary():
-    engine = make_engine()
-    allocator = engine.new_block_allocator(num_blocks=4, block_size=4)
-    cache = allocator.new_cache()
-    ids = torch.randint(0, 96, (1, 4))
-    with torch.no_grad():
-        engine(ids, cache)
-    snapshot = (
-        cache.position,
-        list(cache.block_table),
-        sorted(allocator.free_blocks),
-        cache._write_index_key,
-        cache.block_table_device.clone(),
-        allocator.k_pool.clone(),
-        allocator.v_pool.clone(),
-    )
+        engine(ids[:, :filled], cache)
+    before = snapshot(cache)
     engine.set_moe_mode("direct")
     with torch.no_grad(), pytest.raises(RuntimeError, match="direct"):
-        engine(ids[:, :1], cache)  # the next token would open a new block
-    assert cache.position == snapshot[0] and cache.block_table == snapshot[1]
-    assert sorted(allocator.free_blocks) == snapshot[2] and cache._write_index_key == snapshot[3]
-    for now, then in zip((cache.block_table_device, allocator.k_pool, allocator.v_pool), snapshot[4:]):
-        assert torch.equal(now, then)
+        engine(ids[:, filled:], cache)
+    assert_unchanged(cache, before)
+
+
+@pytest.mark.parametrize("mode", ["fast", "", "DIRECT", None])
+def test_unknown_attention_modes_are_refused(mode):
+    with pytest.raises(ValueError, match="attention_mode"):
+        make_engine().new_block_allocator(num_blocks=2, block_size=2, attention_mode=mode)
 
 
 @pytest.mark.parametrize("block_size", [1, 4, 16])
 def test_cpu_paged_cache_matches_oracle_closed_forms(block_size):
     """The product's CPU write/read against the oracle's append_rows/gather_rows."""
-    cfg = ModelConfig(**TINY128)
+    cfg = ModelConfig(**SMALL128)
     allocator = BlockAllocator(cfg, num_blocks=40, block_size=block_size, device="cpu")
     random.Random(block_size).shuffle(allocator.free_blocks)
     cache = PagedKVCache(allocator)
@@ -293,7 +311,7 @@ def test_is_supported_is_false_off_device():
 
 
 def test_contiguous_kvcache_is_a_view():
-    cfg = ModelConfig(**TINY)
+    cfg = ModelConfig(**SMALL)
     cache = KVCache(cfg, 1, "cpu")
     k = torch.randn(1, cfg.num_heads, 3, cfg.head_dim)
     cache.write(0, 2, k, -k)
@@ -366,7 +384,7 @@ def test_decode_plans_are_dropped_when_parameters_can_change():
     """A block's one-token launch plan holds parameter addresses; conversions
     (.to / .float / .double), load_state_dict (copy and assign) and
     drop_decode_plan() forget it, so the next decode token builds a new one."""
-    model = Model(ModelConfig(**TINY)).eval()
+    model = Model(ModelConfig(**SMALL)).eval()
     blocks = list(model.MoEBlocks)
 
     def plant():
@@ -392,7 +410,7 @@ def test_submodule_changes_advance_the_plan_epoch():
     submodule (the block itself is not told)."""
     from moe_engine import model as model_mod
 
-    model = Model(ModelConfig(**TINY)).eval()
+    model = Model(ModelConfig(**SMALL)).eval()
     block = model.MoEBlocks[0]
     for change in (
         lambda: block.moe.float(),
@@ -403,11 +421,11 @@ def test_submodule_changes_advance_the_plan_epoch():
         lambda: block.moe.router.float(),
         lambda: block.moe.experts[1].net[0].float(),
         lambda: block.attn_norm.float(),
-        lambda: setattr(block.attention.out_proj, "weight", torch.nn.Parameter(torch.zeros(32, 32))),
-        lambda: setattr(block.moe_norm, "bias", torch.nn.Parameter(torch.zeros(32))),
+        lambda: setattr(block.attention.out_proj, "weight", torch.nn.Parameter(torch.zeros(WIDTH, WIDTH))),
+        lambda: setattr(block.moe_norm, "bias", torch.nn.Parameter(torch.zeros(WIDTH))),
         # The embedding tables (the first block's plan and a captured decode
         # step read them) and a plan dropped by hand.
-        lambda: setattr(model.positional_embedding, "weight", torch.nn.Parameter(torch.zeros(128, 32))),
+        lambda: setattr(model.positional_embedding, "weight", torch.nn.Parameter(torch.zeros(SMALL["max_seq_length"], WIDTH))),
         lambda: model.token_embedding.float(),
         lambda: model.load_state_dict({k: v.clone() for k, v in model.state_dict().items()}, assign=True),
         lambda: block.drop_decode_plan(),
@@ -434,7 +452,7 @@ def test_mode_and_eps_changes_advance_the_plan_epoch():
     setting the value a module already holds does not."""
     from moe_engine.model import _TENSOR_EPOCH
 
-    model = Model(ModelConfig(**TINY)).eval()
+    model = Model(ModelConfig(**SMALL)).eval()
     block = model.MoEBlocks[0]
     before = _TENSOR_EPOCH[0]
     block.moe.set_mode(block.moe.mode)
@@ -454,7 +472,7 @@ def test_copies_leave_launch_plans_and_steps_behind():
     import ctypes
     import pickle
 
-    model = Model(ModelConfig(**TINY)).eval()
+    model = Model(ModelConfig(**SMALL)).eval()
     model._steps["key"] = (None, (ctypes.c_void_p * 2)(1, 2), [])  # pointers: not copyable themselves
     block = model.MoEBlocks[1]
     block._plans["key"] = ("key", None, None)

@@ -204,6 +204,38 @@ def test_config4_timed_step(out_dtype):
     assert np.array_equal(ref.raw_bits(got.cpu()), ref.raw_bits(again.cpu()))
 
 
+def test_north_star_64_sequences_of_8192_tokens():
+    """The north star's literal shape, 64 x 8192 uniform (bench.py's
+    north_star_64x8192 figure times exactly this step object): one
+    mie_paged_decode_append call puts the missing new rows back bit for bit,
+    and every sequence's float32 output is the oracle's attention over its
+    full 8192-token context within 2e-3; the bf16-output step as well."""
+    from moe_engine import workloads
+
+    print_case("north star 64 x 8192")
+    step = workloads.north_star_step(out_dtype=torch.float32)
+    w = step.w
+    assert w.lens == [8192] * 64 and sum(len(t) for t in w.tables) == 64 * 512
+    part, ws = _native.decode_plan(64, 12, 64, 16, 8192, torch.bfloat16, 0)
+    assert ws == 0 and part >= 8192  # the workgroup form, one launch
+    k_missing, v_missing = w.k_pool.clone(), w.v_pool.clone()
+    got = step.fused().clone()
+    k_full, v_full = w.k_pool.clone(), w.v_pool.clone()
+    for b, table in enumerate(w.tables):  # the step wrote exactly the new rows
+        blk = table[-1]
+        assert torch.equal(k_full[0, blk, :, 15].view(torch.int16), step.k_new[b].view(torch.int16))
+        assert torch.equal(v_full[0, blk, :, 15].view(torch.int16), step.v_new[b].view(torch.int16))
+        k_missing[0, blk, :, 15] = k_full[0, blk, :, 15]
+        v_missing[0, blk, :, 15] = v_full[0, blk, :, 15]
+    assert torch.equal(k_missing.view(torch.int16), k_full.view(torch.int16))
+    assert torch.equal(v_missing.view(torch.int16), v_full.view(torch.int16))
+    del k_missing, v_missing, k_full, v_full
+    want = oracle_outputs(w)
+    np.testing.assert_allclose(got.cpu().numpy(), want, rtol=0, atol=2e-3)
+    step.out = torch.empty(64, 12, 64, dtype=torch.bfloat16, device="cuda")
+    assert bf16_close(step.fused().float().cpu().numpy(), want)
+
+
 def test_config4_unfused_step():
     """bench.py --unfused: the append launch, then the decode launch, leave
     the pools the fused step leaves, and both outputs are the oracle's (the

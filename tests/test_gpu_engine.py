@@ -13,7 +13,7 @@ import torch
 
 from conftest import print_case
 from moe_engine import _native
-from moe_engine.model import Model, ModelConfig
+from moe_engine.model import BlockAllocator, Model, ModelConfig
 
 pytestmark = pytest.mark.gpu
 
@@ -86,6 +86,43 @@ def test_blocks_reused_after_generation():
     second = model.generate(prompt, max_new_tokens=20, temperature=0, cache=cache)
     cache.free()
     assert torch.equal(first, second)
+
+
+def test_device_mirror_follows_the_host_table_through_the_append_launch():
+    """_reserve appends new block ids to the device mirror with one
+    mie_block_table_append launch (ids in its arguments) for up to 16 new
+    blocks, else an indexed copy; either way the mirror's first
+    len(block_table) entries equal the host table, in LIFO order, and
+    entries past it keep what they held."""
+    torch.manual_seed(0)
+    cfg = ModelConfig(**TINY)
+    allocator = BlockAllocator(cfg, num_blocks=64, block_size=4, device="cuda", attention_mode="direct")
+    cache = allocator.new_cache()
+    lib = _native.lib()
+    real = lib.mie_block_table_append
+    launches = []
+
+    def counted(*args):
+        launches.append(args[4])
+        return real(*args)
+
+    lib.mie_block_table_append = counted
+    try:
+        cache._reserve(9)  # 3 blocks: one launch
+        assert cache.block_table == [63, 62, 61] and launches == [3]
+        for n in range(10, 41):  # one new block every 4 tokens
+            cache._reserve(n)
+        assert len(cache.block_table) == 10 and launches == [3] + [1] * 7
+        cache._reserve(40 + 4 * 20)  # 20 new blocks at once: the indexed copy
+        assert len(cache.block_table) == 30 and len(launches) == 8
+    finally:
+        lib.mie_block_table_append = real
+    torch.cuda.synchronize()
+    mirror = cache.block_table_device.cpu().tolist()
+    assert mirror[:30] == cache.block_table == list(range(63, 33, -1))
+    assert mirror[30:] == [0] * 34
+    cache.free()
+    assert cache.block_table == [] and sorted(allocator.free_blocks) == list(range(64))
 
 
 def test_direct_mode_rejects_float64_before_mutating():

@@ -157,3 +157,109 @@ def test_moe_ab_on_the_gpu_decodes_the_same_tokens_both_ways():
         assert rep["summary"]["direct"]["total_decode_steps"] == 10
         assert len(rep["paired_delta_direct_minus_reference"]["per_round_delta_ms"]) == 2
     assert {block.moe.mode for block in model.MoEBlocks} == {"auto"}
+
+
+def test_rounds_rotate_the_systems_and_allocate_in_that_order(monkeypatch):
+    """ab_compare and context_sweep: a warm-up visit, then in round r the
+    systems allocate their caches and run in round_order(systems, r) -
+    rotated by r // 2, reversed in odd rounds; the paired deltas come from
+    the per-round means."""
+    model = Model(ModelConfig(**TINY)).eval()
+    systems = ["contiguous", "paged-gather", "paged-direct"]
+    made, ran = [], []
+    step_ms = {"contiguous": 2.0, "paged-gather": 3.0, "paged-direct": 1.0}
+
+    def fake_cache(m, system, block_size=16):
+        made.append(system)
+        return system
+
+    def fake_cell(m, cache, system, ctx, steps, filler):
+        ran.append((system, ctx))
+        return [step_ms[system] * 1e-3] * steps
+
+    monkeypatch.setattr(harness, "make_cache", fake_cache)
+    monkeypatch.setattr(harness, "_sweep_cell", fake_cell)
+    rep = harness.context_sweep(model, contexts=(16, 24), systems=systems, rounds=3, steps=2)
+    visits = [made[i:i + 3] for i in range(0, len(made), 3)]
+    assert visits[0] == systems  # warm-up
+    a, b, c = systems
+    # rounds 0, 1, 2, each at contexts 16 and 24
+    assert visits[1:] == [[a, b, c], [a, b, c], [c, b, a], [c, b, a], [b, c, a], [b, c, a]]
+    assert [s for s, _ in ran] == made
+    assert rep["median_step_ms"]["paged-direct"] == {16: 1.0, 24: 1.0}
+    d = rep["paired_deltas"][24]["paged-direct_minus_contiguous"]
+    assert d["mean_delta_ms"] == pytest.approx(-1.0) and d["ci95_ms"] == pytest.approx([-1.0, -1.0])
+    assert not rep["placement_sampled"]  # no pad on the CPU
+
+    made.clear()
+
+    def fake_round(m, cache, prompt_ids, new_tokens, warm_steps=0):
+        assert warm_steps == 1
+        return 0.1, [step_ms[cache] * 1e-3] * new_tokens, [5] * (new_tokens + 1)
+
+    monkeypatch.setattr(harness, "run_round", fake_round)
+    rep = harness.ab_compare(model, torch.zeros(3, dtype=torch.long), systems, rounds=4, new_tokens=3)
+    assert made[:3] == systems and made[3:6] == systems and made[6:9] == systems[::-1]
+    assert made[9:12] == systems[1:] + systems[:1] and made[12:15] == (systems[1:] + systems[:1])[::-1]
+    assert rep["paired_deltas"]["paged-gather_minus_contiguous"]["mean_delta_ms"] == pytest.approx(1.0)
+    assert rep["tokens_identical"] and rep["rounds"] == 4
+
+
+def test_round_order_runs_every_pair_both_ways():
+    systems = list(harness.SWEEP_SYSTEMS)
+    for x in systems:
+        for y in systems:
+            if x != y:
+                before = [o.index(x) < o.index(y) for o in (harness.round_order(systems, r) for r in range(12))]
+                assert sum(before) == 6
+    assert {harness.round_order(systems, r)[0] for r in range(0, 12, 2)} == set(systems)
+
+
+def test_fresh_placement_takes_no_pad_off_the_gpu():
+    import random
+
+    assert harness.fresh_placement(random.Random(0), "cpu") is None
+
+
+@pytest.mark.gpu
+def test_context_sweep_and_attention_micro_on_the_gpu():
+    """The sweep and the micro on a small model with every system: each round
+    places the caches afresh (a pad is taken), graph systems capture again,
+    and the report has a median for every (system, context) and the
+    paging-cost intervals at every context."""
+    cfg = dict(max_seq_length=64, vocab_size=512, num_layers=2, hidden_dim=64, num_heads=4, num_experts=4, top_k=2)
+    model = harness.make_model(cfg, device="cuda")
+    rep = harness.context_sweep(model, contexts=(16, 40, 64), rounds=3, steps=4, filler=7)
+    assert rep["placement_sampled"] and rep["rounds"] == 3
+    for system in harness.SWEEP_SYSTEMS:
+        assert set(rep["median_step_ms"][system]) == {16, 40, 64}
+        assert all(v > 0 for v in rep["median_step_ms"][system].values())
+    for ctx in (16, 40, 64):
+        cost = rep["paging_cost_ms"][ctx]
+        assert set(cost) == {"paged-direct_minus_contiguous-direct",
+                             "paged-direct-graph_minus_contiguous-direct-graph"}
+        assert all(c["ci95_ms"][0] <= c["mean_delta_ms"] <= c["ci95_ms"][1] for c in cost.values())
+    micro = harness.attention_micro(cfg, contexts=(16, 64), rounds=2, iters=10)
+    for ctx in (16, 64):
+        row = micro[ctx]
+        assert set(harness.MICRO_VARIANTS) <= set(row)
+        assert row["paged_direct_device_us"] > 0 and row["contiguous_direct_device_us"] > 0
+        assert "paging_cost_device_us" in row and "paging_cost_host_launched_us" in row
+
+
+@pytest.mark.gpu
+def test_graph_ab_round_captures_again_and_matches_eager_tokens():
+    """ab_compare with placement: every round allocates fresh caches and each
+    graph system captures its step again; the graphed, eager, paged and
+    contiguous-layout systems all choose the same greedy tokens."""
+    cfg = dict(max_seq_length=96, vocab_size=512, num_layers=2, hidden_dim=64, num_heads=4, num_experts=4, top_k=2)
+    model = harness.make_model(cfg, device="cuda")
+    prompt = torch.randint(0, cfg["vocab_size"], (7,), generator=torch.Generator().manual_seed(5)).cuda()
+    systems = ("paged-direct", harness.CONTIGUOUS_DIRECT, harness.GRAPH_SYSTEM, harness.CONTIGUOUS_DIRECT_GRAPH)
+    rep = harness.ab_compare(model, prompt, systems, rounds=3, new_tokens=20)
+    assert rep["tokens_identical"] and rep["placement_sampled"]
+    assert len(rep["tokens"]) == 21
+    for a, b in harness.PAGING_COST_PAIRS:
+        assert len(rep["paired_deltas"][f"{a}_minus_{b}"]["per_round_delta_ms"]) == 3
+    want = model.generate(prompt, 21, temperature=0)[0, len(prompt):].tolist()
+    assert rep["tokens"] == want
