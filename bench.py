@@ -38,7 +38,7 @@ sys.path.insert(0, str(ROOT / "moe-inference-engine_amd"))
 
 METRIC = "paged-decode attention HBM GB/s (% of peak) + per-token decode latency ms"
 PEAK_HBM_GBS = 8000.0  # MI355X HBM3E
-SECONDARY_NAMES = ("launch_floor", "north_star_64x8192", "config2_single_layer", "config3_append_gather",
+SECONDARY_NAMES = ("launch_floor", "round_latency", "north_star_64x8192", "config2_single_layer", "config3_append_gather",
                    "config5_long_context", "fused_moe_decode", "config1_e2e_decode", "config1_context_sweep",
                    "config1_attention_micro", "config1_bf16_decode")
 TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_config4_traffic.json"
@@ -493,6 +493,75 @@ def secondary_launch_floor(torch):
             "note": "empty kernel, 256 workgroups x 256 threads; 64 calls per graph, device time per call"}
 
 
+def secondary_round_latency(torch, calls=64, reps=7):
+    """One dependent memory round on this box, measured with product kernels
+    replayed from HIP graphs of `calls` launches each: the empty kernel
+    (mie_empty_launch, one workgroup), mie_argmax over 64 floats (one round:
+    the row, then a reduction and a store) and mie_embed of one token (two
+    rounds: the token id, then its table row).  Each call reads its own
+    rows, 1 MiB apart; `cold` replays follow a 1 GiB fill that evicts the
+    L2s and the last-level cache, `warm` replays repeat without it.  The
+    differences argmax - empty and embed - argmax each estimate one round."""
+    from moe_engine import _native
+
+    lib = _native.lib()
+    dev = "cuda"
+    vocab, dim = 8192, 768
+    gen = torch.Generator().manual_seed(0)
+    tok = torch.randn(vocab, dim, generator=gen).to(dev)
+    pos = torch.randn(16, dim, generator=gen).to(dev)
+    ids = torch.zeros(calls, 64, dtype=torch.int64)
+    ids[:, 0] = torch.randperm(vocab, generator=gen)[:calls]
+    ids = ids.to(dev)  # one id per 512-byte line
+    out = torch.empty(calls, dim, device=dev)
+    rows = torch.randn(calls, 1 << 18, generator=gen).to(dev)
+    picks = torch.empty(calls, 8, dtype=torch.int64, device=dev)
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+
+    def run(rc, what):
+        if rc:
+            raise RuntimeError(f"{what} failed: {lib.mie_last_error()}")
+
+    kinds = {
+        "empty": lambda i, st: run(lib.mie_empty_launch(1, st), "mie_empty_launch"),
+        "argmax": lambda i, st: run(lib.mie_argmax(rows[i].data_ptr(), 64, picks[i].data_ptr(), 0, st), "mie_argmax"),
+        "embed": lambda i, st: run(lib.mie_embed(ids[i].data_ptr(), None, i % 16, 1, tok.data_ptr(), vocab,
+                                                 pos.data_ptr(), 16, dim, out[i].data_ptr(), 0, st), "mie_embed"),
+    }
+    res = {}
+    for name, fn in kinds.items():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(calls):
+                fn(i, side.cuda_stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(calls):
+                fn(i, side.cuda_stream)
+        for mode in ("cold", "warm"):
+            times = []
+            for r in range(reps):
+                if mode == "cold":
+                    flush.fill_(r & 0xFF)
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                graph.replay()
+                stop.record()
+                torch.cuda.synchronize()
+                times.append(start.elapsed_time(stop) * 1e3 / calls)
+            res[f"{name}_{mode}_us"] = round(statistics.median(times), 3)
+        del graph
+    for mode in ("cold", "warm"):
+        res[f"first_round_{mode}_us"] = round(res[f"argmax_{mode}_us"] - res[f"empty_{mode}_us"], 3)
+        res[f"second_round_{mode}_us"] = round(res[f"embed_{mode}_us"] - res[f"argmax_{mode}_us"], 3)
+    res["note"] = ("device time per call, 64 calls per graph (median of 7 replays); each call reads its own rows; "
+                   "cold replays follow a 1 GiB fill")
+    del flush, rows, tok
+    return res
+
+
 def add_floor_fractions(secondary):
     """Latency-bound figures as fractions of the launch floor (floor / time:
     1.0 would be a call that costs no more than its empty launches) next to
@@ -677,6 +746,7 @@ def main():
         chosen = [n for n in args.secondary.split(",") if n] or list(SECONDARY_NAMES)
         for name, fn in (
             ("launch_floor", secondary_launch_floor),
+            ("round_latency", secondary_round_latency),
             ("north_star_64x8192", secondary_north_star),
             ("config2_single_layer", secondary_config2),
             ("config3_append_gather", secondary_config3),

@@ -64,6 +64,10 @@ constexpr int kWindow = 64;          // FAST path: block ids held one per lane
 // second bounds the merge work per (sequence, head).
 constexpr int kTargetItems = 3072;  // auto plan: wavefronts to stay below
 constexpr int kMaxParts = 256;       // auto plan: partitions per sequence to stay below
+// Merge of split contexts: float4 columns of a head per reduce workgroup (8:
+// two workgroups per head at head_dim 64), so each thread holds the partials
+// of at most 8 partitions in registers per 256 partitions.
+constexpr int RW_COLS = 8;
 // Occupancy floor for the main kernels: every built shape fits 4 waves/SIMD
 // (<= 128 VGPRs) without spills; at 3 waves/SIMD config 4 runs ~8 % slower.
 constexpr int kMinWaves = 4;
@@ -705,65 +709,103 @@ void paged_decode_wg_kernel(DecodeArgs a, WgOrder order) {
 // are independent; the PL states of a column are then merged through LDS.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void paged_decode_reduce_kernel(DecodeArgs a) {
+  // One workgroup per (sequence, head, chunk of RW_COLS float4 columns).
+  // Every thread first issues all of its loads - its partition's (m, l) and
+  // the acc columns of RW_NPT partitions - in one memory round, before the
+  // sequence's length is known (a device length is one more load, issued
+  // beside them), and only then joins the workgroup-wide max: the merge
+  // waits on one round trip, not on a chain of them.  Partitions past the
+  // sequence's last (up to the launch's bound, max_parts) are read and
+  // dropped with selects, so neither stale workspace nor a NaN partial (a
+  // bad block id) reaches the output except through its own weight.  More
+  // than 256 partitions (a caller-chosen partition size) are taken 256 at a
+  // time with the running sums rescaled.
   constexpr int COLS = D / 4;
-  constexpr int PL = 256 / COLS;
-  __shared__ float s_m[256], s_l[256];
-  __shared__ float4 s_acc[256];
-  const int h = blockIdx.x;
+  constexpr int CW = RW_COLS < COLS ? RW_COLS : COLS;  // float4 columns per workgroup
+  constexpr int PL = 256 / CW;                         // partition lanes
+  constexpr int NPT = 256 / PL;                        // partitions per thread per 256
+  __shared__ float s_max[4], s_sum[4];
+  __shared__ float s_w[256];
+  __shared__ float4 s_o[4][CW];
+  const int h = blockIdx.x / (COLS / CW);
+  const int chunk = blockIdx.x % (COLS / CW);
   const int b = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int c = tid % CW, g = tid / CW;
+  const int64_t base = (static_cast<int64_t>(b) * a.H + h) * a.max_parts;
+  const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + base;
+  const float* accs = a.ws_acc + base * D + (chunk * CW + c) * 4;
+  const int last = a.max_parts - 1;
+
+  float2 mlv = ml[min(tid, last)];
+  float4 av[NPT];
+#pragma unroll
+  for (int i = 0; i < NPT; ++i) av[i] = *reinterpret_cast<const float4*>(accs + static_cast<int64_t>(min(g + i * PL, last)) * D);
   const int ctx = seq_ctx(a, b);
   const int nparts = (ctx + (1 << a.part_shift) - 1) >> a.part_shift;
-  if (nparts <= 1) return;
-  const int tid = threadIdx.x;
-  const int col = tid % COLS;
-  const int pl = tid / COLS;
-  const int64_t base = (static_cast<int64_t>(b) * a.H + h) * a.max_parts;
-  const float* ml = a.ws_ml + 2 * base;
-  const float* accs = a.ws_acc + base * D + col * 4;
+  // A sequence of one partition (its output is already written) takes the
+  // same path with every partition masked and stores nothing: no branch on
+  // the length stands between the loads above and their issue.
+  const bool merge = nparts > 1;
 
-  float m = -INFINITY, l = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (pl < PL) {
-#pragma unroll 4
-    for (int i = pl; i < nparts; i += PL) {
-      const float mi = ml[2 * i];
-      const float li = ml[2 * i + 1];
-      const float4 ai = *reinterpret_cast<const float4*>(accs + static_cast<int64_t>(i) * D);
-      const float mn = fmaxf(m, mi);
-      const float mr = mn == -INFINITY ? 0.f : mn;
-      const float ca = mie::fast_exp2(m - mr);
-      const float cb = mie::fast_exp2(mi - mr);
-      l = l * ca + li * cb;
-      acc.x = acc.x * ca + ai.x * cb;
-      acc.y = acc.y * ca + ai.y * cb;
-      acc.z = acc.z * ca + ai.z * cb;
-      acc.w = acc.w * ca + ai.w * cb;
-      m = mn;
-    }
-  }
-  s_m[tid] = m;
-  s_l[tid] = l;
-  s_acc[tid] = acc;
-  __syncthreads();
-  if (tid >= COLS) return;
-  float mx = -INFINITY;
-  for (int r = 0; r < PL; ++r) mx = fmaxf(mx, s_m[r * COLS + tid]);
-  const float mr = mx == -INFINITY ? 0.f : mx;
-  float lt = 0.f;
-  float o[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < PL; ++r) {
-    const float w = mie::fast_exp2(s_m[r * COLS + tid] - mr);
-    const float4 v = s_acc[r * COLS + tid];
-    lt += s_l[r * COLS + tid] * w;
-    o[0] += v.x * w;
-    o[1] += v.y * w;
-    o[2] += v.z * w;
-    o[3] += v.w * w;
-  }
-  const float inv = 1.f / lt;
+  float M = -INFINITY, L = 0.f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int p0 = 0;;) {
+    const bool mine = p0 + tid < nparts;
+    const float mt = mine ? mlv.x : -INFINITY;
+    const float wmax = mie::wave_max(mt);
+    if (lane == 0) s_max[wave] = wmax;
+    __syncthreads();
+    const float mn = fmaxf(M, fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3])));
+    const float mr = mn == -INFINITY ? 0.f : mn;
+    const float keep = mie::fast_exp2(M - mr);  // 0 for the first 256
+    const float w = mine ? mie::fast_exp2(mt - mr) : 0.f;
+    s_w[tid] = w;
+    const float lsum = mie::wave_sum(mine ? mlv.y * w : 0.f);
+    if (lane == 0) s_sum[wave] = lsum;
+    __syncthreads();
+    L = L * keep + ((s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]));
+    o.x *= keep;
+    o.y *= keep;
+    o.z *= keep;
+    o.w *= keep;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] *= inv;
-  store_out<DT, 4>(a.out, b * a.o_sb + h * a.o_sh + tid * 4, o, a.out_f32);
+    for (int i = 0; i < NPT; ++i) {
+      const int q = g + i * PL;
+      const bool in = p0 + q < nparts;
+      const float wi = s_w[q];
+      o.x = in ? fmaf(wi, av[i].x, o.x) : o.x;
+      o.y = in ? fmaf(wi, av[i].y, o.y) : o.y;
+      o.z = in ? fmaf(wi, av[i].z, o.z) : o.z;
+      o.w = in ? fmaf(wi, av[i].w, o.w) : o.w;
+    }
+    M = mn;
+    p0 += 256;
+    if (p0 >= nparts) break;
+    __syncthreads();  // s_max, s_sum and s_w are rewritten by the next 256
+    mlv = ml[min(p0 + tid, last)];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+      av[i] = *reinterpret_cast<const float4*>(accs + static_cast<int64_t>(min(p0 + g + i * PL, last)) * D);
+  }
+  // Sum over the partition lanes: lanes c, c + CW, ... of a wave hold the
+  // same columns, then the four waves through LDS.
+#pragma unroll
+  for (int off = CW; off < 64; off <<= 1) {
+    o.x += __shfl_xor(o.x, off);
+    o.y += __shfl_xor(o.y, off);
+    o.z += __shfl_xor(o.z, off);
+    o.w += __shfl_xor(o.w, off);
+  }
+  if (lane < CW) s_o[wave][lane] = o;
+  __syncthreads();
+  if (tid >= CW || !merge) return;
+  const float4 v0 = s_o[0][tid], v1 = s_o[1][tid], v2 = s_o[2][tid], v3 = s_o[3][tid];
+  const float inv = 1.f / L;
+  float r[4] = {((v0.x + v1.x) + (v2.x + v3.x)) * inv, ((v0.y + v1.y) + (v2.y + v3.y)) * inv,
+                ((v0.z + v1.z) + (v2.z + v3.z)) * inv, ((v0.w + v1.w) + (v2.w + v3.w)) * inv};
+  store_out<DT, 4>(a.out, b * a.o_sb + h * a.o_sh + (chunk * CW + c) * 4, r, a.out_f32);
 }
 
 // ---- host side --------------------------------------------------------------
@@ -904,7 +946,9 @@ int32_t launch(DecodeArgs& a, int batch, bool fast, bool wg, const WgOrder& orde
   }
   int32_t rc = mie::check_launch("paged_decode_kernel");
   if (rc != MIE_OK || a.max_parts <= 1) return rc;
-  paged_decode_reduce_kernel<DT, D><<<dim3(a.H, batch), 256, 0, st>>>(a);
+  constexpr int kCols = D / 4;
+  constexpr int kChunks = kCols / (RW_COLS < kCols ? RW_COLS : kCols);
+  paged_decode_reduce_kernel<DT, D><<<dim3(a.H * kChunks, batch), 256, 0, st>>>(a);
   return mie::check_launch("paged_decode_reduce_kernel");
 }
 

@@ -628,7 +628,17 @@ def main(argv=None):
     parser.add_argument("--systems", default=None,
                         help="any of " + ", ".join(ALL_SYSTEMS) + " (moe-ab: one eager system, default contiguous)")
     parser.add_argument("--device", default="cuda")
+    parser.add_argument("--copy-calibration-mib", type=int, default=0,
+                        help="first run 10 plain device copies of this many MiB (each reads and writes that many "
+                        "bytes), to scale hardware byte counters against a kernel of known traffic")
     args = parser.parse_args(argv)
+    if args.copy_calibration_mib > 0:
+        src = torch.ones(args.copy_calibration_mib << 18, dtype=torch.float32, device=args.device)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        sync(args.device)
+        del src, dst
     contexts = [int(c) for c in args.contexts.split(",")]
     default_systems = {"moe-ab": "contiguous", "sweep": ",".join(SWEEP_SYSTEMS)}.get(args.mode, ",".join(SYSTEMS))
     systems = (args.systems or default_systems).split(",")

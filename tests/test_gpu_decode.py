@@ -71,9 +71,11 @@ def test_kernel_matches_oracle_production_shape(context_len):
 @pytest.mark.parametrize("context_len", [17, 190])
 def test_kernel_handles_noncontiguous_blocks(context_len):
     print_case("noncontiguous", context_len)
-    cache, written = filled_cache(PROD, context_len, 16, shuffle=True)
+    cache, written = filled_cache(PROD, context_len, 16, shuffle=True, seed=5)
     table = cache.block_table
-    assert any(b != a + 1 for a, b in zip(table, table[1:])), "table accidentally contiguous"
+    # The shuffled pool must really scatter the context: some two logical
+    # neighbours are not neighbours in the pool.
+    assert any(abs(b - a) != 1 for a, b in zip(table, table[1:]))
     q = torch.randn(1, 8, 1, 96, generator=torch.Generator().manual_seed(1))
     got = paged_attention.decode(q.cuda(), cache, 0, context_len)
     np.testing.assert_allclose(got[0, :, 0].cpu().numpy(), oracle(q, written[0]), rtol=0, atol=1e-5)
