@@ -130,19 +130,12 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   const int g = lane / LPT;          // row within a wave load
   const int c4 = (lane % LPT) * 4;   // this lane's 4 columns of a row
 
-  // First memory round, all loads independent: this workgroup's W_out rows, q, the block
-  // table up to the host's bound (nblk_max entries, at most 1024 = 4 per
-  // thread), and the live length.
-  typename M::raw4 wv[kRowSteps];
-  const int row0 = rblk * a.rows_per_block;
-  const int row_end = min(a.dim, row0 + a.rows_per_block);
-#pragma unroll
-  for (int s = 0; s < kRowSteps; ++s) {
-    int row = row0 + (s * kWaves + wave) * TPL + g;
-    row = row < row_end ? row : row0;  // in bounds; the product is dropped below
-    wv[s] = M::stream_raw(static_cast<const T*>(a.w) + static_cast<int64_t>(row) * a.dim + h * D + c4);
-  }
-  const typename M::raw4 qraw = M::load_raw(static_cast<const T*>(a.q) + h * D + c4);
+  // First memory round, all loads independent: the block table up to the
+  // host's bound (nblk_max entries, at most 1024 = 4 per thread) and the live
+  // length, then q and this workgroup's W_out rows.  Vector loads complete in
+  // issue order, so the table goes first: the K/V round waits only for it (an
+  // L2 hit), while the W_out rows (from HBM) stay in flight until the
+  // projection.
   constexpr int kTablePerThread = kMaxTable / 256;
   int tb[kTablePerThread];
 #pragma unroll
@@ -152,6 +145,16 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
     tb[u] = u * 256 < a.nblk_max ? a.bt[ic] : 0;
   }
   int ctx = a.ctx_dev ? *a.ctx_dev : a.ctx;
+  const typename M::raw4 qraw = M::load_raw(static_cast<const T*>(a.q) + h * D + c4);
+  typename M::raw4 wv[kRowSteps];
+  const int row0 = rblk * a.rows_per_block;
+  const int row_end = min(a.dim, row0 + a.rows_per_block);
+#pragma unroll
+  for (int s = 0; s < kRowSteps; ++s) {
+    int row = row0 + (s * kWaves + wave) * TPL + g;
+    row = row < row_end ? row : row0;  // in bounds; the product is dropped below
+    wv[s] = M::stream_raw(static_cast<const T*>(a.w) + static_cast<int64_t>(row) * a.dim + h * D + c4);
+  }
   ctx = ctx < 0 ? 0 : (ctx > a.max_ctx ? a.max_ctx : ctx);
   const int nblk = static_cast<int>(a.bs.div(static_cast<uint32_t>(ctx + a.bs.d - 1)));  // <= nblk_max
   int bad = 0;
@@ -191,6 +194,11 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       kv[b] = M::load_raw(kh + off);
       vv[b] = M::load_raw(vh + off);
     }
+    // Every K and V load of the round is issued before the first score: the
+    // scheduler would otherwise reuse load registers and start later loads
+    // only after earlier ones returned.  One 4-wave workgroup per CU, so the
+    // registers this holds cost no occupancy.
+    __builtin_amdgcn_sched_barrier(0);
     float sc[kBatch];
     float mb = m;
 #pragma unroll
@@ -199,18 +207,19 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       sc[b] = valid[b] ? sc[b] : -INFINITY;
       mb = fmaxf(mb, sc[b]);
     }
-    if (mb != -INFINITY) {
-      const float alpha = m == -INFINITY ? 0.f : mie::fast_exp2(m - mb);
-      l *= alpha;
-      o *= alpha;
+    // Branch-free, so that the V loads issue beside the K loads instead of
+    // after the scores: a batch with no valid row leaves mb = m = -inf, every
+    // p = 0 and alpha = 0 on a state that is still empty.
+    const float alpha = m == -INFINITY ? 0.f : mie::fast_exp2(m - mb);
+    l *= alpha;
+    o *= alpha;
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b) {
-        const float p = valid[b] ? mie::fast_exp2(sc[b] - mb) : 0.f;
-        l += p;
-        o += p * M::widen(vv[b]);
-      }
-      m = mb;
+    for (int b = 0; b < kBatch; ++b) {
+      const float p = valid[b] ? mie::fast_exp2(sc[b] - mb) : 0.f;
+      l += p;
+      o += p * M::widen(vv[b]);
     }
+    m = mb;
   }
   // Merge the TPL row groups of the wave (lanes g * LPT + c hold the same
   // columns for every g), then the four waves through LDS.
