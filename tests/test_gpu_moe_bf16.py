@@ -216,3 +216,46 @@ def test_bf16_model_decodes_through_the_fused_moe(seed):
     decided = len(rows) if len(near) == 0 else int(near[0])
     n = 12 + decided
     assert torch.equal(fused[:, :n], reference[:, :n]), f"tokens part before step {decided}"
+
+
+def test_bf16_config1_shape_tokens_follow_the_pytorch_moe():
+    """BASELINE config 1's model in bfloat16 (seed 0, 12 layers, d 768,
+    12 x 64, top-2 of 8, FFN 2048, vocab 50257) on a paged-direct cache:
+    under MoE mode 'auto' the decode takes the HIP MoE, where the reference's
+    'auto' would take the PyTorch MoE for bfloat16.  The greedy tokens of the
+    two must agree up to the first step whose top two logits (teacher-forced
+    on the PyTorch MoE's sequence) lie within 4 bfloat16 ulps."""
+    from moe_engine.harness import CONFIG1
+
+    print_case("bf16 config1 shape")
+    model = _bf16_model(0, CONFIG1)
+    prompt = torch.randint(0, CONFIG1["vocab_size"], (32,), generator=torch.Generator().manual_seed(0)).cuda()
+    alloc = model.new_block_allocator(num_blocks=64, block_size=16, attention_mode="direct")
+    n = 24
+
+    def greedy(mode):
+        model.set_moe_mode(mode)
+        cache = alloc.new_cache()
+        try:
+            return model.generate(prompt, n, temperature=0, cache=cache)
+        finally:
+            cache.free()
+
+    try:
+        fused = greedy("auto")
+        reference = greedy("reference")
+        with torch.no_grad():
+            cache = alloc.new_cache()
+            rows = [model(reference[:, :32], cache)[0, -1]]
+            for t in range(32, reference.shape[1] - 1):
+                rows.append(model(reference[:, t : t + 1], cache)[0, -1])
+            cache.free()
+    finally:
+        model.set_moe_mode("auto")
+    logits = torch.stack(rows).float()
+    top2 = logits.topk(2, dim=-1).values
+    near = ((top2[:, 0] - top2[:, 1]) <= 4 * 2.0**-7 * top2[:, 0].abs().clamp(min=1.0)).nonzero()
+    decided = len(rows) if len(near) == 0 else int(near[0])
+    assert decided > 0, "the first step is already a near-tie"
+    m = 32 + decided
+    assert torch.equal(fused[:, :m], reference[:, :m]), f"tokens part before step {decided}"
