@@ -231,78 +231,95 @@ __global__ __launch_bounds__(256) void moe_w1_gelu_kernel(MoeArgs a) {
   const int dim = a.dim;
   const int e0 = wave, e1 = wave + 4;
 
-  // 1. All global reads that do not depend on the routing, kept as loaded
-  //    and widened after the last one is issued.
+  // 1. All global reads that do not depend on the routing, in one memory
+  //    round.  The vectors every wave needs - x (with the attention's sums
+  //    and out_proj's bias, h) and the norm's weight and bias - are read
+  //    once per workgroup: wave w reads chunks w, w + 4, ... of them, forms h
+  //    there and leaves the three chunks in LDS, where every wave picks up the
+  //    whole vectors in its own lane layout after the barrier.  Each wave's
+  //    two router rows go out after its share, so waiting for the share does
+  //    not wait for them.
+  __shared__ __align__(16) float s_vec[3][kMaxDim];  // h, norm weight, norm bias
   f32x4_t y[NCH], gw[NCH], gb[NCH], q0[NCH], q1[NCH];
-  {
-    typename M::raw4 ry[NCH], rgw[NCH], rgb[NCH], rq0[NCH], rq1[NCH];
-    const typename M::raw4 zr = M::zero_raw();
+  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+  constexpr int NS = (NCH + 3) / 4;  // chunks of the shared vectors per wave
+  constexpr int NA = ACC ? NS : 1;
+  typename M::raw4 ry[NS], rgw[NS], rgb[NS], bo[NA];
+  i64x2_t acc_lo[NA], acc_hi[NA];
+  long long acc_flag = 0;
+  const typename M::raw4 zr = M::zero_raw();
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      const int i = c * 256 + lane * 4;
-      const bool valid = i < dim;
-      ry[c] = valid ? M::load_raw(xs + i) : zr;
-      rgw[c] = NORM && valid ? M::load_raw(ln_w + i) : zr;
-      rgb[c] = NORM && valid && ln_b ? M::load_raw(ln_b + i) : zr;
-      rq0[c] = valid && e0 < a.E ? M::load_raw(router + static_cast<int64_t>(e0) * dim + i) : zr;
-      rq1[c] = valid && e1 < a.E ? M::load_raw(router + static_cast<int64_t>(e1) * dim + i) : zr;
-    }
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-      y[c] = M::widen(ry[c]);
-      gw[c] = M::widen(rgw[c]);
-      gb[c] = M::widen(rgb[c]);
-      q0[c] = M::widen(rq0[c]);
-      q1[c] = M::widen(rq1[c]);
+  for (int u = 0; u < NS; ++u) {
+    const int c = wave + 4 * u;
+    const int i = c * 256 + lane * 4;
+    const int ic = c < NCH && i < dim ? i : 0;  // in bounds; dropped below
+    ry[u] = M::load_raw(xs + ic);
+    rgw[u] = NORM ? M::load_raw(ln_w + ic) : zr;
+    // Without a norm bias the weight is read in its place (a valid address,
+    // so no branch splits the round) and the value is dropped below.
+    rgb[u] = NORM ? M::load_raw((ln_b ? ln_b : ln_w) + ic) : zr;
+    if constexpr (ACC) {
+      bo[u] = M::load_raw((a.b_out ? static_cast<const T*>(a.b_out) : xs) + ic);
+      acc_lo[u] = *reinterpret_cast<const i64x2_t*>(a.acc + ic);
+      acc_hi[u] = *reinterpret_cast<const i64x2_t*>(a.acc + ic + 2);
     }
   }
-  const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
-  // Accumulator form: the fixed-point sums, the output projection's bias and
-  // the flag, loaded with the rest (unconditionally: lanes past dim re-read
-  // element 0 and drop it), so they add no memory round.
-  constexpr int NA = ACC ? NCH : 1;
-  i64x2_t acc_lo[NA], acc_hi[NA];
-  typename M::raw4 bo[NA];
-  long long acc_flag = 0;
-  if constexpr (ACC) {
-    const T* bsrc = a.b_out ? static_cast<const T*>(a.b_out) : xs;
+  if constexpr (ACC) acc_flag = *reinterpret_cast<const long long*>(a.acc + dim);
+  {
+    typename M::raw4 rq0[NCH], rq1[NCH];
+    // Rows past E and columns past dim read row 0, column 0 (in bounds) and
+    // are zeroed once loaded: a load under a branch would make the wave wait
+    // for every load issued before it at the join.
+    const int r0 = e0 < a.E ? e0 : 0, r1 = e1 < a.E ? e1 : 0;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       const int i = c * 256 + lane * 4;
       const int ic = i < dim ? i : 0;
-      bo[c] = M::load_raw(bsrc + ic);
-      acc_lo[c] = *reinterpret_cast<const i64x2_t*>(a.acc + ic);
-      acc_hi[c] = *reinterpret_cast<const i64x2_t*>(a.acc + ic + 2);
+      rq0[c] = M::load_raw(router + static_cast<int64_t>(r0) * dim + ic);
+      rq1[c] = M::load_raw(router + static_cast<int64_t>(r1) * dim + ic);
     }
-    acc_flag = *reinterpret_cast<const long long*>(a.acc + dim);
     // Keep the scheduler from sinking any of these loads below the first use
     // of the ones before them (which would cost a memory round).
     __builtin_amdgcn_sched_barrier(0);
-  }
-  if constexpr (ACC) {
-    // h = x + (acc * 2^-32 + b_out): the attention output projection summed
-    // over heads in fixed point (int64 -> float is one rounding, the power of
-    // two scale is exact), its bias, then the residual - the rounding points
-    // of x + out_proj(a): the projection's output, then the sum, each rounded
-    // to the storage type.
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
-      const int i = c * 256 + lane * 4;
-      f32x4_t o = {static_cast<float>(acc_lo[c].x), static_cast<float>(acc_lo[c].y),
-                   static_cast<float>(acc_hi[c].x), static_cast<float>(acc_hi[c].y)};
-      o *= 2.3283064365386963e-10f;  // 2^-32
-      if (a.b_out) o += M::widen(bo[c]);
-      f32x4_t hv = M::R4(y[c] + M::R4(o));
-      if (acc_flag != 0) hv = f32x4_t{NAN, NAN, NAN, NAN};
-      y[c] = i < dim ? hv : zero;
+      const bool valid = c * 256 + lane * 4 < dim;
+      q0[c] = valid && e0 < a.E ? M::widen(rq0[c]) : zero;
+      q1[c] = valid && e1 < a.E ? M::widen(rq1[c]) : zero;
     }
-    if (blockIdx.x == 0 && blockIdx.y == 0 && wave == 0) {
+  }
+  // h = x + (acc * 2^-32 + b_out) in the accumulator form: the attention
+  // output projection summed over heads in fixed point (int64 -> float is one
+  // rounding, the power of two scale is exact), its bias, then the residual -
+  // the rounding points of x + out_proj(a): the projection's output, then the
+  // sum, each rounded to the storage type.  Otherwise h = x.
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) {
-        const int i = c * 256 + lane * 4;
-        if (i < dim) M::put4(static_cast<T*>(a.h_out) + i, y[c]);
-      }
+  for (int u = 0; u < NS; ++u) {
+    const int c = wave + 4 * u;
+    if (c >= NCH) continue;
+    const int i = c * 256 + lane * 4;
+    f32x4_t hv = M::widen(ry[u]);
+    if constexpr (ACC) {
+      f32x4_t o = {static_cast<float>(acc_lo[u].x), static_cast<float>(acc_lo[u].y),
+                   static_cast<float>(acc_hi[u].x), static_cast<float>(acc_hi[u].y)};
+      o *= 2.3283064365386963e-10f;  // 2^-32
+      if (a.b_out) o += M::widen(bo[u]);
+      hv = M::R4(hv + M::R4(o));
+      if (acc_flag != 0) hv = f32x4_t{NAN, NAN, NAN, NAN};
+      if (blockIdx.x == 0 && blockIdx.y == 0 && i < dim) M::put4(static_cast<T*>(a.h_out) + i, hv);
     }
+    const bool valid = i < dim;
+    *reinterpret_cast<f32x4_t*>(&s_vec[0][i]) = valid ? hv : zero;
+    *reinterpret_cast<f32x4_t*>(&s_vec[1][i]) = valid ? M::widen(rgw[u]) : zero;
+    *reinterpret_cast<f32x4_t*>(&s_vec[2][i]) = valid && ln_b ? M::widen(rgb[u]) : zero;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int i = c * 256 + lane * 4;
+    y[c] = *reinterpret_cast<const f32x4_t*>(&s_vec[0][i]);
+    gw[c] = *reinterpret_cast<const f32x4_t*>(&s_vec[1][i]);
+    gb[c] = *reinterpret_cast<const f32x4_t*>(&s_vec[2][i]);
   }
 
   // 2. The block's LayerNorm (float32, biased variance), per wave.
