@@ -348,6 +348,14 @@ def secondary_config3(torch):
             tables.append(t)
         cold = [lambda l=l, t=t: kv_ops.gather(k_pool, v_pool, l, t, C, outk, outv) for t in tables for l in range(L)]
         gather_cold = graph_replay_us(torch, cold)
+        # Copy ceiling: the same bytes moved by the runtime's device-to-device
+        # copy (read gb / 2, write gb / 2) from 12 distinct sources into one
+        # destination, as the 12 layers' gathers read 12 pool slices into one
+        # output, replayed from one graph.
+        srcs = torch.empty(L, gb // 4, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty(gb // 4, dtype=torch.bfloat16, device="cuda")
+        copy_dev = graph_replay_us(torch, [lambda l=l: dst.copy_(srcs[l]) for l in range(L)])
+        del srcs, dst
         res[f"c{C}"] = {
             "append_device_us_per_layer": round(append_dev, 2),
             "append_host_launched_us_per_layer": round(append_host, 2),
@@ -356,6 +364,8 @@ def secondary_config3(torch):
             "gather_gbs": round(gb / gather_dev / 1e3, 1),
             "gather_cold_device_us_per_layer": round(gather_cold, 2),
             "gather_cold_gbs": round(gb / gather_cold / 1e3, 1),
+            "copy_device_us_per_layer": round(copy_dev, 2),
+            "copy_gbs": round(gb / copy_dev / 1e3, 1),
             "gather_bytes_per_layer": gb,
         }
         del tables
