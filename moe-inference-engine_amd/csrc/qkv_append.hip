@@ -41,10 +41,7 @@
 namespace {
 
 constexpr int kRowsPerWave = 2;   // QKV and output projections
-#ifndef MIE_HEAD_ROWS_PER_WAVE
-#define MIE_HEAD_ROWS_PER_WAVE 4
-#endif
-constexpr int kHeadRowsPerWave = MIE_HEAD_ROWS_PER_WAVE;  // the LM head: fewer waves re-normalising x
+constexpr int kHeadRowsPerWave = 4;  // the LM head: fewer waves re-normalising x
 constexpr int kWavesPerGroup = 4;
 
 enum Mode { kQkv, kLinear, kHead };
