@@ -117,6 +117,37 @@ def test_append_skips_out_of_range_block_ids():
     assert k_pool.sum().item() == 16 and v_pool.sum().item() == -16
 
 
+def test_gather_leaves_rows_of_out_of_pool_blocks_unwritten():
+    """Table entries of -1 or past the pool are never read: the gather leaves
+    those tokens' output rows as they were, and copies every other token
+    exactly (the oracle's gather over the valid blocks)."""
+    NB, H, BS, D = 6, 3, 4, 8
+    gen = torch.Generator().manual_seed(11)
+    k_pool = torch.randn(2, NB, H, BS, D, generator=gen)
+    v_pool = torch.randn(2, NB, H, BS, D, generator=gen)
+    table = [4, -1, NB, 0, 2]  # blocks 1 and 2 of the sequence are outside the pool
+    length = 4 * BS + 3  # the last block is partial
+    sentinel = 7.0
+    out_k = torch.full((1, H, length, D), sentinel, device="cuda")
+    out_v = torch.full((1, H, length, D), -sentinel, device="cuda")
+    kv_ops.gather(k_pool.cuda(), v_pool.cuda(), 1, torch.tensor(table, dtype=torch.int32, device="cuda"), length,
+                  out_k, out_v)
+    got_k, got_v = out_k[0].cpu(), out_v[0].cpu()
+    for j, blk in enumerate(table):
+        rows = slice(j * BS, min(length, (j + 1) * BS))
+        if 0 <= blk < NB:
+            n = rows.stop - rows.start
+            assert torch.equal(got_k[:, rows], k_pool[1, blk, :, :n])
+            assert torch.equal(got_v[:, rows], v_pool[1, blk, :, :n])
+        else:
+            assert got_k[:, rows].eq(sentinel).all() and got_v[:, rows].eq(-sentinel).all()
+    # Against the oracle wherever the table is valid: substitute a valid id and
+    # compare only the valid blocks' rows.
+    want_k = ref.gather_rows(ref.raw_bits(k_pool), 1, [b if 0 <= b < NB else 0 for b in table], length)
+    valid = np.concatenate([np.full(min(length, (j + 1) * BS) - j * BS, 0 <= b < NB) for j, b in enumerate(table)])
+    assert np.array_equal(ref.raw_bits(got_k)[:, valid], want_k[:, valid])
+
+
 @pytest.mark.parametrize("context", [128, 1024, 8192])
 def test_config3_append_and_gather_round_trip(context):
     """12 layers, 12 x 64, bf16, block 16, random tables
