@@ -8,11 +8,21 @@ whether the step's new token comes through the fused append
 (mie_paged_decode_append: each sequence's last K/V row is taken out of the
 pool and passed as the new rows, so only the kernel's store can put it back).
 Each case checks every sequence against oracle.paged_ref.attention_fp64 on the
-same pool contents: float32 inputs within 1e-5, bfloat16 inputs within 2e-3
-with float32 output or 2e-3 + 2^-8 |ref| with bf16 output (the tolerances of
-the north star and of tests/test_gpu_decode.py); with the fused append the
-pool must also be bit-identical to its state before the rows were taken out.
-The cases print before they run, so a failure names its draw.
+same pool contents: float32 inputs within 1e-5 + 2^-18 |ref|, bfloat16 inputs
+within 2e-3 with float32 output or 2e-3 + 2^-8 |ref| with bf16 output; with the
+fused append the pool must also be bit-identical to its state before the rows
+were taken out.  The cases print before they run, so a failure names its draw.
+
+The float32 bound has a relative term that the fixed-shape tests
+(tests/test_gpu_decode.py, the north star's 1e-5) do not need.  The draws go
+beyond those shapes: up to ~3000 tokens at head_dim 96 or 128 with 1 % of the
+keys scaled by 20, where outputs reach |ref| ~ 5.  There float32 arithmetic
+itself misses float64 by more than 1e-5.  For seed 3701 (head_dim 96, 2829
+tokens, |ref| up to 3.93), PyTorch's own float32 scaled_dot_product_attention
+on the same inputs is 1.29e-5 from float64 on the GPU (math backend) and
+5.8e-6 on the CPU, and this kernel 1.07e-5.  2^-18 |ref| (3.8e-6 per unit of
+|ref|) admits float32-level error at those magnitudes and nothing near a
+dropped term.
 """
 
 import os
@@ -78,7 +88,7 @@ def test_random_decode_matches_oracle(seed):
         assert torch.equal(got[b], torch.zeros_like(got[b]))
     got = got.float().cpu().numpy()
     if c["dtype"] == torch.float32:
-        np.testing.assert_allclose(got, want, rtol=0, atol=1e-5)
+        np.testing.assert_allclose(got, want, rtol=2.0**-18, atol=1e-5)
     elif c["out_f32"]:
         np.testing.assert_allclose(got, want, rtol=0, atol=2e-3)
     else:
