@@ -27,16 +27,17 @@
 // partials could leave int64 - but sets acc[dim] instead, and the consumer
 // then writes NaN.
 //
-// Work decomposition: grid (8 * R * ceil(H / 8)) workgroups of 4 waves.  The
+// Work decomposition: grid (8 * R * ceil(H / 8)) workgroups of W waves (4, or
+// 8 when the launch's context bound exceeds one round of 4: kShortMaxCtx).  The
 // hardware dispatches workgroup i to XCD i mod 8, so workgroup (8 j + x) is
 // head x + 8 (j / R), rows block j % R: the R workgroups of a head share one
 // XCD's L2, and the head's K/V, which each of them reads, comes from HBM once.
-// Inside a workgroup the 4 waves split the context (token t goes to wave
-// (t / TPL) mod 4) and merge their softmax states in LDS; then each wave
+// Inside a workgroup the W waves split the context (token t goes to wave
+// (t / TPL) mod W) and merge their softmax states in LDS; then each wave
 // computes TPL rows per wave load of its share of the row block.  Everything
 // that does not depend on the attention - q, the block table, this
 // workgroup's W_out slice - is read in the first memory round; the K/V tiles
-// in the second (one round per 32 tokens per wave).
+// in the second (one round per kBatch * TPL tokens per wave, 32 at head_dim 64).
 //
 // float32 or bfloat16 (q, the pools and W_out in one dtype; every product and
 // sum in float32, the head's attention output rounded to the dtype before the
@@ -51,14 +52,22 @@
 namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kWaves = 4;
 constexpr int kMaxTable = mie::kAttnOutMaxBlocks;  // block-table entries held in LDS
 constexpr int kBatch = 8;         // wave loads of K (and of V) per memory round
-// Wave loads of W_out rows per wave: 3 gives 48 rows per workgroup at
-// head_dim 64 (R = 16 workgroups per head at dim 768, 192 in all).  Measured
-// on MI355X (config 1, kernel trace): 6 loads (R = 8) 7.0 us per launch, 3
-// with plain K/V loads 5.6 us, 2 with plain loads 5.7 us.
-constexpr int kRowSteps = 3;
+// Rows of W_out per workgroup, in wave loads of TPL rows: 12 of them, 48 rows
+// at head_dim 64 (R = 16 workgroups per head at dim 768, 192 in all).
+// Measured on MI355X (config 1, kernel trace, 4 waves): 24 wave loads (R = 8)
+// 7.0 us per launch, 12 with plain K/V loads 5.6 us, 8 with plain loads 5.7 us.
+constexpr int kRowLoads = 12;
+// Waves per workgroup.  A wave's share of the context is one memory round per
+// kBatch * TPL of its tokens, so a workgroup covers W * kBatch * TPL tokens a
+// round (128 for 4 waves at head_dim 64).  Four waves are fastest for short
+// contexts, eight past one round of four.  Config 1's graphed step on MI355X
+// (ms per token, 4 / 8 / 16 waves): 64 tokens 0.292 / 0.299 / 0.320, 128
+// 0.299 / 0.302 / 0.322, 192 0.316 / 0.307 / 0.325, 256 0.323 / 0.315 / 0.332,
+// 512 0.352 / 0.332 / 0.335, 1024 0.409 / 0.375 / 0.372.
+constexpr int kShortWaves = 4, kLongWaves = 8;
+constexpr int kShortMaxCtx = 128;  // contexts (the launch's bound) the short form takes
 constexpr float kFix = 4294967296.0f;  // 2^32
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -110,11 +119,13 @@ __device__ __forceinline__ void merge_state(float& m, float& l, f32x4_t& o, floa
   m = mm;
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
+template <typename T, int D, int kWaves>
+__global__ __launch_bounds__(64 * kWaves) void attn_out_kernel(AttnOutArgs a) {
   using M = mie::Mem<T>;
   constexpr int LPT = Shape<D>::LPT;
   constexpr int TPL = Shape<D>::TPL;
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int kRowSteps = (kRowLoads + kWaves - 1) / kWaves;  // wave loads of W_out rows per wave
   __shared__ int32_t s_bt[kMaxTable];
   __shared__ float s_ml[kWaves][2];
   __shared__ __align__(16) float s_o[kWaves][D];
@@ -136,13 +147,13 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   // issue order, so the table goes first: the K/V round waits only for it (an
   // L2 hit), while the W_out rows (from HBM) stay in flight until the
   // projection.
-  constexpr int kTablePerThread = kMaxTable / 256;
+  constexpr int kTablePerThread = kMaxTable / kThreads;
   int tb[kTablePerThread];
 #pragma unroll
   for (int u = 0; u < kTablePerThread; ++u) {
-    const int i = u * 256 + static_cast<int>(threadIdx.x);
+    const int i = u * kThreads + static_cast<int>(threadIdx.x);
     const int ic = i < a.bt_len ? i : 0;  // bt_len >= 1
-    tb[u] = u * 256 < a.nblk_max ? a.bt[ic] : 0;
+    tb[u] = u * kThreads < a.nblk_max ? a.bt[ic] : 0;
   }
   int ctx = a.ctx_dev ? *a.ctx_dev : a.ctx;
   const typename M::raw4 qraw = M::load_raw(static_cast<const T*>(a.q) + h * D + c4);
@@ -160,7 +171,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   int bad = 0;
 #pragma unroll
   for (int u = 0; u < kTablePerThread; ++u) {
-    const int i = u * 256 + static_cast<int>(threadIdx.x);
+    const int i = u * kThreads + static_cast<int>(threadIdx.x);
     if (i < nblk) {
       const int blk = i < a.bt_len ? tb[u] : -1;
       s_bt[i] = blk;
@@ -196,8 +207,8 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
     }
     // Every K and V load of the round is issued before the first score: the
     // scheduler would otherwise reuse load registers and start later loads
-    // only after earlier ones returned.  One 4-wave workgroup per CU, so the
-    // registers this holds cost no occupancy.
+    // only after earlier ones returned.  At most one or two workgroups per
+    // CU, so the registers this holds cost no occupancy that is used.
     __builtin_amdgcn_sched_barrier(0);
     float sc[kBatch];
     float mb = m;
@@ -222,7 +233,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
     m = mb;
   }
   // Merge the TPL row groups of the wave (lanes g * LPT + c hold the same
-  // columns for every g), then the four waves through LDS.
+  // columns for every g), then the W waves through LDS.
 #pragma unroll
   for (int off = LPT; off < 64; off <<= 1) {
     const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
@@ -328,24 +339,28 @@ int32_t attn_out_launch(const void* q, const void* k_pool, const void* v_pool, i
   a.acc = static_cast<unsigned long long*>(acc);
   a.fix_limit = 2147483648.0f / static_cast<float>(num_heads);  // H partials of |y| * 2^32 < 2^63 / H
   const int tpl = 64 / (head_dim / 4);
-  a.rows_per_block = kWaves * tpl * kRowSteps;
+  a.rows_per_block = kRowLoads * tpl;
   a.R = (a.dim + a.rows_per_block - 1) / a.rows_per_block;
   const dim3 grid(8 * a.R * ((num_heads + 7) / 8));
   const bool f32 = dtype == MIE_DTYPE_F32;
+  const bool short_ctx = max_ctx <= kShortMaxCtx;
+#define MIE_ATTN_OUT_CASE(DD)                                                             \
+  case DD:                                                                                \
+    if (short_ctx) {                                                                      \
+      if (f32) attn_out_kernel<float, DD, kShortWaves><<<grid, 64 * kShortWaves, 0, stream>>>(a);       \
+      else attn_out_kernel<uint16_t, DD, kShortWaves><<<grid, 64 * kShortWaves, 0, stream>>>(a);        \
+    } else {                                                                              \
+      if (f32) attn_out_kernel<float, DD, kLongWaves><<<grid, 64 * kLongWaves, 0, stream>>>(a);         \
+      else attn_out_kernel<uint16_t, DD, kLongWaves><<<grid, 64 * kLongWaves, 0, stream>>>(a);          \
+    }                                                                                     \
+    break;
   switch (head_dim) {
-    case 32:
-      if (f32) attn_out_kernel<float, 32><<<grid, 256, 0, stream>>>(a);
-      else attn_out_kernel<uint16_t, 32><<<grid, 256, 0, stream>>>(a);
-      break;
-    case 64:
-      if (f32) attn_out_kernel<float, 64><<<grid, 256, 0, stream>>>(a);
-      else attn_out_kernel<uint16_t, 64><<<grid, 256, 0, stream>>>(a);
-      break;
+    MIE_ATTN_OUT_CASE(32)
+    MIE_ATTN_OUT_CASE(64)
     default:
-      if (f32) attn_out_kernel<float, 128><<<grid, 256, 0, stream>>>(a);
-      else attn_out_kernel<uint16_t, 128><<<grid, 256, 0, stream>>>(a);
-      break;
+    MIE_ATTN_OUT_CASE(128)
   }
+#undef MIE_ATTN_OUT_CASE
   return mie::check_launch("attn_out_kernel");
 }
 

@@ -11,9 +11,9 @@ in (the previous step's pick, which the graph writes into a fixed buffer), the
 position of the new token and the context length (advanced by the graph's
 last launch).  The paged cache is put in graph mode (PagedKVCache.graph_pos /
 graph_ctx), so the append and the decode read those device values, and the
-decode launch is planned for the model's capacity (partition_tokens 0 lets
-the library choose; for 12 heads and up to 1024 positions that is one
-workgroup per head).  The host keeps only the block bookkeeping: before each
+launches are planned for a bound on the position (FIRST_CONTEXT_BOUND and
+its doublings, up to the model's capacity; partition_tokens 0 lets the
+library choose the decode's form).  A step past the bound is captured again.  The host keeps only the block bookkeeping: before each
 replay it reserves the block the new token needs (one host-to-device copy of
 one block id every block_size tokens); the replay itself never allocates.
 
@@ -26,6 +26,15 @@ import torch
 
 from moe_engine import paged_attention, projection
 from moe_engine.model import _TENSOR_EPOCH, EOS_TOKEN_ID, PagedKVCache
+
+# A captured step serves positions up to a bound: the smallest of 127, 255,
+# 511, ... (contexts of 128, 256, 512, ... tokens) that holds the position it
+# was captured at, capped by the model's context and the pool.  The launches are
+# planned for that bound (the fused attention takes 4 waves per workgroup up to
+# 128 tokens and 8 beyond), so a step past it is captured again for the next
+# bound, and a sequence starting below it (a later request) is captured again
+# for its own.
+FIRST_CONTEXT_BOUND = 128
 
 
 class GraphedDecoder:
@@ -68,6 +77,8 @@ class GraphedDecoder:
         self._logits = torch.empty(1, vocab, dtype=weight.dtype, device=device)
         self._head_ws = torch.empty(projection.head_workspace_bytes(vocab), dtype=torch.uint8, device=device)
         self.partition_tokens = partition_tokens
+        self.bound = None  # the largest position the captured step serves
+        self.captures = 0
         self.graph = None
         self._graph_out = None
         self._plans = None
@@ -76,15 +87,23 @@ class GraphedDecoder:
         self.next_token = None
         self.replays = 0
 
-    def _graph_mode(self, on):
+    def position_bound(self, position):
+        """The largest position a step captured at `position` serves: the
+        context bound of FIRST_CONTEXT_BOUND doubled until it holds the
+        position, at most the model's context or the pool's capacity."""
+        c = self.cache
+        limit = min(self.model.max_seq_length, c.allocator.num_blocks * c.allocator.block_size) - 1
+        bound = FIRST_CONTEXT_BOUND
+        while bound - 1 < position:
+            bound *= 2
+        return min(bound - 1, limit)
+
+    def _graph_mode(self, on, bound=None):
         c = self.cache
         c.graph_pos = self.pos if on else None
         c.graph_ctx = self.ctx if on else None
         c.graph_partition_tokens = self.partition_tokens if on else 0
-        # The largest position a replay can reach: the model's context or the
-        # pool's capacity, whichever is smaller.
-        capacity = c.allocator.num_blocks * c.allocator.block_size
-        c.graph_max_position = min(self.model.max_seq_length, capacity) - 1 if on else None
+        c.graph_max_position = bound if on else None
 
     def _forward_body(self):
         """The captured step: embeddings and blocks (Model._hidden_states),
@@ -114,12 +133,18 @@ class GraphedDecoder:
         if cache.position >= self.model.max_seq_length:
             raise RuntimeError("KV cache is full")
         cache._reserve(cache.position + 1)
-        if self.graph is not None and self._epoch != _TENSOR_EPOCH[0]:
+        if self.graph is not None and (self._epoch != _TENSOR_EPOCH[0]
+                                       or self.position_bound(cache.position) != self.bound):
             # A tensor the captured step reads was replaced (a conversion, an
-            # assigning load, a parameter swapped with drop_decode_plan):
-            # run eagerly and capture again.
+            # assigning load, a parameter swapped with drop_decode_plan), or
+            # the position left the captured step's bound: run eagerly and
+            # capture again.
             self.graph = self._graph_out = self._plans = None
-        self._graph_mode(True)
+        if self.graph is None:
+            # This step runs eagerly at the current position and the capture
+            # serves the steps from the next one on.
+            self.bound = self.position_bound(cache.position + 1)
+        self._graph_mode(True, self.bound)
         try:
             if self.graph is None:
                 # The first step runs eagerly on the stream the capture will use
@@ -145,6 +170,7 @@ class GraphedDecoder:
                     # of the block) replaces, so the decoder holds them.
                     self._plans = [block._one_token for block in self.model.MoEBlocks]
                     self._epoch = _TENSOR_EPOCH[0]
+                    self.captures += 1
             else:
                 self.graph.replay()
                 cache.position += 1

@@ -74,6 +74,7 @@ CASES = [
     # (heads, head_dim, block_size, context lengths)
     (12, 64, 16, [1, 2, 33, 96, 97]),  # config 1's shape and contexts
     (12, 64, 16, [1024, 2048]),
+    (12, 64, 16, [128, 129]),  # either side of the switch from 4 to 8 waves per workgroup
     (12, 64, 1, [1, 40]),
     (12, 64, 5, [7, 130]),  # a block size that is not a power of two
     (12, 64, 64, [63, 64, 65, 700]),

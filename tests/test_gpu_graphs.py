@@ -39,26 +39,32 @@ def tiny_model(dtype=torch.float32, max_seq_length=None, **over):
 
 # (hidden_dim, num_heads): head_dim 32 has the four-launch block (attention
 # fused with out_proj) up to 1024 positions; TINY's head_dim 4 only the
-# five-launch one.
-@pytest.mark.parametrize("block_size,max_seq_length,num_blocks,hidden_dim,num_heads,launches", [
-    (4, 128, 80, 64, 2, 4),
-    (16, 128, 80, 64, 2, 4),
-    (16, 128, 80, 32, 8, 5),
-    (16, 2200, 140, 64, 2, 6),  # the two-head decode splits 2200 positions: partitions + merge
+# five-launch one.  A captured step serves positions up to a bound (127, 255,
+# ... capped by the capacity); `captures` counts the captures a run needs.
+@pytest.mark.parametrize("block_size,max_seq_length,num_blocks,hidden_dim,num_heads,prompt_len,steps,captures,launches", [
+    (4, 128, 80, 64, 2, 9, 100, 1, 4),
+    (16, 128, 80, 64, 2, 9, 100, 1, 4),
+    (16, 128, 80, 32, 8, 9, 100, 1, 5),
+    # past 128 positions the fused attention takes 8 waves per workgroup: the
+    # step is captured again at position 128 for the bound 255
+    (16, 2200, 140, 64, 2, 110, 40, 2, 4),
+    # the bound 2047: the two-head decode splits its context (partitions + merge)
+    (16, 2200, 160, 64, 2, 1100, 30, 1, 6),  # 160 blocks: both caches hold 1130 tokens
 ])
-def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks, hidden_dim, num_heads, launches):
-    print_case("graph replay vs eager", block_size, max_seq_length, num_blocks, hidden_dim, num_heads)
+def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks, hidden_dim, num_heads, prompt_len,
+                                         steps, captures, launches):
+    print_case("graph replay vs eager", block_size, max_seq_length, num_blocks, hidden_dim, num_heads, prompt_len)
     model = tiny_model(max_seq_length=max_seq_length, hidden_dim=hidden_dim, num_heads=num_heads)
     allocator = model.new_block_allocator(num_blocks=num_blocks, block_size=block_size, attention_mode="direct")
     graphed, eager = allocator.new_cache(), allocator.new_cache()
-    prompt = torch.randint(0, TINY["vocab_size"], (1, 9), device="cuda")
+    prompt = torch.randint(0, TINY["vocab_size"], (1, prompt_len), device="cuda")
     with torch.no_grad():
         first = model(prompt, graphed)[:, -1]
         torch.testing.assert_close(model(prompt, eager)[:, -1], first)
         decoder = GraphedDecoder(model, graphed)
         token = first.argmax(-1, keepdim=True)
         decoder.prime(token)
-        for step in range(100):
+        for step in range(steps):
             got = decoder.step()
             got_logits = decoder.logits.clone()
             # Eager work between replays: the same step on the other sequence,
@@ -70,9 +76,10 @@ def test_every_replay_matches_eager_step(block_size, max_seq_length, num_blocks,
             token = want_logits.argmax(-1, keepdim=True)
             assert torch.equal(got, token), f"step {step}"
             assert graphed.position == eager.position
-    assert decoder.replays == 99
+    assert decoder.captures == captures and decoder.replays == steps - captures
     # The form the captured blocks took, for the capture's position bound.
-    bound = min(max_seq_length, num_blocks * block_size) - 1
+    bound = decoder.position_bound(graphed.position)
+    assert decoder.bound == bound
     lib = _native.lib()
     for plan in decoder._plans:
         assert plan is not None and plan[2] is not None
