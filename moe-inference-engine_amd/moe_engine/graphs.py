@@ -13,9 +13,10 @@ last launch).  The paged cache is put in graph mode (PagedKVCache.graph_pos /
 graph_ctx), so the append and the decode read those device values, and the
 launches are planned for a bound on the position (FIRST_CONTEXT_BOUND and
 its doublings, up to the model's capacity; partition_tokens 0 lets the
-library choose the decode's form).  A step past the bound is captured again.  The host keeps only the block bookkeeping: before each
-replay it reserves the block the new token needs (one host-to-device copy of
-one block id every block_size tokens); the replay itself never allocates.
+library choose the decode's form).  A step past the bound is captured
+again.  The host keeps only the block bookkeeping: before each replay it
+reserves the block the new token needs (one block id appended to the device
+table every block_size tokens); the replay itself never allocates.
 
 Only greedy decoding (temperature 0) over a PagedKVCache whose attention can
 run the direct kernel, with the fused MoE (float32 or bfloat16), is captured; everything
