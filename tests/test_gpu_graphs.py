@@ -19,7 +19,7 @@ import torch
 
 from conftest import print_case
 from moe_engine import _native
-from moe_engine.graphs import GraphedDecoder, generate_graphed
+from moe_engine.graphs import GraphedDecoder, GraphedGenerator, generate_graphed
 from moe_engine.model import Model, ModelConfig
 
 pytestmark = pytest.mark.gpu
@@ -165,6 +165,29 @@ def test_replaced_weights_are_captured_again():
         assert captures == 3 and decoder.replays == 6
     graphed.free()
     eager.free()
+
+
+def test_generator_captures_again_when_a_request_changes_the_position_bound():
+    """GraphedGenerator keeps one captured step across requests while their
+    positions stay inside its bound (127, 255, ...).  A longer request is
+    captured again for the larger bound, a short one after it for the smaller
+    one again; every request's tokens equal Model.generate's."""
+    print_case("graph generator bounds")
+    model = tiny_model(max_seq_length=512, hidden_dim=64, num_heads=2)
+    allocator = model.new_block_allocator(num_blocks=40, block_size=16, attention_mode="direct")
+    gen = GraphedGenerator(model, allocator.new_cache())
+    g = torch.Generator().manual_seed(4)
+    requests = [(5, 12, 1), (9, 20, 1), (200, 12, 2), (7, 10, 3)]  # prompt length, new tokens, captures after
+    for prompt_len, new, captures in requests:
+        prompt = torch.randint(0, TINY["vocab_size"], (1, prompt_len), generator=g).cuda()
+        cache = allocator.new_cache()
+        want = model.generate(prompt, max_new_tokens=new, temperature=0, cache=cache)
+        cache.free()
+        got = gen.generate(prompt, new)
+        assert torch.equal(got, want), (prompt_len, new)
+        assert gen.decoder.captures == captures, (prompt_len, gen.decoder.captures)
+    assert gen.decoder.bound == 127
+    assert len(allocator.free_blocks) == allocator.num_blocks
 
 
 def test_generate_graphed_matches_generate():
