@@ -11,6 +11,8 @@ different summation orders: rtol / atol 1e-4, the reference's float32 bound
 for paged against contiguous attention (tests/test_paged_attention.py:148).
 Some cases start past 1024 cached tokens, where the plan takes the
 five-launch block (and, with few heads, a split context and a workspace).
+Others start just below 128, so the fused attention's launch switches from
+4 to 8 waves per workgroup during the decode (and a graph is captured again).
 The greedy tokens of a graphed decode must equal Model.generate's.
 """
 
@@ -33,7 +35,7 @@ def draw(seed):
     head_dim = rng.choice([32, 64, 96, 128])
     heads = rng.choice([1, 2, 3, 4, 6])
     long = rng.random() < 0.3
-    return dict(
+    c = dict(
         hidden_dim=head_dim * heads,
         num_heads=heads,
         num_layers=rng.choice([1, 2, 3]),
@@ -46,6 +48,13 @@ def draw(seed):
         decode=rng.randint(3, 8),
         top_k_draw=rng.random(),
     )
+    # A separate stream, so adding this draw left the other draws of each seed
+    # unchanged: a quarter of the short cases cross 128 positions.
+    rng2 = random.Random(seed + 200_000)
+    if not long and rng2.random() < 0.25:
+        c["prompt"] = rng2.randint(118, 127)
+        c["decode"] = rng2.randint(8, 16)
+    return c
 
 
 # MIE_PLAN_RANDOM_CASES widens the sweep for a one-off run.
@@ -91,8 +100,9 @@ def test_plans_match_the_per_call_path(seed):
     assert (launches == 4) == (fused_shape and ids.shape[1] <= 1024)
     want = run(False)
     torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
-    # The same model decoding greedily from a HIP graph.
-    if c["prompt"] <= 60:
+    # The same model decoding greedily from a HIP graph (across a re-capture
+    # at 128 positions for the prompts that start just below it).
+    if c["prompt"] <= 127:
         prompt = ids[0, : c["prompt"]]
         cache = alloc.new_cache()
         eager = model.generate(prompt, max_new_tokens=c["decode"], temperature=0, cache=cache)
