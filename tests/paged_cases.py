@@ -29,6 +29,17 @@ def oracle_outputs(w: Workload, batches=None):
     return np.stack(out)
 
 
+def oracle_scales(w: Workload, batches=None):
+    """The scale of each output element, sum_t p_t |v_t| (the attention of
+    |v| in float64): what float32 rounding of the weighted sum is relative to.
+    It bounds |output| and does not shrink when the sum cancels."""
+    out = []
+    for b in range(len(w.lens)) if batches is None else batches:
+        k, v = sequence_kv(w, b)
+        out.append(ref.attention_fp64(ref.to_f64(w.q[b]), ref.to_f64(k), np.abs(ref.to_f64(v))))
+    return np.stack(out)
+
+
 def bf16_close(got, want, atol=2e-3):
     """bf16 outputs: |got - want| <= atol + 2^-8 |want| (one bf16 rounding of a
     value near |want| may add up to 2^-9 |want|; twice that is allowed)."""

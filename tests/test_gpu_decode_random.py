@@ -8,7 +8,8 @@ whether the step's new token comes through the fused append
 (mie_paged_decode_append: each sequence's last K/V row is taken out of the
 pool and passed as the new rows, so only the kernel's store can put it back).
 Each case checks every sequence against oracle.paged_ref.attention_fp64 on the
-same pool contents: float32 inputs within 1e-5 + 2^-18 |ref|, bfloat16 inputs
+same pool contents: float32 inputs within 1e-5 + 2^-18 scale (scale = the
+float64 attention of |v|, sum_t p_t |v_t|, which bounds |ref|), bfloat16 inputs
 within 2e-3 with float32 output or 2e-3 + 2^-8 |ref| with bf16 output; with the
 fused append the pool must also be bit-identical to its state before the rows
 were taken out.  The cases print before they run, so a failure names its draw.
@@ -20,9 +21,12 @@ keys scaled by 20, where outputs reach |ref| ~ 5.  There float32 arithmetic
 itself misses float64 by more than 1e-5.  For seed 3701 (head_dim 96, 2829
 tokens, |ref| up to 3.93), PyTorch's own float32 scaled_dot_product_attention
 on the same inputs is 1.29e-5 from float64 on the GPU (math backend) and
-5.8e-6 on the CPU, and this kernel 1.07e-5.  2^-18 |ref| (3.8e-6 per unit of
-|ref|) admits float32-level error at those magnitudes and nothing near a
-dropped term.
+5.8e-6 on the CPU, and this kernel 1.07e-5.  For seed 19080 (head_dim 64,
+block 8, 36 sequences up to 2935 tokens, split into 128-token partitions)
+the CPU's float32 SDPA is 1.01e-5 from float64 and this kernel 1.18e-5, at an
+output of 0.42 whose terms cancel.  The relative term therefore scales with
+sum_t p_t |v_t|, the size of the terms rounded, not with |ref|: 2^-18 of it
+(3.8e-6 per unit) admits float32-level error and nothing near a dropped term.
 """
 
 import os
@@ -35,7 +39,7 @@ import torch
 from conftest import print_case
 from moe_engine import _native, paged_attention
 from oracle import paged_ref as ref
-from paged_cases import bf16_close, make_workload, oracle_outputs, take_last_tokens
+from paged_cases import bf16_close, make_workload, oracle_outputs, oracle_scales, take_last_tokens
 
 pytestmark = pytest.mark.gpu
 
@@ -88,7 +92,9 @@ def test_random_decode_matches_oracle(seed):
         assert torch.equal(got[b], torch.zeros_like(got[b]))
     got = got.float().cpu().numpy()
     if c["dtype"] == torch.float32:
-        np.testing.assert_allclose(got, want, rtol=2.0**-18, atol=1e-5)
+        bound = 1e-5 + 2.0**-18 * oracle_scales(w)
+        err = np.abs(got - want)
+        assert (err <= bound).all(), f"max error {err.max():.3e} (bound there {bound.flat[err.argmax()]:.3e})"
     elif c["out_f32"]:
         np.testing.assert_allclose(got, want, rtol=0, atol=2e-3)
     else:
