@@ -16,8 +16,8 @@ were taken out.  The cases print before they run, so a failure names its draw.
 
 The float32 bound has a relative term that the fixed-shape tests
 (tests/test_gpu_decode.py, the north star's 1e-5) do not need.  The draws go
-beyond those shapes: up to ~3000 tokens at head_dim 96 or 128 with 1 % of the
-keys scaled by 20, where outputs reach |ref| ~ 5.  There float32 arithmetic
+beyond those shapes: up to ~3000 tokens per sequence with 1 % of the keys
+scaled by 20, where outputs reach |ref| ~ 5.  There float32 arithmetic
 itself misses float64 by more than 1e-5.  For seed 3701 (head_dim 96, 2829
 tokens, |ref| up to 3.93), PyTorch's own float32 scaled_dot_product_attention
 on the same inputs is 1.29e-5 from float64 on the GPU (math backend) and
