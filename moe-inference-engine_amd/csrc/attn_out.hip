@@ -178,8 +178,18 @@ __global__ __launch_bounds__(64 * kWaves) void attn_out_kernel(AttnOutArgs a) {
       bad |= blk < 0 || blk >= a.num_blocks;
     }
   }
-  // A context block outside the pool (never read) makes the head's attention NaN.
-  const bool any_bad = __syncthreads_or(bad) != 0;
+  // A context block outside the pool (never read) makes the head's attention
+  // NaN.  Each wave posts its own flag (a ballot, no initialisation needed)
+  // and the barrier publishes them with the table: __syncthreads_or would read
+  // the workgroup size from the launch's hidden arguments, 256 more bytes of
+  // kernel arguments per launch.
+  __shared__ int s_badw[kWaves];
+  const unsigned long long wave_bad = __ballot(bad);
+  if (lane == 0) s_badw[wave] = wave_bad != 0;
+  __syncthreads();
+  bool any_bad = false;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) any_bad |= s_badw[w] != 0;
 
   // Later memory rounds: this wave's tokens t = (step * 4 + wave) * TPL + g, kBatch wave
   // loads of K and V per round; online softmax per TPL-row group.

@@ -9,6 +9,11 @@
 
 namespace {
 
+// Threads per workgroup of both kernels, a constant rather than blockDim: reading
+// blockDim makes the kernel take the launch's hidden arguments, 256 more bytes of
+// kernel arguments per launch.
+constexpr int kCopyThreads = 256;
+
 template <int VB> struct Raw;
 template <> struct Raw<16> { using T = uint4; };
 template <> struct Raw<8> { using T = uint2; };
@@ -38,12 +43,12 @@ struct AppendArgs {
   mie::FastDiv bs;      // block_size
 };
 
-// grid = (ceil(2 * vecs_per_kv / blockDim), seq_len, batch): one token row set
+// grid = (ceil(2 * vecs_per_kv / kCopyThreads), seq_len, batch): one token row set
 // (all heads of K and V) per (y, z).
 template <int VB>
-__global__ __launch_bounds__(256) void kv_append_kernel(AppendArgs a) {
+__global__ __launch_bounds__(kCopyThreads) void kv_append_kernel(AppendArgs a) {
   using T = typename Raw<VB>::T;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  const int i = blockIdx.x * kCopyThreads + threadIdx.x;
   if (i >= 2 * a.vecs_per_kv) return;
   const int s = blockIdx.y;
   const int b = blockIdx.z;
@@ -84,11 +89,11 @@ struct GatherArgs {
   mie::FastDiv bs;
 };
 
-// grid = (ceil(length * vecs_per_row / blockDim), num_heads, 2 [K, V]).
+// grid = (ceil(length * vecs_per_row / kCopyThreads), num_heads, 2 [K, V]).
 template <int VB>
-__global__ __launch_bounds__(256) void kv_gather_kernel(GatherArgs a) {
+__global__ __launch_bounds__(kCopyThreads) void kv_gather_kernel(GatherArgs a) {
   using T = typename Raw<VB>::T;
-  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  const uint32_t i = blockIdx.x * kCopyThreads + threadIdx.x;
   const uint32_t t = a.vecs_per_row.div(i);
   if (t >= static_cast<uint32_t>(a.length)) return;
   const uint32_t vec = i - t * a.vecs_per_row.d;
@@ -175,7 +180,7 @@ int32_t mie::kv_append_impl(void* k_pool, void* v_pool, int64_t pool_stride_bloc
   a.vecs_per_row = a.row_bytes / vb;
   a.vecs_per_kv = num_heads * a.vecs_per_row;
 
-  const int threads = 256;
+  const int threads = kCopyThreads;
   dim3 grid((2 * a.vecs_per_kv + threads - 1) / threads, seq_len, batch);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (vb) {
@@ -248,7 +253,7 @@ extern "C" int32_t mie_kv_gather(const void* k_pool, const void* v_pool, int64_t
   if (total >= (int64_t{1} << 31))
     return mie::fail(MIE_ERR_INVALID, "mie_kv_gather: length * row vectors exceeds 2^31");
 
-  const int threads = 256;
+  const int threads = kCopyThreads;
   dim3 grid(static_cast<uint32_t>((total + threads - 1) / threads), num_heads, 2);
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (vb) {
