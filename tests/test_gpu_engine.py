@@ -467,7 +467,10 @@ def test_decode_step_runs_every_block_in_one_call():
             for t in range(6, 30):
                 for s in range(2):
                     steps[s].append(model(ids[s : s + 1, t : t + 1], caches[s])[:, -1])
+        # The one-call steps took a new block every 4 tokens and wrote its id
+        # into the device table from layer 0's QKV launch: the mirror matches.
         for c in caches:
+            assert c.block_table_device[: len(c.block_table)].tolist() == c.block_table
             c.free()
         assert calls.done == 2 * (30 - 6 - 1)
         for s in range(2):
